@@ -1,0 +1,175 @@
+"""Batch-1 greedy decode throughput of the hip device on the Qwen3-0.6B shape.
+
+Workload: Qwen3-0.6B architecture (28 layers, hidden 1024, 16 Q / 8 KV heads,
+head_dim 128, MLP 3072, vocab 151936, tied embeddings, q/k-norm, RoPE theta
+1e6) with seeded synthetic N(0, 0.02) bf16 weights and RMSNorm gains of 1; a
+16-token uniform-random prompt, then greedy decode. A step is one decode token
+(one forward pass of one token through the whole model, on the device, plus the
+greedy pick). The timed region holds exactly `--steps` decode steps from
+position 16, after `--warmup` untimed steps; weights, caches and the prompt's
+keys and values are resident in HBM before it starts.
+
+Prints one JSON line (the benchmark contract) with the roofline of the decode
+step and the CPU oracle's throughput on the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+
+def kv_bytes_per_token(c, ctx_from: int, steps: int, kv_elem: int) -> float:
+    """Average KV-cache bytes a decode step reads (every cached position, both
+    caches, every layer) and writes (its own position)."""
+    kvd = c.num_key_value_heads * c.head_dim()
+    avg_ctx = sum(ctx_from + i + 1 for i in range(steps)) / steps
+    read = c.num_hidden_layers * 2 * avg_ctx * kvd * kv_elem
+    write = c.num_hidden_layers * 2 * kvd * kv_elem
+    return read + write
+
+
+def cpu_baseline(cfg, weights, prompt, steps: int, repeats: int) -> dict:
+    """The CPU oracle (C restatement of the reference's Cpu device and forward
+    pass) on the same weights and prompt: greedy decode tokens/s from position
+    len(prompt), median of `repeats` runs."""
+    from oracle import ref
+
+    cores = min(os.cpu_count() or 1, 16)
+    ref.set_threads(cores)
+    model = ref.RefModel(cfg, weights)
+    rates, tokens = [], []
+    for _ in range(repeats):
+        st = model.state(len(prompt) + steps)
+        logits = model.forward(st, prompt, 0)
+        toks = []
+        t0 = time.perf_counter()
+        for i in range(steps):
+            tok = ref.argmax(logits)
+            toks.append(tok)
+            logits = model.forward(st, [tok], len(prompt) + i)
+        rates.append(steps / (time.perf_counter() - t0))
+        tokens = toks
+    rates.sort()
+    return {
+        "value": rates[len(rates) // 2],
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{steps} greedy decode steps after the {len(prompt)}-token prompt, median of {repeats} runs",
+        "tokens": tokens,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32, help="timed decode steps")
+    ap.add_argument("--warmup", type=int, default=32, help="untimed decode steps before the timed ones")
+    ap.add_argument("--prompt", type=int, default=16)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--kv", choices=["f32", "bf16"], default="f32")
+    ap.add_argument("--model", choices=["qwen3-0.6b", "qwen3-4b"], default="qwen3-0.6b")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--cpu-repeats", type=int, default=3)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the decode path runs on a single MI355X and --gpus {args.gpus} "
+              "is not supported (no multi-GPU sharding is built).", file=sys.stderr)
+        return 2
+
+    from titania_amd import QWEN3_0_6B, QWEN3_4B, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, Hip, synth
+    from titania_amd.model import Model, State
+
+    cfg = QWEN3_0_6B if args.model == "qwen3-0.6b" else QWEN3_4B
+    kv = TH_KV_F32 if args.kv == "f32" else TH_KV_BF16
+    kv_elem = 4 if kv == TH_KV_F32 else 2
+
+    t = time.perf_counter()
+    weights = synth.weights(cfg, seed=args.seed)
+    prompt = synth.prompt(args.prompt, cfg.vocab_size, seed=args.seed)
+    gen_s = time.perf_counter() - t
+
+    dev = Hip(0)
+    model = Model(dev, cfg, weights)
+    K, W = args.steps, args.warmup
+    state = State(model, args.prompt + max(K, W, 1), kv)
+
+    # Warmup: prefill, W decode steps (captures the decode graph).
+    model.forward(state, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    if W:
+        model.decode(state, args.prompt, W)
+    # Timed: the prompt is re-run first (rewriting positions 0..15), then exactly K steps.
+    model.forward(state, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    dev.synchronize()
+    dev.timer_begin()
+    t0 = time.perf_counter()
+    tokens = model.decode(state, args.prompt, K)
+    wall = time.perf_counter() - t0
+    gpu_ms = dev.timer_end()
+    ms_per_step = wall * 1000.0 / K
+
+    weight_bytes = cfg.weight_bytes_per_token()
+    kvb = kv_bytes_per_token(cfg, args.prompt, K, kv_elem)
+    logits_bytes = 4 * cfg.vocab_size
+    bytes_per_token = weight_bytes + kvb + logits_bytes
+    achieved = bytes_per_token / (gpu_ms / 1000.0 / K) / 1e9
+
+    out = {
+        "metric": "batch-1 decode tokens/s (Qwen3-0.6B shape) + % of HBM GB/s roofline",
+        "value": K / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) bf16 weights, gains 1, uniform-random prompt)",
+        "config": {
+            "workload": f"{args.model} greedy decode, {args.prompt}-token prompt, {K} steps, batch 1, "
+                        f"{args.kv} KV cache",
+            "model": args.model,
+            "global_batch": 1,
+            "seq_len": args.prompt + K,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode step (HIP graph of one token's kernels)",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "bytes_per_step": bytes_per_token,
+            "gpu_ms_per_step": gpu_ms / K,
+        },
+        "synth_s": gen_s,
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(cfg, weights, prompt, K, args.cpu_repeats)
+        out["parity_tokens_match"] = [int(x) for x in tokens] == cb.pop("tokens")
+        out["cpu_baseline"] = cb
+    print(json.dumps(out))
+    state.close()
+    model.close()
+    dev.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

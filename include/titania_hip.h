@@ -1,0 +1,168 @@
+/*
+ * titania_hip.h: the C ABI of the `hip` device, a gfx950 (MI355X) backend for
+ * Titania's Qwen3 forward pass.
+ *
+ * The boundary replaced is the Rust trait `Device` (model/device.rs:9-89): one
+ * entry point per trait method, with opaque handles for the associated types
+ * `Buffer` (f32 activations) and `Weight` (bf16 tensor). Each declaration cites
+ * the trait method it stands for. Where the trait panics on misuse (the length
+ * asserts of model/cpu.rs:22,40,52-53 and model/titania.rs:125,140,147,156-157,188)
+ * these functions return TH_ERR_INVALID before touching the GPU, and
+ * th_last_error() says why.
+ *
+ * Beyond the trait, the device offers fused operations whose results equal the
+ * composition of the primitives in the order model/model.rs:93-149 calls them,
+ * and the forward pass itself (model/model.rs:83-149) with a device-resident
+ * greedy decode loop.
+ *
+ * Threading: a device and its handles belong to one host thread at a time
+ * (the reference builds and uses its model on one worker thread,
+ * cli/run.rs:49,121-127). All work runs in order on one HIP stream per device.
+ */
+#ifndef TITANIA_HIP_H
+#define TITANIA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define TH_API __attribute__((visibility("default")))
+#else
+#define TH_API
+#endif
+
+/* Status codes. */
+#define TH_OK 0
+#define TH_ERR_INVALID 1 /* misuse: a length, shape, offset or position out of range */
+#define TH_ERR_HIP 2     /* a HIP runtime call failed */
+#define TH_ERR_NOMEM 3   /* device or host allocation failed */
+
+typedef struct th_device th_device; /* a GPU, its stream and its scratch memory */
+typedef struct th_buffer th_buffer; /* model/device.rs:10-13 `Device::Buffer` */
+typedef struct th_weight th_weight; /* model/device.rs:14-15 `Device::Weight` */
+
+/* Message describing the last failure on the calling thread ("" if none). */
+TH_API const char *th_last_error(void);
+
+/* Opens GPU `ordinal` (stands in for `Cpu` / `Titania::new`, cli/run.rs:121-128). */
+TH_API int th_device_create(int ordinal, th_device **out);
+TH_API void th_device_destroy(th_device *dev);
+/* Waits for all work queued on the device. */
+TH_API int th_device_synchronize(th_device *dev);
+
+/* model/device.rs:17-18 `upload`: copies a row-major bf16 tensor (raw bits,
+ * model/weights.rs:13-17) of `ndim` (1 or 2) dimensions into device memory. */
+TH_API int th_upload(th_device *dev, const uint16_t *data, const size_t *shape, size_t ndim, th_weight **out);
+TH_API void th_weight_free(th_device *dev, th_weight *w);
+/* Shape of a weight: writes ndim and up to 2 extents. */
+TH_API int th_weight_shape(const th_weight *w, size_t *shape, size_t *ndim);
+
+/* model/device.rs:20-21 `alloc`: a zeroed buffer of `len` f32 activations. */
+TH_API int th_alloc(th_device *dev, size_t len, th_buffer **out);
+TH_API void th_buffer_free(th_device *dev, th_buffer *buf);
+/* model/device.rs:23-26 `resize`: len <= the allocated length; contents gained are undefined. */
+TH_API int th_resize(th_device *dev, th_buffer *buf, size_t len);
+TH_API size_t th_buffer_len(const th_buffer *buf);
+/* model/device.rs:28-29 `read`: copies the buffer's `len` activations out (blocking). */
+TH_API int th_read(th_device *dev, const th_buffer *buf, float *out, size_t len);
+/* model/device.rs:31-32 `write`: `len` must equal the buffer's length. */
+TH_API int th_write(th_device *dev, th_buffer *buf, const float *data, size_t len);
+/* model/device.rs:34-42 `copy`: dst[dst_offset..][..len] = src[src_offset..][..len]. */
+TH_API int th_copy(th_device *dev, th_buffer *dst, size_t dst_offset, const th_buffer *src, size_t src_offset,
+            size_t len);
+
+/* model/device.rs:44-46 `embed`: out[t] = table[tokens[t]]; out.len == n * table.shape[1]. */
+TH_API int th_embed(th_device *dev, th_buffer *out, const th_weight *table, const uint32_t *tokens, size_t n);
+/* model/device.rs:48-51 `matmul`: out[t] = w . x[t] for w [rows, cols]; n = x.len / cols. */
+TH_API int th_matmul(th_device *dev, th_buffer *out, const th_weight *w, const th_buffer *x);
+/* model/device.rs:53-54 `add`: x += y. */
+TH_API int th_add(th_device *dev, th_buffer *x, const th_buffer *y);
+/* model/device.rs:56-58 `rmsnorm`: each weight.len-long row of x. */
+TH_API int th_rmsnorm(th_device *dev, th_buffer *x, const th_weight *weight, float eps);
+/* model/device.rs:60-66 `rope`: table[(p * head_dim/2 + i) * 2..][..2] = (cos, sin). */
+TH_API int th_rope(th_device *dev, th_buffer *x, const th_buffer *table, size_t pos, size_t n_heads, size_t head_dim);
+/* model/device.rs:68-85 `attention`: caches laid out [position][n_kv_heads][head_dim]. */
+TH_API int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
+                 const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads);
+/* model/device.rs:87-88 `silu_mul`: gate = silu(gate) * up. */
+TH_API int th_silu_mul(th_device *dev, th_buffer *gate, const th_buffer *up);
+
+/* Device-side timing: th_timer_begin records an event on the device's stream,
+ * th_timer_end records another, waits for it and gives the milliseconds between
+ * the two (the GPU time of the work queued in between). */
+TH_API int th_timer_begin(th_device *dev);
+TH_API int th_timer_end(th_device *dev, float *ms);
+
+/* ---- fused extensions (each equals its composition of trait methods) ---- */
+
+/* x += y, then xb = rmsnorm(x) with `weight` (the add, copy and rmsnorm of
+ * model/model.rs:132-136). y may be NULL for copy + rmsnorm alone (model.rs:106-107). */
+TH_API int th_add_rmsnorm(th_device *dev, th_buffer *x, const th_buffer *y, th_buffer *xb, const th_weight *weight,
+                   float eps);
+/* Greedy choice (model/sampler.rs:21-33 at temperature 0): index of the largest
+ * of the buffer's values under IEEE total order, lowest index on ties. */
+TH_API int th_argmax(th_device *dev, const th_buffer *logits, uint32_t *token);
+
+/* ---- the forward pass (model/model.rs) ---- */
+
+/* Architecture (model/config.rs:9-36, head_dim resolved as config.rs:32-35 does). */
+typedef struct th_config {
+    int64_t hidden_size;
+    int64_t intermediate_size;
+    int64_t num_hidden_layers;
+    int64_t num_attention_heads;
+    int64_t num_key_value_heads;
+    int64_t head_dim;
+    int64_t vocab_size;
+    float rms_norm_eps;
+    float rope_theta;
+    int64_t tie_word_embeddings;
+} th_config;
+
+typedef struct th_model th_model; /* model/model.rs:10-19 `Model` */
+typedef struct th_state th_state; /* model/model.rs:152-172 `State` */
+
+/* Builds a model from uploaded weights (model/model.rs:40-77). `weights` holds
+ * 11 handles per layer in the order model.rs:50-60 loads them (input_layernorm,
+ * q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, post_attention_layernorm,
+ * gate_proj, up_proj, down_proj; q_norm and k_norm may be NULL), then
+ * embed_tokens, norm, and lm_head (NULL when tie_word_embeddings). The model
+ * borrows the handles: free them only after th_model_destroy. */
+TH_API int th_model_create(th_device *dev, const th_config *config, const th_weight *const *weights, size_t n_weights,
+                    th_model **out);
+TH_API void th_model_destroy(th_model *model);
+
+#define TH_KV_F32 0  /* f32 caches, as the reference stores them (model/model.rs:206-207) */
+#define TH_KV_BF16 1 /* bf16 caches: half the bytes per position */
+
+/* model/model.rs:176-211 `State::new` for sequences of up to max_len tokens.
+ * The caches are laid out per layer and per KV head: [layer][kv_head][max_len][head_dim]. */
+TH_API int th_state_create(th_model *model, size_t max_len, int kv_dtype, th_state **out);
+TH_API void th_state_destroy(th_state *state);
+
+#define TH_PATH_OPS 0   /* one trait primitive per step, exactly as model.rs:103-148 calls them */
+#define TH_PATH_FUSED 1 /* fused kernels, same results within rounding */
+
+/* model/model.rs:83-91 `Model::forward`: runs n tokens, the first at position
+ * pos, adds their keys and values to the caches and writes the logits of the
+ * token after the last into `logits` (vocab_size floats; NULL to skip the copy). */
+TH_API int th_forward(th_model *model, th_state *state, const uint32_t *tokens, size_t n, size_t pos, float *logits,
+               int path);
+
+/* Greedy decode as model/chat.rs:149-178 drives it at temperature 0, kept on
+ * the device: `steps` times, pick the argmax of the current logits and feed it
+ * at position pos, pos + 1, ... The first pick is from the logits the last
+ * th_forward left. Writes the picked tokens to out_tokens and, if out_logits is
+ * not NULL, the logits after each fed token (steps * vocab_size floats). One
+ * step is one HIP graph replay; the host waits once, at the end. */
+TH_API int th_decode(th_model *model, th_state *state, size_t pos, size_t steps, uint32_t *out_tokens, float *out_logits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TITANIA_HIP_H */

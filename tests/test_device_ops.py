@@ -1,0 +1,283 @@
+"""Per-operation parity of the hip device against the CPU oracle.
+
+The first group restates the reference's own differential tests
+(model/titania.rs:268-370): same shapes, same closed-form xorshift inputs, same
+tolerance |a - e| <= 1e-5 + 1e-4 |e|. The second runs the Qwen3-0.6B decode
+shapes (bf16 weights, f32 activations N(0, 1), seeded) and the GQA decode
+attention at contexts 512, 4096 and 32768, against the north-star bar of
+relative error <= 1e-3 (and tighter elementwise bounds where fp32 rounding
+allows).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import ref
+from titania_amd import InvalidArgument, Tensor
+from titania_amd.synth import bf16_to_f32, f32_to_bf16, normal_bf16
+from util import assert_close, numbers, rel_error, tensor
+
+pytestmark = pytest.mark.gpu
+
+
+def buffers(hip, n, seed):
+    """A buffer on the device and its host copy, holding numbers(n, seed)."""
+    values = numbers(n, seed)
+    buf = hip.alloc(n)
+    hip.write(buf, values)
+    return values, buf
+
+
+# ---- model/titania.rs:268-370 ----
+
+def test_elementwise(hip):
+    n = 300
+    cx, x = buffers(hip, n, 1)
+    cy, y = buffers(hip, n, 2)
+    cx = ref.add(cx, cy)
+    hip.add(x, y)
+    assert_close(hip.read(x), cx, what="add")
+
+    cx = ref.silu_mul(cx, cy)
+    hip.silu_mul(x, y)
+    assert_close(hip.read(x), cx, what="silu_mul")
+
+    cdst, dst = buffers(hip, n + 10, 3)
+    cdst = ref.copy(cdst, 7, cx, 5, n - 5)
+    hip.copy(dst, 7, x, 5, n - 5)
+    assert_close(hip.read(dst), cdst, what="copy")
+
+
+def test_resize(hip):
+    cx, x = buffers(hip, 300, 1)
+    cy, y = buffers(hip, 100, 2)
+    hip.resize(x, 100)
+    cx = ref.add(cx[:100], cy)
+    hip.add(x, y)
+    assert_close(hip.read(x), cx, what="resize+add")
+    hip.resize(x, 300)
+    assert len(hip.read(x)) == 300
+
+
+def test_embed(hip):
+    table = tensor((10, 128), 4)
+    tokens = [3, 9, 0]
+    _, out = buffers(hip, 3 * 128, 5)
+    expected = ref.embed(table.data, 128, tokens)
+    w = hip.upload(table)
+    hip.embed(out, w, tokens)
+    got = hip.read(out)
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), "embed is exact"
+
+
+@pytest.mark.parametrize("rows,cols,n", [(24, 256, 1), (5, 64, 3), (9, 384, 16), (24, 128, 19)])
+def test_matmul(hip, rows, cols, n):
+    w = tensor((rows, cols), 6)
+    cx, x = buffers(hip, n * cols, 7)
+    _, out = buffers(hip, n * rows, 8)
+    expected = ref.matmul(w.data, rows, cols, cx)
+    hip.matmul(out, hip.upload(w), x)
+    assert_close(hip.read(out), expected, what=f"matmul {rows}x{cols} n={n}")
+
+
+@pytest.mark.parametrize("rows,dim", [(3, 128), (1, 1024), (9, 64)])
+def test_rmsnorm(hip, rows, dim):
+    weight = tensor((dim,), 9)
+    cx, x = buffers(hip, rows * dim, 10)
+    expected = ref.rmsnorm(cx, weight.data, 1e-6)
+    hip.rmsnorm(x, hip.upload(weight), 1e-6)
+    assert_close(hip.read(x), expected, what="rmsnorm")
+
+
+@pytest.mark.parametrize("n", [1, 3])
+def test_rope(hip, n):
+    cx, x = buffers(hip, n * 4 * 128, 11)
+    ctable, table = buffers(hip, 40 * 128, 16)
+    expected = ref.rope(cx, ctable, 37, 4, 128)
+    hip.rope(x, table, 37, 4, 128)
+    assert_close(hip.read(x), expected, what="rope")
+
+
+@pytest.mark.parametrize("pos,n", [(0, 1), (6, 1), (32, 1), (39, 1), (0, 5), (30, 10)])
+def test_attention(hip, pos, n):
+    n_heads, head_dim, n_kv_heads, max_len = 4, 64, 2, 40
+    kv_len = max_len * n_kv_heads * head_dim
+    cq, q = buffers(hip, n * n_heads * head_dim, 12)
+    ck, k = buffers(hip, kv_len, 13)
+    cv, v = buffers(hip, kv_len, 14)
+    _, out = buffers(hip, n * n_heads * head_dim, 15)
+    if pos + n > max_len:
+        pytest.skip("past the cache")
+    expected = ref.attention(cq, ck, cv, pos, n_heads, head_dim, n_kv_heads)
+    hip.attention(out, q, k, v, pos, n_heads, head_dim, n_kv_heads)
+    assert_close(hip.read(out), expected, what=f"attention pos={pos} n={n}")
+
+
+# ---- the reference's panics are errors here ----
+
+def test_misuse_is_an_error(hip):
+    x = hip.alloc(10)
+    with pytest.raises(InvalidArgument):
+        hip.resize(x, 11)
+    with pytest.raises(InvalidArgument):
+        hip.write(x, np.zeros(9, np.float32))
+    w = hip.upload(tensor((4, 8), 1))
+    out = hip.alloc(4)
+    with pytest.raises(InvalidArgument):
+        hip.matmul(out, w, x)  # 10 is not a whole number of 8-long rows
+    table = hip.upload(tensor((10, 8), 2))
+    e = hip.alloc(8)
+    with pytest.raises(InvalidArgument):
+        hip.embed(e, table, [10])  # past the table
+    rt = hip.alloc(4 * 8)
+    q = hip.alloc(2 * 8)
+    with pytest.raises(InvalidArgument):
+        hip.rope(q, rt, 4, 2, 8)  # position 4 is past a 4-position table
+    with pytest.raises(InvalidArgument):
+        hip.copy(x, 5, x, 0, 6)
+
+
+# ---- Qwen3-0.6B decode shapes: bf16 W and f32 x, N(0, 1) ----
+
+QWEN_GEMV = {
+    "q": (2048, 1024), "k+v": (1024, 1024), "o": (1024, 2048), "gate+up": (6144, 1024),
+    "down": (1024, 3072), "lm_head": (151936, 1024),
+}
+
+
+def _row_bound(wbits, rows, cols, x, n):
+    w = bf16_to_f32(wbits).reshape(rows, cols).astype(np.float64)
+    xx = np.asarray(x, np.float64).reshape(n, cols)
+    return (np.abs(xx) @ np.abs(w).T).reshape(-1)
+
+
+@pytest.mark.parametrize("name", list(QWEN_GEMV))
+@pytest.mark.parametrize("n", [1, 4])
+def test_qwen_gemv(hip, name, n):
+    rows, cols = QWEN_GEMV[name]
+    wbits = normal_bf16(rows * cols, 100, name)
+    x = bf16_to_f32(normal_bf16(n * cols, 101, name + "x")) + np.float32(1e-3) * bf16_to_f32(
+        normal_bf16(n * cols, 102, name + "x2"))
+    expected = ref.matmul(wbits, rows, cols, x)
+    xb = hip.alloc(n * cols)
+    hip.write(xb, x)
+    out = hip.alloc(n * rows)
+    hip.matmul(out, hip.upload(Tensor((rows, cols), wbits)), xb)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-3
+    # fp32 accumulation in another order: within a few ulps of the row's magnitude.
+    bound = _row_bound(wbits, rows, cols, x, n)
+    assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
+
+
+@pytest.mark.parametrize("n", [16, 64])
+def test_qwen_gemm(hip, n):
+    rows, cols = 2048, 1024
+    wbits = normal_bf16(rows * cols, 103, "gemm")
+    x = bf16_to_f32(normal_bf16(n * cols, 104, "gemmx")) * np.float32(1.37)
+    expected = ref.matmul(wbits, rows, cols, x)
+    xb = hip.alloc(n * cols)
+    hip.write(xb, x)
+    out = hip.alloc(n * rows)
+    hip.matmul(out, hip.upload(Tensor((rows, cols), wbits)), xb)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-3
+    bound = _row_bound(wbits, rows, cols, x, n)
+    assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
+
+
+def test_qwen_norms_and_rope(hip):
+    # RMSNorm over 1024 and per head over 128 (16 q heads + 8 k heads), gains 1 + N(0, .1).
+    for rows, dim, seed in [(1, 1024, 110), (16, 128, 111), (8, 128, 112)]:
+        g = f32_to_bf16(1.0 + bf16_to_f32(normal_bf16(dim, seed, "g", 0.1)))
+        x = bf16_to_f32(normal_bf16(rows * dim, seed, "x")) * np.float32(3.0)
+        expected = ref.rmsnorm(x, g, 1e-6)
+        xb = hip.alloc(rows * dim)
+        hip.write(xb, x)
+        hip.rmsnorm(xb, hip.upload(Tensor((dim,), g)), 1e-6)
+        got = hip.read(xb)
+        assert rel_error(got, expected) <= 1e-3
+        assert_close(got, expected, rel=1e-5, abs_=1e-6, what=f"rmsnorm {rows}x{dim}")
+    # RoPE on 16 + 8 heads x 128 with the theta = 1e6 table at a late position.
+    table = ref.rope_table(4096, 128, 1e6)
+    tb = hip.alloc(table.size)
+    hip.write(tb, table)
+    for heads in (16, 8):
+        x = bf16_to_f32(normal_bf16(heads * 128, 113 + heads, "r"))
+        expected = ref.rope(x, table, 4000, heads, 128)
+        xb = hip.alloc(x.size)
+        hip.write(xb, x)
+        hip.rope(xb, tb, 4000, heads, 128)
+        assert_close(hip.read(xb), expected, rel=1e-5, abs_=1e-6, what="rope")
+
+
+@pytest.mark.parametrize("ctx", [512, 4096, 32768])
+def test_qwen_decode_attention(hip, ctx):
+    """GQA decode: 16 Q heads, 8 KV heads, head_dim 128, caches of bf16-rounded
+    N(0, 1), the query at position ctx - 1."""
+    H, KVH, hd = 16, 8, 128
+    kv = bf16_to_f32(normal_bf16(ctx * KVH * hd, ctx, "k"))
+    vv = bf16_to_f32(normal_bf16(ctx * KVH * hd, ctx, "v"))
+    q = bf16_to_f32(normal_bf16(H * hd, ctx, "q"))
+    expected = ref.attention(q, kv, vv, ctx - 1, H, hd, KVH)
+    bk, bv, bq, out = hip.alloc(kv.size), hip.alloc(vv.size), hip.alloc(q.size), hip.alloc(q.size)
+    hip.write(bk, kv)
+    hip.write(bv, vv)
+    hip.write(bq, q)
+    hip.attention(out, bq, bk, bv, ctx - 1, H, hd, KVH)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-3
+    assert_close(got, expected, rel=1e-4, abs_=1e-5, what=f"attention ctx={ctx}")
+
+
+def test_prefill_attention(hip):
+    """Causal attention of 100 tokens from position 20 (several splits)."""
+    H, KVH, hd, n, pos = 16, 8, 128, 100, 20
+    L = pos + n
+    kv = bf16_to_f32(normal_bf16(L * KVH * hd, 7, "pk"))
+    vv = bf16_to_f32(normal_bf16(L * KVH * hd, 7, "pv"))
+    q = bf16_to_f32(normal_bf16(n * H * hd, 7, "pq"))
+    expected = ref.attention(q, kv, vv, pos, H, hd, KVH)
+    bk, bv, bq, out = hip.alloc(kv.size), hip.alloc(vv.size), hip.alloc(q.size), hip.alloc(q.size)
+    hip.write(bk, kv)
+    hip.write(bv, vv)
+    hip.write(bq, q)
+    hip.attention(out, bq, bk, bv, pos, H, hd, KVH)
+    assert_close(hip.read(out), expected, rel=1e-4, abs_=1e-5, what="prefill attention")
+
+
+# ---- fused extensions ----
+
+def test_add_rmsnorm(hip):
+    rows, dim = 3, 1024
+    g = f32_to_bf16(1.0 + bf16_to_f32(normal_bf16(dim, 120, "g", 0.1)))
+    x = numbers(rows * dim, 21)
+    y = numbers(rows * dim, 22)
+    cx = ref.add(x, y)
+    cxb = ref.rmsnorm(cx, g, 1e-6)
+    bx, by, bxb = hip.alloc(x.size), hip.alloc(y.size), hip.alloc(x.size)
+    hip.write(bx, x)
+    hip.write(by, y)
+    hip.add_rmsnorm(bx, by, bxb, hip.upload(Tensor((dim,), g)), 1e-6)
+    assert_close(hip.read(bx), cx, what="x += y")
+    assert_close(hip.read(bxb), cxb, what="rmsnorm(x)")
+
+
+def test_argmax(hip):
+    v = 151936
+    x = bf16_to_f32(normal_bf16(v, 130, "logits"))
+    b = hip.alloc(v)
+    hip.write(b, x)
+    assert hip.argmax(b) == ref.argmax(x) == int(np.argmax(x))
+    # Ties go to the lowest index; -0.0 < +0.0 under total order.
+    y = np.zeros(v, np.float32)
+    y[[5000, 70000, 150000]] = 3.0
+    hip.write(b, y)
+    assert hip.argmax(b) == ref.argmax(y) == 5000
+    z = np.full(v, -1.0, np.float32)
+    z[10] = -0.0
+    z[11] = 0.0
+    hip.write(b, z)
+    assert hip.argmax(b) == ref.argmax(z) == 11

@@ -1,0 +1,114 @@
+"""End-to-end parity of the forward pass and the greedy decode loop against the
+CPU oracle (model/model.rs:83-149 restated in oracle/cpu_ref.c).
+
+Bars (the north star's): final logits within 2e-2 max-abs, identical greedy
+token streams. A token stream may only differ at a step where the oracle's two
+largest logits are closer than the logit error bound; with fp32 caches the
+error is ~1e-5, so on these seeds the streams must match exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import ref
+from titania_amd import QWEN3_0_6B, QWEN3_TINY, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS
+from titania_amd import synth
+from titania_amd.model import Model, State
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def tiny(hip):
+    w = synth.weights(QWEN3_TINY, seed=3, random_gains=True)
+    m = Model(hip, QWEN3_TINY, w)
+    yield m, ref.RefModel(QWEN3_TINY, w)
+    m.close()
+
+
+@pytest.mark.parametrize("path", [TH_PATH_OPS, TH_PATH_FUSED])
+def test_tiny_forward(tiny, path):
+    m, r = tiny
+    c = QWEN3_TINY
+    prompt = synth.prompt(100, c.vocab_size, seed=5)  # more than one 64-token batch
+    st, rs = State(m, 128), r.state(128)
+    got = m.forward(st, prompt, 0, path)
+    exp = r.forward(rs, prompt, 0)
+    assert np.max(np.abs(got - exp)) <= 1e-4
+    for i, tok in enumerate([7, 999, 0]):
+        got = m.forward(st, [tok], 100 + i, path)
+        exp = r.forward(rs, [tok], 100 + i)
+        assert np.max(np.abs(got - exp)) <= 1e-4
+    st.close()
+
+
+@pytest.mark.parametrize("kv", [TH_KV_F32, TH_KV_BF16])
+def test_tiny_decode(tiny, kv):
+    m, r = tiny
+    c = QWEN3_TINY
+    prompt = synth.prompt(9, c.vocab_size, seed=6)
+    steps = 20
+    st = State(m, 64, kv)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    toks, logits = m.decode(st, len(prompt), steps, keep_logits=True)
+    rtoks, gaps, last = r.generate(r.state(64), prompt, steps)
+    tol = 1e-4 if kv == TH_KV_F32 else LOGIT_TOL
+    assert float(np.std(last)) > 0.05
+    assert np.max(np.abs(logits[-1] - last)) <= tol
+    assert list(toks) == list(rtoks) or np.min(gaps) < tol
+    # The decode loop continues where it left off.
+    more = m.decode(st, len(prompt) + steps, 5)
+    assert len(more) == 5
+    st.close()
+
+
+def test_paths_refuse_to_mix(tiny):
+    m, _ = tiny
+    st = State(m, 32)
+    m.forward(st, [1, 2, 3], 0, TH_PATH_OPS)
+    with pytest.raises(Exception):
+        m.forward(st, [4], 3, TH_PATH_FUSED)
+    st.close()
+
+
+@pytest.fixture(scope="module")
+def qwen06(hip):
+    w = synth.weights(QWEN3_0_6B, seed=0)
+    m = Model(hip, QWEN3_0_6B, w)
+    yield m, ref.RefModel(QWEN3_0_6B, w)
+    m.close()
+
+
+def test_qwen06_greedy(qwen06):
+    """Qwen3-0.6B shape, seeded N(0, 0.02) weights: 16-token prompt, 32 greedy steps."""
+    m, r = qwen06
+    c = QWEN3_0_6B
+    prompt = synth.prompt(16, c.vocab_size, seed=0)
+    steps = 32
+    st = State(m, 16 + steps)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    toks, logits = m.decode(st, 16, steps, keep_logits=True)
+    rtoks, gaps, last = r.generate(r.state(16 + steps), prompt, steps)
+    # The run is not vacuous: the oracle's logits spread like N(0, 0.64) and pick several tokens.
+    assert 0.3 < float(np.std(last)) < 2.0
+    assert len(set(rtoks.tolist())) >= 2
+    err = float(np.max(np.abs(logits[-1] - last)))
+    assert err <= LOGIT_TOL, err
+    first_diff = next((i for i in range(steps) if toks[i] != rtoks[i]), None)
+    assert first_diff is None, (first_diff, float(gaps[first_diff]), err)
+    st.close()
+
+
+def test_qwen06_ops_path_logits(qwen06):
+    """The trait-primitive path on the same model: prompt logits against the oracle."""
+    m, r = qwen06
+    prompt = synth.prompt(16, QWEN3_0_6B.vocab_size, seed=1)
+    st = State(m, 32)
+    got = m.forward(st, prompt, 0, TH_PATH_OPS)
+    exp = r.forward(r.state(32), prompt, 0)
+    assert float(np.max(np.abs(got - exp))) <= LOGIT_TOL
+    st.close()

@@ -1,0 +1,246 @@
+// Device::attention (model/cpu.rs:113-149): causal grouped-query attention over
+// key/value caches, as split-K flash decoding.
+//
+// One block handles one (token, KV head, split of the sequence); every query
+// head that shares the KV head is processed in the same block, so each cached
+// key and value row is read once per block. A split walks its positions in
+// sub-chunks of up to 256 whose scores sit in LDS, keeping a running max, sum
+// of exponentials and unnormalized accumulator (online softmax). With one split
+// the block writes the normalized output; otherwise it writes its partial and
+// a combine pass merges the splits by log-sum-exp rescaling.
+//
+// The split ranges are derived on the device from the token's context length,
+// so a launch of fixed shape serves any position; the position may come from
+// device memory, which lets one captured decode step replay at every position.
+#include "common.h"
+#include "device_util.h"
+
+namespace th {
+
+constexpr int kAttnMaxGroup = 8;   // query heads per KV head
+constexpr int kAttnSub = 256;      // positions scored per sub-chunk
+
+template <typename KV>
+__device__ __forceinline__ void load8(const KV *p, float f[8]);
+
+template <>
+__device__ __forceinline__ void load8<float>(const float *p, float f[8]) {
+    float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t *p, float f[8]) {
+    unpack8(*reinterpret_cast<const uint4 *>(p), f);
+}
+
+__device__ __forceinline__ float load1(const float *p) { return *p; }
+__device__ __forceinline__ float load1(const uint16_t *p) { return bf16_to_f32(*p); }
+
+template <int HD, typename KV>
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnKernelArgs a) {
+    constexpr int LPK = HD / 8;      // lanes per key row (8 elements each)
+    constexpr int KPW = 64 / LPK;    // key rows per wave per step
+    constexpr int KPB = 4 * KPW;     // key rows per block per step
+    constexpr int NP = 256 / HD;     // thread groups splitting the value rows
+
+    __shared__ float scores[kAttnMaxGroup][kAttnSub];
+    __shared__ float red[kAttnMaxGroup][256];
+    __shared__ float stat_m[kAttnMaxGroup], stat_l[kAttnMaxGroup], alpha[kAttnMaxGroup];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x % a.nsplit;
+    const int g = (blockIdx.x / a.nsplit) % a.n_kv_heads;
+    const long long t = blockIdx.x / (a.nsplit * a.n_kv_heads);
+    const int G = a.group;
+    const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
+    const long long len = pos + t + 1;  // the token attends up to its own position
+    const long long chunk = ((len + a.nsplit - 1) / a.nsplit + 15) / 16 * 16;
+    const long long s0 = (long long)split * chunk;
+    const long long s1 = s0 + chunk < len ? s0 + chunk : len;
+
+    const KV *kb = reinterpret_cast<const KV *>(a.k) + (long long)g * a.head_stride;
+    const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
+
+    // This lane's 8 elements of every query head in the group.
+    const int sub = lane % LPK;
+    float qf[kAttnMaxGroup][8];
+#pragma unroll
+    for (int gg = 0; gg < kAttnMaxGroup; ++gg) {
+        if (gg < G) {
+            const float *qh = a.q + ((t * a.n_heads) + (long long)g * G + gg) * HD + sub * 8;
+            load8<float>(qh, qf[gg]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qf[gg][i] = 0.f;
+        }
+    }
+    if (tid < kAttnMaxGroup) {
+        stat_m[tid] = -INFINITY;
+        stat_l[tid] = 0.f;
+    }
+
+    const int d = tid % HD, part = tid / HD;
+    float acc[kAttnMaxGroup];
+#pragma unroll
+    for (int gg = 0; gg < kAttnMaxGroup; ++gg) acc[gg] = 0.f;
+
+    for (long long c0 = s0; c0 < s1; c0 += kAttnSub) {
+        const int cnt = (int)(s1 - c0 < kAttnSub ? s1 - c0 : kAttnSub);
+        // Scores q . k_j * scale.
+        for (int j0 = 0; j0 < cnt; j0 += KPB) {
+            const int j = j0 + wave * KPW + lane / LPK;
+            const bool valid = j < cnt;
+            float kf[8];
+            if (valid) {
+                load8<KV>(kb + (c0 + j) * a.pos_stride + sub * 8, kf);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kf[i] = 0.f;
+            }
+#pragma unroll
+            for (int gg = 0; gg < kAttnMaxGroup; ++gg) {
+                if (gg < G) {
+                    float dd = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) dd = fmaf(qf[gg][i], kf[i], dd);
+                    dd = group_sum<LPK>(dd);
+                    if (valid && sub == 0) scores[gg][j] = a.scale * dd;
+                }
+            }
+        }
+        __syncthreads();
+        // Per query head: new running max, exponentials in place, running sum.
+        for (int gg = wave; gg < G; gg += 4) {
+            float m = -INFINITY;
+            for (int j = lane; j < cnt; j += 64) m = fmaxf(m, scores[gg][j]);
+            m = wave_max(m);
+            const float m_old = stat_m[gg];
+            const float m_new = fmaxf(m_old, m);
+            float l = 0.f;
+            for (int j = lane; j < cnt; j += 64) {
+                float p = expf(scores[gg][j] - m_new);
+                scores[gg][j] = p;
+                l += p;
+            }
+            l = wave_sum(l);
+            if (lane == 0) {
+                const float al = expf(m_old - m_new);
+                alpha[gg] = al;
+                stat_l[gg] = stat_l[gg] * al + l;
+                stat_m[gg] = m_new;
+            }
+        }
+        __syncthreads();
+        // acc = acc * alpha + sum of p_j * v_j; thread (part, d) takes every NP-th position.
+#pragma unroll
+        for (int gg = 0; gg < kAttnMaxGroup; ++gg)
+            if (gg < G) acc[gg] *= alpha[gg];
+        for (int j = part; j < cnt; j += NP) {
+            float v = load1(vb + (c0 + j) * a.pos_stride + d);
+#pragma unroll
+            for (int gg = 0; gg < kAttnMaxGroup; ++gg)
+                if (gg < G) acc[gg] = fmaf(scores[gg][j], v, acc[gg]);
+        }
+        __syncthreads();  // scores and alpha are rewritten by the next sub-chunk
+    }
+
+    __syncthreads();  // the statistics are complete (also when the split is empty)
+    if (NP > 1) {
+#pragma unroll
+        for (int gg = 0; gg < kAttnMaxGroup; ++gg)
+            if (gg < G) red[gg][tid] = acc[gg];
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int gg = 0; gg < kAttnMaxGroup; ++gg) {
+                if (gg < G) {
+                    float s = red[gg][d];
+                    for (int p = 1; p < NP; ++p) s += red[gg][p * HD + d];
+                    acc[gg] = s;
+                }
+            }
+        }
+    }
+    if (part != 0) return;
+
+    for (int gg = 0; gg < G; ++gg) {
+        const long long h = (long long)g * G + gg;
+        if (a.nsplit == 1) {
+            a.out[(t * a.n_heads + h) * HD + d] = acc[gg] / stat_l[gg];
+        } else {
+            const long long slot = (t * a.n_heads + h) * a.nsplit + split;
+            a.part_acc[slot * HD + d] = acc[gg];
+            if (d == 0) {
+                a.part_ml[slot * 2] = stat_m[gg];
+                a.part_ml[slot * 2 + 1] = stat_l[gg];
+            }
+        }
+    }
+}
+
+// Merges the splits of one (token, head): rescales each split's sum and
+// accumulator by exp(m_split - m_max); empty splits (m = -inf) add nothing.
+__global__ void attn_combine_kernel(float *__restrict__ out, const float *__restrict__ part_acc,
+                                    const float *__restrict__ part_ml, int nsplit, int hd) {
+    const long long th = blockIdx.x;  // token * n_heads + head
+    const float *ml = part_ml + th * nsplit * 2;
+    float m = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) m = fmaxf(m, ml[2 * s]);
+    float l = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+        float ms = ml[2 * s];
+        if (ms != -INFINITY) l += ml[2 * s + 1] * expf(ms - m);
+    }
+    for (int dd = threadIdx.x; dd < hd; dd += blockDim.x) {
+        float acc = 0.f;
+        for (int s = 0; s < nsplit; ++s) {
+            float ms = ml[2 * s];
+            if (ms != -INFINITY) acc += part_acc[(th * nsplit + s) * hd + dd] * expf(ms - m);
+        }
+        out[th * hd + dd] = acc / l;
+    }
+}
+
+int attention_splits(size_t n, size_t n_kv_heads, size_t max_len) {
+    // One split while a block's share is short; otherwise about two blocks per
+    // CU, each split covering at least 64 positions.
+    if (max_len <= 512) return 1;
+    size_t blocks_per_split = n * n_kv_heads;
+    size_t want = (512 + blocks_per_split - 1) / blocks_per_split;
+    size_t cap = (max_len + 63) / 64;
+    size_t s = std::min(want, cap);
+    return (int)std::max<size_t>(1, std::min<size_t>(s, 256));
+}
+
+size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit) {
+    if (nsplit <= 1) return 0;
+    return n * n_heads * (size_t)nsplit * (head_dim + 2);
+}
+
+template <int HD>
+static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
+    dim3 grid((unsigned)(n * (size_t)k.n_kv_heads * (size_t)k.nsplit));
+    if (k.kv_bf16)
+        attn_split_kernel<HD, uint16_t><<<grid, 256, 0, s>>>(k);
+    else
+        attn_split_kernel<HD, float><<<grid, 256, 0, s>>>(k);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || k.nsplit == 1) return e;
+    attn_combine_kernel<<<dim3((unsigned)(n * (size_t)k.n_heads)), dim3(HD), 0, s>>>(k.out, k.part_acc, k.part_ml,
+                                                                                     k.nsplit, HD);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim) {
+    if (n == 0) return hipSuccess;
+    switch (head_dim) {
+    case 64: return attn_launch<64>(s, k, n);
+    case 128: return attn_launch<128>(s, k, n);
+    case 256: return attn_launch<256>(s, k, n);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace th

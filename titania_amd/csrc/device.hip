@@ -1,0 +1,378 @@
+// The C ABI of the hip device: one entry point per method of the reference's
+// Device trait (model/device.rs:9-89), argument checks mirroring the
+// reference's asserts, and the fused extensions.
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "common.h"
+
+namespace {
+thread_local std::string g_error;
+}
+
+namespace th {
+
+int fail(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+void clear_error() { g_error.clear(); }
+
+void *scratch(th_device *dev, size_t bytes) {
+    if (bytes <= dev->scratch_bytes) return dev->scratch;
+    size_t want = std::max(bytes, dev->scratch_bytes * 2);
+    want = (want + 255) & ~(size_t)255;
+    if (dev->scratch) {
+        if (hipStreamSynchronize(dev->stream) != hipSuccess) return nullptr;
+        (void)hipFree(dev->scratch);
+        dev->scratch = nullptr;
+        dev->scratch_bytes = 0;
+    }
+    if (hipMalloc(&dev->scratch, want) != hipSuccess) {
+        dev->scratch = nullptr;
+        return nullptr;
+    }
+    dev->scratch_bytes = want;
+    return dev->scratch;
+}
+
+// Copies host token ids into the device's staging area, checking each against
+// the table's row count (the reference indexes out of bounds and panics).
+static int stage_tokens(th_device *dev, const uint32_t *tokens, size_t n, size_t limit, uint32_t **out) {
+    for (size_t i = 0; i < n; ++i)
+        TH_REQUIRE(tokens[i] < limit, "token %u at index %zu is past the table's %zu rows", tokens[i], i, limit);
+    if (n > dev->tokens_cap) {
+        size_t cap = std::max<size_t>(n, 1024);
+        uint32_t *p = nullptr;
+        TH_HIP(hipStreamSynchronize(dev->stream));
+        if (dev->tokens) TH_HIP(hipFree(dev->tokens));
+        dev->tokens = nullptr;
+        dev->tokens_cap = 0;
+        TH_HIP(hipMalloc(&p, cap * sizeof(uint32_t)));
+        dev->tokens = p;
+        dev->tokens_cap = cap;
+    }
+    TH_HIP(hipMemcpyAsync(dev->tokens, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, dev->stream));
+    *out = dev->tokens;
+    return TH_OK;
+}
+
+}  // namespace th
+
+using th::fail;
+
+extern "C" {
+
+const char *th_last_error(void) { return g_error.c_str(); }
+
+int th_device_create(int ordinal, th_device **out) {
+    th::clear_error();
+    TH_REQUIRE(out != nullptr, "th_device_create: null output");
+    int count = 0;
+    TH_HIP(hipGetDeviceCount(&count));
+    TH_REQUIRE(ordinal >= 0 && ordinal < count, "no GPU %d (%d present)", ordinal, count);
+    TH_HIP(hipSetDevice(ordinal));
+    hipDeviceProp_t prop;
+    TH_HIP(hipGetDeviceProperties(&prop, ordinal));
+    auto *dev = new (std::nothrow) th_device();
+    if (!dev) return fail(TH_ERR_NOMEM, "out of host memory");
+    dev->ordinal = ordinal;
+    dev->num_cus = prop.multiProcessorCount;
+    hipError_t e = hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc(&dev->token_out, 256);
+    if (e == hipSuccess) e = hipEventCreate(&dev->ev_begin);
+    if (e == hipSuccess) e = hipEventCreate(&dev->ev_end);
+    if (e != hipSuccess) {
+        th_device_destroy(dev);
+        return fail(TH_ERR_HIP, "device setup failed: %s", hipGetErrorString(e));
+    }
+    *out = dev;
+    return TH_OK;
+}
+
+void th_device_destroy(th_device *dev) {
+    if (!dev) return;
+    (void)hipSetDevice(dev->ordinal);
+    if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+    if (dev->tokens) (void)hipFree(dev->tokens);
+    if (dev->scratch) (void)hipFree(dev->scratch);
+    if (dev->token_out) (void)hipFree(dev->token_out);
+    if (dev->ev_begin) (void)hipEventDestroy(dev->ev_begin);
+    if (dev->ev_end) (void)hipEventDestroy(dev->ev_end);
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
+    delete dev;
+}
+
+int th_device_synchronize(th_device *dev) {
+    TH_REQUIRE(dev, "null device");
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_timer_begin(th_device *dev) {
+    TH_REQUIRE(dev, "null device");
+    TH_HIP(hipEventRecord(dev->ev_begin, dev->stream));
+    return TH_OK;
+}
+
+int th_timer_end(th_device *dev, float *ms) {
+    TH_REQUIRE(dev && ms, "th_timer_end: null argument");
+    TH_HIP(hipEventRecord(dev->ev_end, dev->stream));
+    TH_HIP(hipEventSynchronize(dev->ev_end));
+    TH_HIP(hipEventElapsedTime(ms, dev->ev_begin, dev->ev_end));
+    return TH_OK;
+}
+
+int th_upload(th_device *dev, const uint16_t *data, const size_t *shape, size_t ndim, th_weight **out) {
+    TH_REQUIRE(dev && shape && out, "th_upload: null argument");
+    TH_REQUIRE(ndim == 1 || ndim == 2, "a weight has 1 or 2 dimensions, not %zu", ndim);
+    size_t numel = 1;
+    for (size_t i = 0; i < ndim; ++i) numel *= shape[i];
+    TH_REQUIRE(numel == 0 || data, "th_upload: null data");
+    auto *w = new (std::nothrow) th_weight();
+    if (!w) return fail(TH_ERR_NOMEM, "out of host memory");
+    w->ndim = ndim;
+    w->shape[0] = shape[0];
+    w->shape[1] = ndim == 2 ? shape[1] : 0;
+    w->numel = numel;
+    size_t bytes = std::max<size_t>(numel * 2, 16);
+    hipError_t e = hipMalloc(&w->ptr, bytes);
+    if (e == hipSuccess && numel) e = hipMemcpyAsync(w->ptr, data, numel * 2, hipMemcpyHostToDevice, dev->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+    if (e != hipSuccess) {
+        if (w->ptr) (void)hipFree(w->ptr);
+        delete w;
+        return fail(e == hipErrorOutOfMemory ? TH_ERR_NOMEM : TH_ERR_HIP, "upload of %zu bf16 failed: %s", numel,
+                    hipGetErrorString(e));
+    }
+    *out = w;
+    return TH_OK;
+}
+
+void th_weight_free(th_device *dev, th_weight *w) {
+    if (!w) return;
+    if (dev) (void)hipStreamSynchronize(dev->stream);
+    if (w->ptr) (void)hipFree(w->ptr);
+    delete w;
+}
+
+int th_weight_shape(const th_weight *w, size_t *shape, size_t *ndim) {
+    TH_REQUIRE(w && shape && ndim, "th_weight_shape: null argument");
+    *ndim = w->ndim;
+    shape[0] = w->shape[0];
+    if (w->ndim == 2) shape[1] = w->shape[1];
+    return TH_OK;
+}
+
+int th_alloc(th_device *dev, size_t len, th_buffer **out) {
+    TH_REQUIRE(dev && out, "th_alloc: null argument");
+    auto *b = new (std::nothrow) th_buffer();
+    if (!b) return fail(TH_ERR_NOMEM, "out of host memory");
+    size_t bytes = std::max<size_t>(len * sizeof(float), 16);
+    hipError_t e = hipMalloc(&b->ptr, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(b->ptr, 0, bytes, dev->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(dev->stream);
+    if (e != hipSuccess) {
+        if (b->ptr) (void)hipFree(b->ptr);
+        delete b;
+        return fail(e == hipErrorOutOfMemory ? TH_ERR_NOMEM : TH_ERR_HIP, "alloc of %zu floats failed: %s", len,
+                    hipGetErrorString(e));
+    }
+    b->len = b->cap = len;
+    *out = b;
+    return TH_OK;
+}
+
+void th_buffer_free(th_device *dev, th_buffer *b) {
+    if (!b) return;
+    if (dev) (void)hipStreamSynchronize(dev->stream);
+    if (b->ptr) (void)hipFree(b->ptr);
+    delete b;
+}
+
+// model/cpu.rs:22 / model/titania.rs:125
+int th_resize(th_device *dev, th_buffer *b, size_t len) {
+    TH_REQUIRE(dev && b, "th_resize: null argument");
+    TH_REQUIRE(len <= b->cap, "a buffer of %zu activations can't hold %zu", b->cap, len);
+    b->len = len;
+    return TH_OK;
+}
+
+size_t th_buffer_len(const th_buffer *b) { return b ? b->len : 0; }
+
+int th_read(th_device *dev, const th_buffer *b, float *out, size_t len) {
+    TH_REQUIRE(dev && b, "th_read: null argument");
+    TH_REQUIRE(len == b->len, "reading %zu activations from a buffer of %zu", len, b->len);
+    TH_REQUIRE(len == 0 || out, "th_read: null output");
+    if (len) TH_HIP(hipMemcpyAsync(out, b->ptr, len * sizeof(float), hipMemcpyDeviceToHost, dev->stream));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+// model/titania.rs:133-137: data.len must equal the buffer's length.
+int th_write(th_device *dev, th_buffer *b, const float *data, size_t len) {
+    TH_REQUIRE(dev && b, "th_write: null argument");
+    TH_REQUIRE(len == b->len, "writing %zu activations into a buffer of %zu", len, b->len);
+    TH_REQUIRE(len == 0 || data, "th_write: null data");
+    if (len) TH_HIP(hipMemcpyAsync(b->ptr, data, len * sizeof(float), hipMemcpyHostToDevice, dev->stream));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+// model/titania.rs:139-143
+int th_copy(th_device *dev, th_buffer *dst, size_t dst_offset, const th_buffer *src, size_t src_offset,
+            size_t len) {
+    TH_REQUIRE(dev && dst && src, "th_copy: null argument");
+    TH_REQUIRE(dst_offset <= dst->len && len <= dst->len - dst_offset, "copy of %zu to offset %zu of a buffer of %zu",
+               len, dst_offset, dst->len);
+    TH_REQUIRE(src_offset <= src->len && len <= src->len - src_offset,
+               "copy of %zu from offset %zu of a buffer of %zu", len, src_offset, src->len);
+    TH_HIP(th::launch_copy(dev->stream, dst->ptr + dst_offset, src->ptr + src_offset, len));
+    return TH_OK;
+}
+
+// model/cpu.rs:38-47 / model/titania.rs:145-151
+int th_embed(th_device *dev, th_buffer *out, const th_weight *table, const uint32_t *tokens, size_t n) {
+    TH_REQUIRE(dev && out && table, "th_embed: null argument");
+    TH_REQUIRE(table->ndim == 2, "an embedding table has 2 dimensions");
+    size_t dim = table->shape[1];
+    TH_REQUIRE(out->len == n * dim, "embedding %zu tokens of %zu into a buffer of %zu", n, dim, out->len);
+    if (n == 0) return TH_OK;
+    TH_REQUIRE(tokens, "th_embed: null tokens");
+    uint32_t *d_tokens = nullptr;
+    int rc = th::stage_tokens(dev, tokens, n, table->shape[0], &d_tokens);
+    if (rc != TH_OK) return rc;
+    TH_HIP(th::launch_embed(dev->stream, out->ptr, table->ptr, dim, d_tokens, n));
+    return TH_OK;
+}
+
+// model/cpu.rs:49-53 / model/titania.rs:153-157
+int th_matmul(th_device *dev, th_buffer *out, const th_weight *w, const th_buffer *x) {
+    TH_REQUIRE(dev && out && w && x, "th_matmul: null argument");
+    TH_REQUIRE(w->ndim == 2, "a matmul weight has 2 dimensions");
+    size_t rows = w->shape[0], cols = w->shape[1];
+    TH_REQUIRE(cols > 0, "a matmul weight has columns");
+    size_t n = x->len / cols;
+    TH_REQUIRE(x->len == n * cols, "x holds %zu activations, not a whole number of %zu-long rows", x->len, cols);
+    TH_REQUIRE(out->len == n * rows, "out holds %zu activations, not %zu tokens x %zu rows", out->len, n, rows);
+    TH_REQUIRE(out->ptr != x->ptr || n == 0, "matmul cannot write its input");
+    TH_HIP(th::launch_matmul(dev->stream, out->ptr, w->ptr, rows, cols, x->ptr, n));
+    return TH_OK;
+}
+
+// model/cpu.rs:79-83 (zip: the shorter length)
+int th_add(th_device *dev, th_buffer *x, const th_buffer *y) {
+    TH_REQUIRE(dev && x && y, "th_add: null argument");
+    TH_HIP(th::launch_add(dev->stream, x->ptr, y->ptr, std::min(x->len, y->len)));
+    return TH_OK;
+}
+
+// model/cpu.rs:85-94: whole weight.len-long rows.
+int th_rmsnorm(th_device *dev, th_buffer *x, const th_weight *w, float eps) {
+    TH_REQUIRE(dev && x && w, "th_rmsnorm: null argument");
+    size_t dim = w->numel;
+    TH_REQUIRE(dim > 0, "an rmsnorm weight has elements");
+    TH_HIP(th::launch_rmsnorm(dev->stream, x->ptr, x->len / dim, w->ptr, dim, eps));
+    return TH_OK;
+}
+
+// model/cpu.rs:96-111 / model/titania.rs:177-184
+int th_rope(th_device *dev, th_buffer *x, const th_buffer *table, size_t pos, size_t n_heads, size_t head_dim) {
+    TH_REQUIRE(dev && x && table, "th_rope: null argument");
+    TH_REQUIRE(n_heads > 0 && head_dim > 0 && head_dim % 2 == 0, "rope needs heads of an even length");
+    size_t n = x->len / (n_heads * head_dim);
+    TH_REQUIRE(x->len == n * n_heads * head_dim, "x holds %zu activations, not whole tokens of %zu x %zu", x->len,
+               n_heads, head_dim);
+    if (n == 0) return TH_OK;
+    TH_REQUIRE((pos + n) * head_dim <= table->len, "position %zu is past the end of the table", pos + n - 1);
+    TH_HIP(th::launch_rope(dev->stream, x->ptr, n, table->ptr, pos, n_heads, head_dim));
+    return TH_OK;
+}
+
+// model/cpu.rs:113-149 / model/titania.rs:186-209
+int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
+                 const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads) {
+    TH_REQUIRE(dev && out && q && k_cache && v_cache, "th_attention: null argument");
+    TH_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
+               "%zu query heads do not split into groups over %zu KV heads", n_heads, n_kv_heads);
+    TH_REQUIRE(n_heads / n_kv_heads <= 8, "at most 8 query heads per KV head are supported");
+    TH_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim %zu is not 64, 128 or 256",
+               head_dim);
+    size_t n = q->len / (n_heads * head_dim);
+    TH_REQUIRE(q->len == n * n_heads * head_dim, "q holds %zu activations, not whole tokens", q->len);
+    TH_REQUIRE(out->len == q->len, "out holds %zu activations, q %zu", out->len, q->len);
+    if (n == 0) return TH_OK;
+    size_t kv_dim = n_kv_heads * head_dim;
+    TH_REQUIRE(k_cache->len >= (pos + n) * kv_dim && v_cache->len >= (pos + n) * kv_dim,
+               "the caches do not hold position %zu", pos + n - 1);
+    TH_REQUIRE(out->ptr != q->ptr, "attention cannot write its queries");
+    int nsplit = th::attention_splits(n, n_kv_heads, pos + n);
+    size_t floats = th::attention_scratch(n, n_heads, head_dim, nsplit);
+    float *scr = nullptr;
+    if (floats) {
+        scr = static_cast<float *>(th::scratch(dev, floats * sizeof(float)));
+        if (!scr) return fail(TH_ERR_NOMEM, "no scratch for attention (%zu floats)", floats);
+    }
+    th::AttnKernelArgs a{};
+    a.out = out->ptr;
+    a.q = q->ptr;
+    a.k = k_cache->ptr;
+    a.v = v_cache->ptr;
+    a.n_heads = (int)n_heads;
+    a.n_kv_heads = (int)n_kv_heads;
+    a.group = (int)(n_heads / n_kv_heads);
+    a.pos = (long long)pos;
+    a.pos_dev = nullptr;
+    a.pos_stride = (long long)kv_dim;  // reference layout: [position][kv head][head_dim]
+    a.head_stride = (long long)head_dim;
+    a.nsplit = nsplit;
+    a.kv_bf16 = 0;
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    a.part_acc = scr;
+    a.part_ml = scr ? scr + n * n_heads * (size_t)nsplit * head_dim : nullptr;
+    TH_HIP(th::launch_attention(dev->stream, a, n, head_dim));
+    return TH_OK;
+}
+
+// model/cpu.rs:151-155 (zip: the shorter length)
+int th_silu_mul(th_device *dev, th_buffer *gate, const th_buffer *up) {
+    TH_REQUIRE(dev && gate && up, "th_silu_mul: null argument");
+    TH_HIP(th::launch_silu_mul(dev->stream, gate->ptr, up->ptr, std::min(gate->len, up->len)));
+    return TH_OK;
+}
+
+int th_add_rmsnorm(th_device *dev, th_buffer *x, const th_buffer *y, th_buffer *xb, const th_weight *w,
+                   float eps) {
+    TH_REQUIRE(dev && x && xb && w, "th_add_rmsnorm: null argument");
+    size_t dim = w->numel;
+    TH_REQUIRE(dim > 0, "an rmsnorm weight has elements");
+    TH_REQUIRE(xb->len == x->len, "xb holds %zu activations, x %zu", xb->len, x->len);
+    TH_REQUIRE(!y || y->len >= x->len, "y holds %zu activations, x %zu", y ? y->len : 0, x->len);
+    TH_REQUIRE(!y || (y->ptr != x->ptr && y->ptr != xb->ptr), "y must not alias x or xb");
+    TH_HIP(th::launch_add_rmsnorm(dev->stream, x->ptr, y ? y->ptr : nullptr, xb->ptr, x->len / dim, w->ptr, dim,
+                                  eps));
+    return TH_OK;
+}
+
+int th_argmax(th_device *dev, const th_buffer *logits, uint32_t *token) {
+    TH_REQUIRE(dev && logits && token, "th_argmax: null argument");
+    TH_REQUIRE(logits->len > 0, "argmax of an empty buffer");
+    size_t m = th::argmax_partials(logits->len);
+    auto *partials = static_cast<uint64_t *>(th::scratch(dev, m * sizeof(uint64_t)));
+    if (!partials) return fail(TH_ERR_NOMEM, "no scratch for argmax");
+    TH_HIP(th::launch_argmax(dev->stream, logits->ptr, logits->len, partials, dev->token_out));
+    TH_HIP(hipMemcpyAsync(token, dev->token_out, sizeof(uint32_t), hipMemcpyDeviceToHost, dev->stream));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,80 @@
+// Device-side helpers shared by the kernels: bf16 unpacking, wave64
+// reductions, the SiLU activation and the packed argmax key.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace th {
+
+// bf16 is the top half of an f32 (model/cpu.rs:158-161).
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Eight bf16 (one 16-byte load) to f32, element order preserved.
+__device__ __forceinline__ void unpack8(const uint4 &w, float f[8]) {
+    f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+    f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+    f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+    f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+
+// Round-to-nearest-even f32 -> bf16 bits (finite inputs; NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint64_t other = __shfl_xor(v, o, 64);
+        v = max_u64(v, other);
+    }
+    return v;
+}
+
+// f32 under IEEE total order (Rust's f32::total_cmp) as an unsigned key, packed
+// above the inverted index so that the u64 maximum is the largest value at the
+// lowest index.
+__device__ __forceinline__ uint64_t argmax_pack(float f, uint32_t idx) {
+    int32_t k = __float_as_int(f);
+    k ^= (int32_t)(((uint32_t)(k >> 31)) >> 1);
+    uint32_t key = (uint32_t)k ^ 0x80000000u;
+    return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint32_t argmax_index(uint64_t packed) {
+    return 0xffffffffu - (uint32_t)(packed & 0xffffffffu);
+}
+
+// model/cpu.rs:153: g / (1 + exp(-g)).
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+}  // namespace th

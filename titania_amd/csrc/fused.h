@@ -1,0 +1,52 @@
+// Fused forward-pass kernels and the device-resident state of the greedy decode loop.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "device_util.h"
+
+namespace th {
+
+// Arguments of the per-head q/k-norm + RoPE + KV append kernel. Caches are
+// addressed as base + head * head_stride + position * pos_stride (elements).
+struct QkvPostArgs {
+    float *q;        // [n][n_heads][head_dim], normalized and rotated in place
+    const float *k;  // [n][n_kv_heads][head_dim]
+    const float *v;  // [n][n_kv_heads][head_dim]
+    const uint16_t *q_norm, *k_norm;  // per-head gains, or null for none
+    const float *rope;                // [max_len][head_dim/2][cos, sin]
+    void *k_cache, *v_cache;
+    long long head_stride, pos_stride;
+    long long pos;
+    const long long *pos_dev;  // position from device memory when not null
+    int n, n_heads, n_kv_heads, head_dim;
+    int kv_bf16;
+    float eps;
+};
+
+hipError_t launch_qk_norm_rope_append(hipStream_t s, const QkvPostArgs &a);
+
+// State of the on-device greedy loop, in device memory so that one captured
+// decode step can replay at every position.
+struct StepState {
+    long long pos;         // position of the token to feed next
+    long long step;        // tokens fed so far in this decode call
+    uint32_t token;        // token to feed next
+    uint32_t pad;
+    uint32_t *tokens_out;  // picks, indexed by step
+    float *logits_out;     // logits after each fed token, or null
+};
+
+// argmax of the logits -> st->token and st->tokens_out[st->step]; with
+// `advance`, pos and step move on first.
+hipError_t launch_pick(hipStream_t s, const float *logits, size_t vocab, uint64_t *partials, StepState *st,
+                       int advance);
+hipError_t launch_keep_logits(hipStream_t s, const float *logits, size_t vocab, const StepState *st);
+
+__device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }
+__device__ __forceinline__ void store_kv(uint16_t *p, float v) { *p = f32_to_bf16(v); }
+
+}  // namespace th

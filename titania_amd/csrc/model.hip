@@ -1,0 +1,518 @@
+// The forward pass of model/model.rs on the hip device: Model (model.rs:10-35),
+// State (model.rs:152-233), Model::forward (model.rs:83-149), and a greedy
+// decode loop that stays on the device (model/chat.rs:149-178 at temperature 0).
+//
+// Two paths compute the same function:
+//  - TH_PATH_OPS calls the trait's primitives through the public C ABI in
+//    exactly the order model.rs:103-148 does, on the reference's state layout
+//    (BATCH-token chunks, position-major f32 caches);
+//  - TH_PATH_FUSED runs the fused kernels on caches laid out per layer and per
+//    KV head ([layer][k|v][kv_head][max_len][head_dim], f32 or bf16), and is
+//    what a decode step captures into a HIP graph.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "common.h"
+#include "fused.h"
+
+namespace {
+
+constexpr size_t kBatch = 64;          // model/model.rs:8 BATCH (the ops path)
+constexpr size_t kFusedBatch = 512;    // tokens per chunk on the fused path
+constexpr size_t kWeightsPerLayer = 11;
+
+struct Layer {
+    const th_weight *attn_norm, *q, *k, *v, *o, *q_norm, *k_norm, *mlp_norm, *gate, *up, *down;
+};
+
+}  // namespace
+
+struct th_model {
+    th_device *dev = nullptr;
+    th_config c{};
+    std::vector<Layer> layers;
+    const th_weight *embed = nullptr, *norm = nullptr, *lm_head = nullptr;
+    const th_weight *out_proj() const { return lm_head ? lm_head : embed; }  // model.rs:147
+};
+
+struct th_state {
+    th_model *m = nullptr;
+    size_t max_len = 0;
+    int kv_dtype = TH_KV_F32;
+    int path = -1;  // the path that has filled the caches (-1: none yet)
+
+    // Shared by both paths.
+    th_buffer *rope = nullptr;    // model.rs:192-194
+    th_buffer *logits = nullptr;  // [vocab]
+
+    // TH_PATH_OPS: the reference's State buffers (model.rs:181-207).
+    th_buffer *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr,
+              *gate = nullptr, *up = nullptr;
+    std::vector<th_buffer *> k_cache, v_cache;
+
+    // TH_PATH_FUSED.
+    size_t fb = 0;  // token capacity of the fused buffers
+    float *fx = nullptr, *fxb = nullptr, *fq = nullptr, *fk = nullptr, *fv = nullptr, *fatt = nullptr,
+          *fgate = nullptr, *fup = nullptr, *fy = nullptr;
+    void *kv = nullptr;  // all caches, one allocation
+    size_t kv_elem = 4;
+    float *attn_part = nullptr;  // attention partials for the fused path
+    size_t attn_part_floats = 0;
+    uint64_t *argmax_part = nullptr;
+    th::StepState *step = nullptr;  // device
+    uint32_t *tokens_dev = nullptr;
+    size_t tokens_dev_cap = 0;
+    float *logits_dev = nullptr;  // decode logits kept for the caller
+    size_t logits_dev_cap = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+};
+
+namespace {
+
+using th::fail;
+
+void free_dev(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+// model/model.rs:239-250: (cos, sin) of pos * theta^(-2i/head_dim), pushed as [cos, sin].
+std::vector<float> rope_table(size_t max_len, size_t head_dim, float theta) {
+    size_t half = head_dim / 2;
+    std::vector<float> t;
+    t.reserve(max_len * head_dim);
+    for (size_t pos = 0; pos < max_len; ++pos) {
+        for (size_t i = 0; i < half; ++i) {
+            float freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+            float a = (float)pos * freq;
+            t.push_back(cosf(a));
+            t.push_back(sinf(a));
+        }
+    }
+    return t;
+}
+
+int check_shape(const th_weight *w, size_t r, size_t c, const char *what, size_t layer) {
+    if (!w) return fail(TH_ERR_INVALID, "layer %zu: missing %s", layer, what);
+    if (c == 0) {
+        if (w->numel != r) return fail(TH_ERR_INVALID, "layer %zu: %s has %zu elements, not %zu", layer, what, w->numel, r);
+        return TH_OK;
+    }
+    if (w->ndim != 2 || w->shape[0] != r || w->shape[1] != c)
+        return fail(TH_ERR_INVALID, "layer %zu: %s is not [%zu, %zu]", layer, what, r, c);
+    return TH_OK;
+}
+
+// Device pointer of the cache of (layer, k or v) on the fused path.
+void *cache_ptr(th_state *s, size_t layer, int which) {
+    const th_config &c = s->m->c;
+    size_t per = (size_t)c.num_key_value_heads * s->max_len * (size_t)c.head_dim;
+    return static_cast<char *>(s->kv) + ((layer * 2 + which) * per) * s->kv_elem;
+}
+
+int ensure_ops_state(th_state *s) {
+    if (s->x) return TH_OK;
+    th_model *m = s->m;
+    const th_config &c = m->c;
+    size_t qd = (size_t)(c.num_attention_heads * c.head_dim), kvd = (size_t)(c.num_key_value_heads * c.head_dim);
+    size_t widths[8] = {(size_t)c.hidden_size, (size_t)c.hidden_size, qd, kvd, kvd, qd, (size_t)c.intermediate_size,
+                        (size_t)c.intermediate_size};
+    th_buffer **bufs[8] = {&s->x, &s->xb, &s->q, &s->k, &s->v, &s->att, &s->gate, &s->up};
+    for (int i = 0; i < 8; ++i) {
+        int rc = th_alloc(m->dev, kBatch * widths[i], bufs[i]);
+        if (rc) return rc;
+    }
+    for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
+        th_buffer *kb = nullptr, *vb = nullptr;
+        int rc = th_alloc(m->dev, s->max_len * kvd, &kb);
+        if (rc) return rc;
+        s->k_cache.push_back(kb);
+        rc = th_alloc(m->dev, s->max_len * kvd, &vb);
+        if (rc) return rc;
+        s->v_cache.push_back(vb);
+    }
+    return TH_OK;
+}
+
+#define TRY(call)                 \
+    do {                          \
+        int rc_ = (call);         \
+        if (rc_ != TH_OK) return rc_; \
+    } while (0)
+
+// model/model.rs:93-149, one primitive per step, for n <= BATCH tokens.
+int forward_batch_ops(th_state *s, const uint32_t *tokens, size_t n, size_t pos) {
+    th_model *m = s->m;
+    th_device *d = m->dev;
+    const th_config &c = m->c;
+    const float eps = c.rms_norm_eps;
+    const size_t hd = (size_t)c.head_dim, H = (size_t)c.hidden_size;
+    const size_t kv_dim = (size_t)c.num_key_value_heads * hd;
+    size_t widths[8] = {H, H, (size_t)c.num_attention_heads * hd, kv_dim, kv_dim, (size_t)c.num_attention_heads * hd,
+                        (size_t)c.intermediate_size, (size_t)c.intermediate_size};
+    th_buffer *bufs[8] = {s->x, s->xb, s->q, s->k, s->v, s->att, s->gate, s->up};
+    for (int i = 0; i < 8; ++i) TRY(th_resize(d, bufs[i], n * widths[i]));  // State::batch
+
+    TRY(th_embed(d, s->x, m->embed, tokens, n));
+    for (size_t i = 0; i < m->layers.size(); ++i) {
+        const Layer &L = m->layers[i];
+        TRY(th_copy(d, s->xb, 0, s->x, 0, n * H));
+        TRY(th_rmsnorm(d, s->xb, L.attn_norm, eps));
+        TRY(th_matmul(d, s->q, L.q, s->xb));
+        TRY(th_matmul(d, s->k, L.k, s->xb));
+        TRY(th_matmul(d, s->v, L.v, s->xb));
+        if (L.q_norm) TRY(th_rmsnorm(d, s->q, L.q_norm, eps));
+        if (L.k_norm) TRY(th_rmsnorm(d, s->k, L.k_norm, eps));
+        TRY(th_rope(d, s->q, s->rope, pos, (size_t)c.num_attention_heads, hd));
+        TRY(th_rope(d, s->k, s->rope, pos, (size_t)c.num_key_value_heads, hd));
+        TRY(th_copy(d, s->k_cache[i], pos * kv_dim, s->k, 0, n * kv_dim));
+        TRY(th_copy(d, s->v_cache[i], pos * kv_dim, s->v, 0, n * kv_dim));
+        TRY(th_attention(d, s->att, s->q, s->k_cache[i], s->v_cache[i], pos, (size_t)c.num_attention_heads, hd,
+                         (size_t)c.num_key_value_heads));
+        TRY(th_matmul(d, s->xb, L.o, s->att));
+        TRY(th_add(d, s->x, s->xb));
+
+        TRY(th_copy(d, s->xb, 0, s->x, 0, n * H));
+        TRY(th_rmsnorm(d, s->xb, L.mlp_norm, eps));
+        TRY(th_matmul(d, s->gate, L.gate, s->xb));
+        TRY(th_matmul(d, s->up, L.up, s->xb));
+        TRY(th_silu_mul(d, s->gate, s->up));
+        TRY(th_matmul(d, s->xb, L.down, s->gate));
+        TRY(th_add(d, s->x, s->xb));
+    }
+    TRY(th_resize(d, s->xb, H));
+    TRY(th_copy(d, s->xb, 0, s->x, (n - 1) * H, H));
+    TRY(th_rmsnorm(d, s->xb, m->norm, eps));
+    TRY(th_matmul(d, s->logits, m->out_proj(), s->xb));
+    return TH_OK;
+}
+
+int ensure_fused_state(th_state *s) {
+    if (s->fx) return TH_OK;
+    th_model *m = s->m;
+    const th_config &c = m->c;
+    const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
+    const size_t qd = (size_t)c.num_attention_heads * hd, kvd = (size_t)c.num_key_value_heads * hd;
+    s->fb = std::min(kFusedBatch, s->max_len);
+    struct {
+        float **p;
+        size_t n;
+    } bufs[] = {{&s->fx, H}, {&s->fxb, H}, {&s->fq, qd}, {&s->fk, kvd}, {&s->fv, kvd},
+                {&s->fatt, qd}, {&s->fgate, I}, {&s->fup, I}, {&s->fy, H}};
+    for (auto &b : bufs) TH_HIP(hipMalloc(b.p, s->fb * b.n * sizeof(float)));
+    s->kv_elem = s->kv_dtype == TH_KV_BF16 ? 2 : 4;
+    size_t kv_bytes = (size_t)c.num_hidden_layers * 2 * kvd * s->max_len * s->kv_elem;
+    TH_HIP(hipMalloc(&s->kv, kv_bytes));
+    // Attention partials: enough for any chunk of up to fb tokens at any context
+    // up to max_len (the split count only grows with the context).
+    s->attn_part_floats = 0;
+    for (size_t n = 1; n <= s->fb; ++n) {
+        int ns = th::attention_splits(n, (size_t)c.num_key_value_heads, s->max_len);
+        s->attn_part_floats =
+            std::max(s->attn_part_floats, th::attention_scratch(n, (size_t)c.num_attention_heads, hd, ns));
+    }
+    if (s->attn_part_floats) TH_HIP(hipMalloc(&s->attn_part, s->attn_part_floats * sizeof(float)));
+    TH_HIP(hipMalloc(&s->argmax_part, th::argmax_partials((size_t)c.vocab_size) * sizeof(uint64_t)));
+    TH_HIP(hipMalloc(&s->step, sizeof(th::StepState)));
+    return TH_OK;
+}
+
+// Queues the fused forward of n tokens (n <= s->fb) at position pos, or at
+// *pos_dev when pos_dev is not null (a captured decode step). Token ids are
+// read from the device array `tokens`. Leaves the logits of the last token in
+// s->logits.
+int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, const long long *pos_dev) {
+    th_model *m = s->m;
+    th_device *d = m->dev;
+    hipStream_t st = d->stream;
+    const th_config &c = m->c;
+    const float eps = c.rms_norm_eps;
+    const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
+    const size_t nh = (size_t)c.num_attention_heads, nkv = (size_t)c.num_key_value_heads;
+    const size_t qd = nh * hd;
+    const int kv_bf16 = s->kv_dtype == TH_KV_BF16;
+    const size_t max_ctx = pos_dev ? s->max_len : pos + n;
+    const int nsplit = th::attention_splits(n, nkv, max_ctx);
+    if (th::attention_scratch(n, nh, hd, nsplit) > s->attn_part_floats)
+        return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
+
+    TH_HIP(th::launch_embed(st, s->fx, m->embed->ptr, H, tokens, n));
+    for (size_t i = 0; i < m->layers.size(); ++i) {
+        const Layer &L = m->layers[i];
+        // Residual add of the previous layer's MLP output, then the attention norm.
+        TH_HIP(th::launch_add_rmsnorm(st, s->fx, i ? s->fy : nullptr, s->fxb, n, L.attn_norm->ptr, H, eps));
+        TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
+        TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
+        TH_HIP(th::launch_matmul(st, s->fv, L.v->ptr, nkv * hd, H, s->fxb, n));
+        th::QkvPostArgs qa{};
+        qa.q = s->fq;
+        qa.k = s->fk;
+        qa.v = s->fv;
+        qa.q_norm = L.q_norm ? L.q_norm->ptr : nullptr;
+        qa.k_norm = L.k_norm ? L.k_norm->ptr : nullptr;
+        qa.rope = s->rope->ptr;
+        qa.k_cache = cache_ptr(s, i, 0);
+        qa.v_cache = cache_ptr(s, i, 1);
+        qa.head_stride = (long long)(s->max_len * hd);
+        qa.pos_stride = (long long)hd;
+        qa.pos = (long long)pos;
+        qa.pos_dev = pos_dev;
+        qa.n = (int)n;
+        qa.n_heads = (int)nh;
+        qa.n_kv_heads = (int)nkv;
+        qa.head_dim = (int)hd;
+        qa.kv_bf16 = kv_bf16;
+        qa.eps = eps;
+        TH_HIP(th::launch_qk_norm_rope_append(st, qa));
+
+        th::AttnKernelArgs aa{};
+        aa.out = s->fatt;
+        aa.q = s->fq;
+        aa.k = qa.k_cache;
+        aa.v = qa.v_cache;
+        aa.n_heads = (int)nh;
+        aa.n_kv_heads = (int)nkv;
+        aa.group = (int)(nh / nkv);
+        aa.pos = (long long)pos;
+        aa.pos_dev = pos_dev;
+        aa.pos_stride = (long long)hd;
+        aa.head_stride = (long long)(s->max_len * hd);
+        aa.nsplit = nsplit;
+        aa.kv_bf16 = kv_bf16;
+        aa.scale = 1.0f / sqrtf((float)hd);
+        aa.part_acc = s->attn_part;
+        aa.part_ml = s->attn_part ? s->attn_part + n * nh * (size_t)nsplit * hd : nullptr;
+        TH_HIP(th::launch_attention(st, aa, n, hd));
+
+        TH_HIP(th::launch_matmul(st, s->fy, L.o->ptr, H, qd, s->fatt, n));
+        TH_HIP(th::launch_add_rmsnorm(st, s->fx, s->fy, s->fxb, n, L.mlp_norm->ptr, H, eps));
+        TH_HIP(th::launch_matmul(st, s->fgate, L.gate->ptr, I, H, s->fxb, n));
+        TH_HIP(th::launch_matmul(st, s->fup, L.up->ptr, I, H, s->fxb, n));
+        TH_HIP(th::launch_silu_mul(st, s->fgate, s->fup, n * I));
+        TH_HIP(th::launch_matmul(st, s->fy, L.down->ptr, H, I, s->fgate, n));
+    }
+    // Only the last token's logits are wanted (model.rs:143-147).
+    float *xl = s->fx + (n - 1) * H;
+    TH_HIP(th::launch_add_rmsnorm(st, xl, s->fy + (n - 1) * H, s->fxb, 1, m->norm->ptr, H, eps));
+    TH_HIP(th::launch_matmul(st, s->logits->ptr, m->out_proj()->ptr, (size_t)c.vocab_size, H, s->fxb, 1));
+    return TH_OK;
+}
+
+int stage_state_tokens(th_state *s, const uint32_t *tokens, size_t n) {
+    th_model *m = s->m;
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] >= (uint32_t)m->c.vocab_size)
+            return fail(TH_ERR_INVALID, "token %u at index %zu is past the vocabulary of %lld", tokens[i], i,
+                        (long long)m->c.vocab_size);
+    if (n > s->tokens_dev_cap) {
+        TH_HIP(hipStreamSynchronize(m->dev->stream));
+        free_dev(s->tokens_dev);
+        s->tokens_dev = nullptr;
+        s->tokens_dev_cap = 0;
+        size_t cap = std::max<size_t>(n, 1024);
+        TH_HIP(hipMalloc(&s->tokens_dev, cap * sizeof(uint32_t)));
+        s->tokens_dev_cap = cap;
+    }
+    TH_HIP(hipMemcpyAsync(s->tokens_dev, tokens, n * sizeof(uint32_t), hipMemcpyHostToDevice, m->dev->stream));
+    return TH_OK;
+}
+
+int claim_path(th_state *s, int path) {
+    if (s->path != -1 && s->path != path)
+        return fail(TH_ERR_INVALID, "this state's caches were filled by the other path");
+    if (path == TH_PATH_OPS && s->kv_dtype != TH_KV_F32)
+        return fail(TH_ERR_INVALID, "the ops path keeps the reference's f32 caches");
+    s->path = path;
+    return TH_OK;
+}
+
+// Captures one decode step (n = 1, position and token from s->step) as a graph.
+int capture_step(th_state *s) {
+    if (s->graph_exec) return TH_OK;
+    th_model *m = s->m;
+    hipStream_t st = m->dev->stream;
+    const size_t vocab = (size_t)m->c.vocab_size;
+    TH_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const long long *pos_dev = &s->step->pos;
+    const uint32_t *tok_dev = &s->step->token;
+    int rc = enqueue_fused(s, tok_dev, 1, 0, pos_dev);
+    if (rc == TH_OK) {
+        hipError_t e = th::launch_keep_logits(st, s->logits->ptr, vocab, s->step);
+        if (e == hipSuccess) e = th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 1);
+        if (e != hipSuccess) rc = fail(TH_ERR_HIP, "capture: %s", hipGetErrorString(e));
+    }
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc != TH_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return fail(TH_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    s->graph = g;
+    TH_HIP(hipGraphInstantiate(&s->graph_exec, g, nullptr, nullptr, 0));
+    return TH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int th_model_create(th_device *dev, const th_config *config, const th_weight *const *weights, size_t n_weights,
+                    th_model **out) {
+    TH_REQUIRE(dev && config && weights && out, "th_model_create: null argument");
+    const th_config &c = *config;
+    TH_REQUIRE(c.hidden_size > 0 && c.intermediate_size > 0 && c.num_hidden_layers > 0 && c.num_attention_heads > 0 &&
+                   c.num_key_value_heads > 0 && c.head_dim > 0 && c.vocab_size > 0,
+               "config sizes must be positive");
+    TH_REQUIRE(c.num_attention_heads % c.num_key_value_heads == 0, "query heads must split into KV groups");
+    TH_REQUIRE(c.num_attention_heads / c.num_key_value_heads <= 8, "at most 8 query heads per KV head");
+    TH_REQUIRE(c.head_dim == 64 || c.head_dim == 128 || c.head_dim == 256, "head_dim must be 64, 128 or 256");
+    TH_REQUIRE(c.hidden_size % 8 == 0 && c.intermediate_size % 8 == 0, "hidden and MLP sizes must be multiples of 8");
+    size_t L = (size_t)c.num_hidden_layers;
+    TH_REQUIRE(n_weights == L * kWeightsPerLayer + 3, "expected %zu weights, got %zu", L * kWeightsPerLayer + 3,
+               n_weights);
+    const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
+    const size_t qd = (size_t)c.num_attention_heads * hd, kvd = (size_t)c.num_key_value_heads * hd;
+    auto *m = new (std::nothrow) th_model();
+    if (!m) return fail(TH_ERR_NOMEM, "out of host memory");
+    m->dev = dev;
+    m->c = c;
+    int rc = TH_OK;
+    for (size_t l = 0; l < L && rc == TH_OK; ++l) {
+        const th_weight *const *w = weights + l * kWeightsPerLayer;
+        Layer lay{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7], w[8], w[9], w[10]};
+        if (!rc) rc = check_shape(lay.attn_norm, H, 0, "input_layernorm", l);
+        if (!rc) rc = check_shape(lay.q, qd, H, "q_proj", l);
+        if (!rc) rc = check_shape(lay.k, kvd, H, "k_proj", l);
+        if (!rc) rc = check_shape(lay.v, kvd, H, "v_proj", l);
+        if (!rc) rc = check_shape(lay.o, H, qd, "o_proj", l);
+        if (!rc && lay.q_norm) rc = check_shape(lay.q_norm, hd, 0, "q_norm", l);
+        if (!rc && lay.k_norm) rc = check_shape(lay.k_norm, hd, 0, "k_norm", l);
+        if (!rc) rc = check_shape(lay.mlp_norm, H, 0, "post_attention_layernorm", l);
+        if (!rc) rc = check_shape(lay.gate, I, H, "gate_proj", l);
+        if (!rc) rc = check_shape(lay.up, I, H, "up_proj", l);
+        if (!rc) rc = check_shape(lay.down, H, I, "down_proj", l);
+        m->layers.push_back(lay);
+    }
+    const th_weight *const *tail = weights + L * kWeightsPerLayer;
+    m->embed = tail[0];
+    m->norm = tail[1];
+    m->lm_head = tail[2];
+    if (!rc) rc = check_shape(m->embed, (size_t)c.vocab_size, H, "embed_tokens", L);
+    if (!rc) rc = check_shape(m->norm, H, 0, "norm", L);
+    if (!rc && c.tie_word_embeddings && m->lm_head) rc = fail(TH_ERR_INVALID, "tied embeddings take no lm_head");
+    if (!rc && !c.tie_word_embeddings) rc = check_shape(m->lm_head, (size_t)c.vocab_size, H, "lm_head", L);
+    if (rc) {
+        delete m;
+        return rc;
+    }
+    *out = m;
+    return TH_OK;
+}
+
+void th_model_destroy(th_model *m) { delete m; }
+
+int th_state_create(th_model *m, size_t max_len, int kv_dtype, th_state **out) {
+    TH_REQUIRE(m && out, "th_state_create: null argument");
+    TH_REQUIRE(max_len > 0, "max_len must be positive");
+    TH_REQUIRE(kv_dtype == TH_KV_F32 || kv_dtype == TH_KV_BF16, "unknown KV dtype %d", kv_dtype);
+    auto *s = new (std::nothrow) th_state();
+    if (!s) return fail(TH_ERR_NOMEM, "out of host memory");
+    s->m = m;
+    s->max_len = max_len;
+    s->kv_dtype = kv_dtype;
+    std::vector<float> table = rope_table(max_len, (size_t)m->c.head_dim, m->c.rope_theta);
+    int rc = th_alloc(m->dev, table.size(), &s->rope);
+    if (!rc) rc = th_write(m->dev, s->rope, table.data(), table.size());
+    if (!rc) rc = th_alloc(m->dev, (size_t)m->c.vocab_size, &s->logits);
+    if (rc) {
+        th_state_destroy(s);
+        return rc;
+    }
+    *out = s;
+    return TH_OK;
+}
+
+void th_state_destroy(th_state *s) {
+    if (!s) return;
+    th_device *d = s->m->dev;
+    (void)hipStreamSynchronize(d->stream);
+    if (s->graph_exec) (void)hipGraphExecDestroy(s->graph_exec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    th_buffer *bufs[] = {s->rope, s->logits, s->x, s->xb, s->q, s->k, s->v, s->att, s->gate, s->up};
+    for (th_buffer *b : bufs) th_buffer_free(d, b);
+    for (th_buffer *b : s->k_cache) th_buffer_free(d, b);
+    for (th_buffer *b : s->v_cache) th_buffer_free(d, b);
+    void *ptrs[] = {s->fx,      s->fxb,        s->fq,   s->fk,         s->fv,         s->fatt,
+                    s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
+                    s->step,    s->tokens_dev, s->logits_dev};
+    for (void *p : ptrs) free_dev(p);
+    delete s;
+}
+
+int th_forward(th_model *m, th_state *s, const uint32_t *tokens, size_t n, size_t pos, float *logits, int path) {
+    TH_REQUIRE(m && s && s->m == m, "th_forward: null argument or a state of another model");
+    TH_REQUIRE(n > 0 && tokens, "no tokens to run");  // model.rs:84
+    TH_REQUIRE(pos + n <= s->max_len, "tokens past the end of the cache");  // model.rs:85
+    TH_REQUIRE(path == TH_PATH_OPS || path == TH_PATH_FUSED, "unknown path %d", path);
+    TRY(claim_path(s, path));
+    if (path == TH_PATH_OPS) {
+        TRY(ensure_ops_state(s));
+        for (size_t i = 0; i < n; i += kBatch) TRY(forward_batch_ops(s, tokens + i, std::min(kBatch, n - i), pos + i));
+    } else {
+        TRY(ensure_fused_state(s));
+        TRY(stage_state_tokens(s, tokens, n));
+        for (size_t i = 0; i < n; i += s->fb)
+            TRY(enqueue_fused(s, s->tokens_dev + i, std::min(s->fb, n - i), pos + i, nullptr));
+    }
+    if (logits) return th_read(m->dev, s->logits, logits, s->logits->len);
+    TH_HIP(hipStreamSynchronize(m->dev->stream));
+    return TH_OK;
+}
+
+int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tokens, float *out_logits) {
+    TH_REQUIRE(m && s && s->m == m && out_tokens, "th_decode: null argument or a state of another model");
+    TH_REQUIRE(s->path == TH_PATH_FUSED, "decode continues a fused-path forward; run th_forward first");
+    TH_REQUIRE(pos + steps <= s->max_len, "tokens past the end of the cache");
+    if (steps == 0) return TH_OK;
+    th_device *d = m->dev;
+    hipStream_t st = d->stream;
+    const size_t vocab = (size_t)m->c.vocab_size;
+    TRY(ensure_fused_state(s));
+    if (steps + 1 > s->tokens_dev_cap) {
+        TH_HIP(hipStreamSynchronize(st));
+        free_dev(s->tokens_dev);
+        s->tokens_dev = nullptr;
+        s->tokens_dev_cap = 0;
+        TH_HIP(hipMalloc(&s->tokens_dev, (steps + 1) * sizeof(uint32_t)));
+        s->tokens_dev_cap = steps + 1;
+    }
+    if (out_logits && steps * vocab > s->logits_dev_cap) {
+        TH_HIP(hipStreamSynchronize(st));
+        free_dev(s->logits_dev);
+        s->logits_dev = nullptr;
+        s->logits_dev_cap = 0;
+        TH_HIP(hipMalloc(&s->logits_dev, steps * vocab * sizeof(float)));
+        s->logits_dev_cap = steps * vocab;
+    }
+    th::StepState init{};
+    init.pos = (long long)pos;
+    init.step = 0;
+    init.tokens_out = s->tokens_dev;
+    init.logits_out = out_logits ? s->logits_dev : nullptr;
+    TH_HIP(hipMemcpyAsync(s->step, &init, sizeof init, hipMemcpyHostToDevice, st));
+    TH_HIP(hipStreamSynchronize(st));  // `init` is a stack temporary
+    TRY(capture_step(s));
+    // The first pick comes from the logits the last forward left.
+    TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0));
+    for (size_t i = 0; i < steps; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
+    TH_HIP(hipMemcpyAsync(out_tokens, s->tokens_dev, steps * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    if (out_logits)
+        TH_HIP(hipMemcpyAsync(out_logits, s->logits_dev, steps * vocab * sizeof(float), hipMemcpyDeviceToHost, st));
+    TH_HIP(hipStreamSynchronize(st));
+    return TH_OK;
+}
+
+}  // extern "C"
