@@ -9,6 +9,8 @@ error is ~1e-5, so on these seeds the streams must match exactly.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -111,4 +113,38 @@ def test_qwen06_ops_path_logits(qwen06):
     got = m.forward(st, prompt, 0, TH_PATH_OPS)
     exp = r.forward(r.state(32), prompt, 0)
     assert float(np.max(np.abs(got - exp))) <= LOGIT_TOL
+    st.close()
+
+
+@pytest.fixture
+def decode_mode(request):
+    """Selects the decode implementation for states created in the test."""
+    old = os.environ.get("TITANIA_DECODE")
+    os.environ["TITANIA_DECODE"] = request.param
+    yield request.param
+    if old is None:
+        del os.environ["TITANIA_DECODE"]
+    else:
+        os.environ["TITANIA_DECODE"] = old
+
+
+@pytest.mark.parametrize("decode_mode", ["persistent", "graph"], indirect=True)
+@pytest.mark.parametrize("prompt_len,steps,kv", [(9, 24, TH_KV_F32), (300, 20, TH_KV_F32), (300, 12, TH_KV_BF16)])
+def test_tiny_decode_modes(tiny, decode_mode, prompt_len, steps, kv):
+    """Both decode implementations against the oracle, on one split of the
+    context and (past 256 positions) several splits merged on the device."""
+    m, r = tiny
+    c = QWEN3_TINY
+    prompt = synth.prompt(prompt_len, c.vocab_size, seed=prompt_len)
+    st = State(m, prompt_len + steps + 3, kv)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    toks, logits = m.decode(st, prompt_len, steps, keep_logits=True)
+    rtoks, gaps, last = r.generate(r.state(prompt_len + steps + 3), prompt, steps)
+    tol = 1e-4 if kv == TH_KV_F32 else LOGIT_TOL
+    assert float(np.std(last)) > 0.05
+    assert float(np.max(np.abs(logits[-1] - last))) <= tol
+    assert list(toks) == list(rtoks) or np.min(gaps) < tol
+    # A second call continues from where the first stopped.
+    more = m.decode(st, prompt_len + steps, 3)
+    assert len(more) == 3
     st.close()

@@ -82,6 +82,7 @@ SIGNATURES: dict[str, tuple] = {
     "th_state_destroy": (None, [_P]),
     "th_forward": (_I, [_P, _P, _P, _SZ, _SZ, _P, _I]),
     "th_decode": (_I, [_P, _P, _SZ, _SZ, _P, _P]),
+    "th_decode_trace": (_I, [_P, _P, _SZ, C.POINTER(_SZ)]),
 }
 
 _lib: C.CDLL | None = None

@@ -58,6 +58,6 @@ QWEN3_4B = Config(
 
 # A small model of the same family for quick end-to-end checks.
 QWEN3_TINY = Config(
-    hidden_size=256, intermediate_size=768, num_hidden_layers=2, num_attention_heads=4,
-    num_key_value_heads=2, vocab_size=1000, head_dim_=64,
+    hidden_size=512, intermediate_size=1536, num_hidden_layers=2, num_attention_heads=4,
+    num_key_value_heads=2, vocab_size=1000, head_dim_=128,
 )

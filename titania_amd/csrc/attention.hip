@@ -219,6 +219,12 @@ size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit) 
     return n * n_heads * (size_t)nsplit * (head_dim + 2);
 }
 
+hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,
+                               int nsplit, int hd) {
+    attn_combine_kernel<<<dim3((unsigned)heads), dim3(hd), 0, s>>>(out, part_acc, part_ml, nsplit, hd);
+    return hipGetLastError();
+}
+
 template <int HD>
 static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
     dim3 grid((unsigned)(n * (size_t)k.n_kv_heads * (size_t)k.nsplit));

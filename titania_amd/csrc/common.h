@@ -110,5 +110,8 @@ int attention_splits(size_t n, size_t n_kv_heads, size_t max_len);
 // Scratch floats the partials of `nsplit` splits take (0 for one split).
 size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit);
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim);
+// Merges attention partials of `heads` (token, head) pairs into out.
+hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,
+                               int nsplit, int hd);
 
 }  // namespace th

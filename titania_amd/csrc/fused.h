@@ -44,6 +44,8 @@ struct StepState {
 // `advance`, pos and step move on first.
 hipError_t launch_pick(hipStream_t s, const float *logits, size_t vocab, uint64_t *partials, StepState *st,
                        int advance);
+// The pick from per-block (key, inverted index) maxima already reduced by a kernel.
+hipError_t launch_pick_partials(hipStream_t s, const uint64_t *partials, size_t m, StepState *st, int advance);
 hipError_t launch_keep_logits(hipStream_t s, const float *logits, size_t vocab, const StepState *st);
 
 __device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }

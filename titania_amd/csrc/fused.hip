@@ -107,16 +107,24 @@ hipError_t launch_qk_norm_rope_append(hipStream_t s, const QkvPostArgs &a) {
 // Greedy pick of the decode loop: reduces the argmax partials, records the
 // token as the step's pick and as the next token to feed, and advances the
 // position when `advance` is set (after a token has been fed).
-__global__ __launch_bounds__(256) void pick_kernel(const uint64_t *__restrict__ partials, size_t m, StepState *st,
+__global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__ partials, size_t m, StepState *st,
                                                    int advance) {
-    __shared__ uint64_t red[4];
+    __shared__ uint64_t red[16];
     uint64_t best = 0;
-    for (size_t i = threadIdx.x; i < m; i += 256) best = max_u64(best, partials[i]);
+    // Eight loads in flight per thread per round.
+    for (size_t i0 = threadIdx.x; i0 < m; i0 += 8 * 1024) {
+        uint64_t v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = i0 + k * 1024 < m ? partials[i0 + k * 1024] : 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) best = max_u64(best, v[k]);
+    }
     best = wave_max_u64(best);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint64_t b = max_u64(max_u64(red[0], red[1]), max_u64(red[2], red[3]));
+        uint64_t b = 0;
+        for (int w = 0; w < 16; ++w) b = max_u64(b, red[w]);
         uint32_t tok = argmax_index(b);
         if (advance) {
             st->pos += 1;
@@ -141,7 +149,12 @@ hipError_t launch_pick(hipStream_t s, const float *logits, size_t vocab, uint64_
     size_t m = argmax_partials(vocab);
     hipError_t e = launch_argmax_partials(s, logits, vocab, partials);
     if (e != hipSuccess) return e;
-    pick_kernel<<<1, 256, 0, s>>>(partials, m, st, advance);
+    pick_kernel<<<1, 1024, 0, s>>>(partials, m, st, advance);
+    return hipGetLastError();
+}
+
+hipError_t launch_pick_partials(hipStream_t s, const uint64_t *partials, size_t m, StepState *st, int advance) {
+    pick_kernel<<<1, 1024, 0, s>>>(partials, m, st, advance);
     return hipGetLastError();
 }
 

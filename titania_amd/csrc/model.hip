@@ -14,8 +14,12 @@
 #include <new>
 #include <vector>
 
+#include <cstdlib>
+
 #include "common.h"
+#include "decode.h"
 #include "fused.h"
+#include "step.h"
 
 namespace {
 
@@ -68,6 +72,27 @@ struct th_state {
     size_t logits_dev_cap = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+
+    // The persistent decode kernel (when the shape allows it).
+    bool persistent = false;
+    int blocks = 0;
+    th::LayerWeights *dev_layers = nullptr;
+    unsigned long long *xchg = nullptr;  // all exchange buffers, one allocation
+    unsigned long long *xchg_x = nullptr, *xchg_qkv = nullptr, *xchg_att = nullptr, *xchg_h = nullptr,
+                       *xchg_am = nullptr;
+    float *att_part = nullptr;
+    unsigned *att_count = nullptr;
+    unsigned *status = nullptr;
+    unsigned epoch_base = 0;
+    int chunk = 256, n_splits = 1;
+    // The captured decode step's buffers (fixed addresses for the graph).
+    bool step_fused = false;
+    float *sx_a = nullptr, *sx_b = nullptr, *s_y = nullptr, *s_qkv = nullptr, *s_att = nullptr, *s_o = nullptr,
+          *s_h = nullptr;
+    uint64_t *s_part = nullptr;
+    unsigned long long *trace = nullptr;  // per-phase ticks of the last decode (TITANIA_TRACE steps)
+    int trace_steps = 0;
+    size_t trace_words = 0;
 };
 
 namespace {
@@ -189,6 +214,56 @@ int forward_batch_ops(th_state *s, const uint32_t *tokens, size_t n, size_t pos)
     return TH_OK;
 }
 
+// Resources of the persistent decode kernel: the layer table, the exchange
+// buffers (zeroed: epoch 0 precedes every epoch used), attention partials and
+// counters. Decode runs as a captured graph of step kernels unless
+// TITANIA_DECODE=persistent selects this kernel.
+int ensure_persistent(th_state *s) {
+    th_model *m = s->m;
+    const th_config &c = m->c;
+    const char *mode = getenv("TITANIA_DECODE");
+    s->blocks = th::decode_blocks(m->dev->ordinal);
+    s->persistent = mode && strcmp(mode, "persistent") == 0 &&
+                    th::decode_supported((int)c.hidden_size, (int)c.intermediate_size, (int)c.num_attention_heads,
+                                         (int)c.num_key_value_heads, (int)c.head_dim, (int)c.vocab_size, s->blocks);
+    if (!s->persistent) return TH_OK;
+    std::vector<th::LayerWeights> lw;
+    for (const Layer &L : m->layers)
+        lw.push_back({L.attn_norm->ptr, L.q->ptr, L.k->ptr, L.v->ptr, L.o->ptr, L.q_norm ? L.q_norm->ptr : nullptr,
+                      L.k_norm ? L.k_norm->ptr : nullptr, L.mlp_norm->ptr, L.gate->ptr, L.up->ptr, L.down->ptr});
+    TH_HIP(hipMalloc(&s->dev_layers, lw.size() * sizeof(th::LayerWeights)));
+    TH_HIP(hipMemcpy(s->dev_layers, lw.data(), lw.size() * sizeof(th::LayerWeights), hipMemcpyHostToDevice));
+    const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
+    const size_t qd = (size_t)c.num_attention_heads * hd, kvd = (size_t)c.num_key_value_heads * hd;
+    const size_t R = th::kReplicas;
+    const size_t nx = R * H, nqkv = qd + 2 * kvd, natt = R * qd, nh = R * I, nam = R * 2 * (size_t)s->blocks;
+    const size_t total = nx + nqkv + natt + nh + nam;
+    TH_HIP(hipMalloc(&s->xchg, total * sizeof(unsigned long long)));
+    TH_HIP(hipMemset(s->xchg, 0, total * sizeof(unsigned long long)));
+    s->xchg_x = s->xchg;
+    s->xchg_qkv = s->xchg_x + nx;
+    s->xchg_att = s->xchg_qkv + nqkv;
+    s->xchg_h = s->xchg_att + natt;
+    s->xchg_am = s->xchg_h + nh;
+    s->chunk = 256;
+    s->n_splits = (int)((s->max_len + s->chunk - 1) / s->chunk);
+    TH_HIP(hipMalloc(&s->att_part, (size_t)c.num_attention_heads * s->n_splits * (hd + 2) * sizeof(float)));
+    const size_t ncount = (size_t)c.num_hidden_layers * (size_t)c.num_key_value_heads;
+    TH_HIP(hipMalloc(&s->att_count, ncount * sizeof(unsigned)));
+    TH_HIP(hipMemset(s->att_count, 0, ncount * sizeof(unsigned)));
+    TH_HIP(hipMalloc(&s->status, 64));
+    TH_HIP(hipMemset(s->status, 0, 64));
+    s->epoch_base = 0;
+    const char *tr = getenv("TITANIA_TRACE");
+    s->trace_steps = tr ? std::max(0, atoi(tr)) : 0;
+    if (s->trace_steps) {
+        s->trace_words = th::decode_trace_words((int)c.num_hidden_layers, s->trace_steps);
+        TH_HIP(hipMalloc(&s->trace, s->trace_words * sizeof(unsigned long long)));
+        TH_HIP(hipMemset(s->trace, 0, s->trace_words * sizeof(unsigned long long)));
+    }
+    return TH_OK;
+}
+
 int ensure_fused_state(th_state *s) {
     if (s->fx) return TH_OK;
     th_model *m = s->m;
@@ -216,6 +291,81 @@ int ensure_fused_state(th_state *s) {
     if (s->attn_part_floats) TH_HIP(hipMalloc(&s->attn_part, s->attn_part_floats * sizeof(float)));
     TH_HIP(hipMalloc(&s->argmax_part, th::argmax_partials((size_t)c.vocab_size) * sizeof(uint64_t)));
     TH_HIP(hipMalloc(&s->step, sizeof(th::StepState)));
+    s->step_fused = th::step_supported((int)H, (int)I, (int)c.num_attention_heads, (int)c.num_key_value_heads,
+                                       (int)hd);
+    if (s->step_fused) {
+        struct {
+            float **p;
+            size_t n;
+        } sb[] = {{&s->sx_a, H}, {&s->sx_b, H}, {&s->s_y, H}, {&s->s_qkv, qd + 2 * kvd}, {&s->s_att, qd},
+                  {&s->s_o, H}, {&s->s_h, I}};
+        for (auto &b : sb) TH_HIP(hipMalloc(b.p, b.n * sizeof(float)));
+        TH_HIP(hipMalloc(&s->s_part, (size_t)th::step_logits_partials((int)c.vocab_size) * sizeof(uint64_t)));
+    }
+    return ensure_persistent(s);
+}
+
+// Queues one decode step with the fused step kernels: the token and position
+// come from s->step, the picked token goes back there.
+int enqueue_step(th_state *s) {
+    th_model *m = s->m;
+    hipStream_t st = m->dev->stream;
+    const th_config &c = m->c;
+    const int H = (int)c.hidden_size, I = (int)c.intermediate_size, hd = (int)c.head_dim;
+    const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads;
+    const int qd = nh * hd, kvd = nkv * hd, V = (int)c.vocab_size;
+    const float eps = c.rms_norm_eps;
+    const int nsplit = th::attention_splits(1, (size_t)nkv, s->max_len);
+    if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
+        return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
+    TH_HIP(th::launch_embed(st, s->sx_b, m->embed->ptr, (size_t)H, &s->step->token, 1));
+    const float *y_prev = nullptr;
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+        const Layer &L = m->layers[l];
+        th::StepQkvArgs q{};
+        q.wq = L.q->ptr;
+        q.wk = L.k->ptr;
+        q.wv = L.v->ptr;
+        q.q_rows = qd;
+        q.kv_rows = kvd;
+        q.hidden = H;
+        q.x_prev = s->sx_b;
+        q.y_prev = y_prev;
+        q.gain = L.attn_norm->ptr;
+        q.eps = eps;
+        q.x_out = s->sx_a;
+        q.qkv = s->s_qkv;
+        TH_HIP(th::launch_step_qkv(st, q));
+        th::StepAttnArgs a{};
+        a.qkv = s->s_qkv;
+        a.q_norm = L.q_norm ? L.q_norm->ptr : nullptr;
+        a.k_norm = L.k_norm ? L.k_norm->ptr : nullptr;
+        a.rope = s->rope->ptr;
+        a.k_cache = cache_ptr(s, l, 0);
+        a.v_cache = cache_ptr(s, l, 1);
+        a.head_stride = (long long)(s->max_len * hd);
+        a.pos = &s->step->pos;
+        a.n_heads = nh;
+        a.n_kv_heads = nkv;
+        a.nsplit = nsplit;
+        a.kv_bf16 = s->kv_dtype == TH_KV_BF16;
+        a.eps = eps;
+        a.out = s->s_att;
+        a.part_acc = s->attn_part;
+        a.part_ml = s->attn_part ? s->attn_part + (size_t)nh * nsplit * hd : nullptr;
+        TH_HIP(th::launch_step_attention(st, a));
+        if (nsplit > 1) TH_HIP(th::launch_attn_combine(st, s->s_att, a.part_acc, a.part_ml, (size_t)nh, nsplit, hd));
+        TH_HIP(th::launch_step_gemv(st, L.o->ptr, H, qd, s->s_att, s->s_o));
+        TH_HIP(th::launch_step_gate_up(st, L.gate->ptr, L.up->ptr, I, H, s->sx_a, s->s_o, L.mlp_norm->ptr, eps,
+                                       s->sx_b, s->s_h));
+        TH_HIP(th::launch_step_gemv(st, L.down->ptr, H, I, s->s_h, s->s_y));
+        y_prev = s->s_y;
+    }
+    int np = 0;
+    TH_HIP(th::launch_step_logits(st, m->out_proj()->ptr, V, H, s->sx_b, y_prev, m->norm->ptr, eps,
+                                  s->logits->ptr, s->s_part, &np));
+    TH_HIP(th::launch_keep_logits(st, s->logits->ptr, (size_t)V, s->step));
+    TH_HIP(th::launch_pick_partials(st, s->s_part, (size_t)np, s->step, 1));
     return TH_OK;
 }
 
@@ -335,13 +485,18 @@ int capture_step(th_state *s) {
     hipStream_t st = m->dev->stream;
     const size_t vocab = (size_t)m->c.vocab_size;
     TH_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    const long long *pos_dev = &s->step->pos;
-    const uint32_t *tok_dev = &s->step->token;
-    int rc = enqueue_fused(s, tok_dev, 1, 0, pos_dev);
-    if (rc == TH_OK) {
-        hipError_t e = th::launch_keep_logits(st, s->logits->ptr, vocab, s->step);
-        if (e == hipSuccess) e = th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 1);
-        if (e != hipSuccess) rc = fail(TH_ERR_HIP, "capture: %s", hipGetErrorString(e));
+    int rc;
+    if (s->step_fused) {
+        rc = enqueue_step(s);
+    } else {
+        const long long *pos_dev = &s->step->pos;
+        const uint32_t *tok_dev = &s->step->token;
+        rc = enqueue_fused(s, tok_dev, 1, 0, pos_dev);
+        if (rc == TH_OK) {
+            hipError_t e = th::launch_keep_logits(st, s->logits->ptr, vocab, s->step);
+            if (e == hipSuccess) e = th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 1);
+            if (e != hipSuccess) rc = fail(TH_ERR_HIP, "capture: %s", hipGetErrorString(e));
+        }
     }
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(st, &g);
@@ -352,6 +507,59 @@ int capture_step(th_state *s) {
     if (e != hipSuccess) return fail(TH_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
     s->graph = g;
     TH_HIP(hipGraphInstantiate(&s->graph_exec, g, nullptr, nullptr, 0));
+    return TH_OK;
+}
+
+// All `steps` decode steps in one launch of the persistent kernel; the first
+// pick (from the logits the last forward left) runs just before it.
+int decode_persistent(th_state *s, size_t steps) {
+    th_model *m = s->m;
+    const th_config &c = m->c;
+    hipStream_t st = m->dev->stream;
+    TH_HIP(th::launch_pick(st, s->logits->ptr, (size_t)c.vocab_size, s->argmax_part, s->step, 0));
+    TH_HIP(hipMemsetAsync(s->status, 0, 64, st));
+    th::DecodeParams p{};
+    p.layers = s->dev_layers;
+    p.embed = m->embed->ptr;
+    p.norm = m->norm->ptr;
+    p.lm_head = m->out_proj()->ptr;
+    p.rope = s->rope->ptr;
+    p.kv = s->kv;
+    p.kv_bf16 = s->kv_dtype == TH_KV_BF16;
+    p.logits = s->logits->ptr;
+    p.step = s->step;
+    p.xchg_x = s->xchg_x;
+    p.xchg_qkv = s->xchg_qkv;
+    p.xchg_att = s->xchg_att;
+    p.xchg_h = s->xchg_h;
+    p.xchg_am = s->xchg_am;
+    p.att_part = s->att_part;
+    p.att_count = s->att_count;
+    p.status = s->status;
+    p.epoch_base = s->epoch_base;
+    p.steps = (int)steps;
+    p.hidden = (int)c.hidden_size;
+    p.intermediate = (int)c.intermediate_size;
+    p.n_layers = (int)c.num_hidden_layers;
+    p.n_heads = (int)c.num_attention_heads;
+    p.n_kv_heads = (int)c.num_key_value_heads;
+    p.head_dim = (int)c.head_dim;
+    p.vocab = (int)c.vocab_size;
+    p.max_len = (int)s->max_len;
+    p.chunk = s->chunk;
+    p.n_splits = s->n_splits;
+    p.eps = c.rms_norm_eps;
+    p.timeout_ticks = 200000000LL;  // 2 s at the 100 MHz reference clock
+    p.trace = s->trace;
+    p.trace_steps = s->trace_steps;
+    TH_HIP(th::launch_decode(st, p, s->blocks));
+    s->epoch_base += (unsigned)steps * th::decode_epochs_per_step((int)c.num_hidden_layers);
+    unsigned status[2] = {0, 0};
+    TH_HIP(hipMemcpyAsync(status, s->status, sizeof status, hipMemcpyDeviceToHost, st));
+    TH_HIP(hipStreamSynchronize(st));
+    if (status[0] || status[1])
+        return fail(TH_ERR_HIP, "persistent decode stopped: %u timeouts/aborts, %u protocol errors", status[0],
+                    status[1]);
     return TH_OK;
 }
 
@@ -447,7 +655,9 @@ void th_state_destroy(th_state *s) {
     for (th_buffer *b : s->v_cache) th_buffer_free(d, b);
     void *ptrs[] = {s->fx,      s->fxb,        s->fq,   s->fk,         s->fv,         s->fatt,
                     s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
-                    s->step,    s->tokens_dev, s->logits_dev};
+                    s->step,    s->tokens_dev, s->logits_dev, s->dev_layers, s->xchg, s->att_part,
+                    s->att_count, s->status, s->trace, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
+                    s->s_att, s->s_o, s->s_h, s->s_part};
     for (void *p : ptrs) free_dev(p);
     delete s;
 }
@@ -469,6 +679,15 @@ int th_forward(th_model *m, th_state *s, const uint32_t *tokens, size_t n, size_
     }
     if (logits) return th_read(m->dev, s->logits, logits, s->logits->len);
     TH_HIP(hipStreamSynchronize(m->dev->stream));
+    return TH_OK;
+}
+
+int th_decode_trace(th_state *s, uint64_t *out, size_t cap, size_t *n) {
+    TH_REQUIRE(s && n, "th_decode_trace: null argument");
+    *n = s->trace ? s->trace_words : 0;
+    if (!s->trace || !out) return TH_OK;
+    TH_REQUIRE(cap >= s->trace_words, "trace needs %zu words", s->trace_words);
+    TH_HIP(hipMemcpy(out, s->trace, s->trace_words * sizeof(uint64_t), hipMemcpyDeviceToHost));
     return TH_OK;
 }
 
@@ -504,10 +723,20 @@ int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_
     init.logits_out = out_logits ? s->logits_dev : nullptr;
     TH_HIP(hipMemcpyAsync(s->step, &init, sizeof init, hipMemcpyHostToDevice, st));
     TH_HIP(hipStreamSynchronize(st));  // `init` is a stack temporary
-    TRY(capture_step(s));
-    // The first pick comes from the logits the last forward left.
-    TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0));
-    for (size_t i = 0; i < steps; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
+    const char *mode = getenv("TITANIA_DECODE");
+    if (s->persistent) {
+        TRY(decode_persistent(s, steps));
+    } else if (mode && strcmp(mode, "eager") == 0 && s->step_fused) {
+        // The same step kernels launched one by one (no graph): for profilers
+        // that do not follow graph launches.
+        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0));
+        for (size_t i = 0; i < steps; ++i) TRY(enqueue_step(s));
+    } else {
+        TRY(capture_step(s));
+        // The first pick comes from the logits the last forward left.
+        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0));
+        for (size_t i = 0; i < steps; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
+    }
     TH_HIP(hipMemcpyAsync(out_tokens, s->tokens_dev, steps * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     if (out_logits)
         TH_HIP(hipMemcpyAsync(out_logits, s->logits_dev, steps * vocab * sizeof(float), hipMemcpyDeviceToHost, st));

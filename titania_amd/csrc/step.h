@@ -1,0 +1,74 @@
+// Fused kernels of one greedy decode step (batch 1), for graph capture.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "device_util.h"
+#include "fused.h"
+
+namespace th {
+
+// Whether the step kernels support this shape (head_dim 128, rows of whole
+// 512-column spans).
+bool step_supported(int hidden, int intermediate, int n_heads, int n_kv_heads, int head_dim);
+
+struct StepQkvArgs {
+    const uint16_t *wq, *wk, *wv;
+    int q_rows, kv_rows, hidden;
+    const float *x_prev, *y_prev;  // residual input: x_prev (+ y_prev)
+    const uint16_t *gain;
+    float eps;
+    float *x_out;  // x_prev + y_prev
+    float *qkv;    // [q rows][k rows][v rows]
+};
+
+// x_out = x_prev + y_prev; qkv = [Wq; Wk; Wv] . rmsnorm(x_out).
+hipError_t launch_step_qkv(hipStream_t s, const StepQkvArgs &a);
+
+// out = W . x for W [rows, cols].
+hipError_t launch_step_gemv(hipStream_t s, const uint16_t *w, int rows, int cols, const float *x, float *out);
+
+// x_out = x1 + o; h[j] = silu(gate_j . n) * (up_j . n) with n = rmsnorm(x_out).
+hipError_t launch_step_gate_up(hipStream_t s, const uint16_t *gate, const uint16_t *up, int inter, int hidden,
+                               const float *x1, const float *o, const uint16_t *gain, float eps, float *x_out,
+                               float *h);
+
+// logits = W . rmsnorm(x + y), and per-block argmax partials.
+hipError_t launch_step_logits(hipStream_t s, const uint16_t *w, int vocab, int hidden, const float *x,
+                              const float *y, const uint16_t *gain, float eps, float *logits, uint64_t *partials,
+                              int *n_partials);
+int step_logits_partials(int vocab);
+
+struct StepAttnArgs {
+    const float *qkv;  // raw q, k, v rows of the step (the q/k/v GEMV's output)
+    const uint16_t *q_norm, *k_norm;  // or null
+    const float *rope;                // [max_len][head_dim/2][cos, sin]
+    void *k_cache, *v_cache;          // the layer's caches, [kv_head][max_len][head_dim]
+    long long head_stride;            // max_len * head_dim
+    const long long *pos;             // the step's position (device)
+    int n_heads, n_kv_heads;
+    int nsplit;
+    int kv_bf16;
+    float eps;
+    float *out;       // [n_heads][head_dim] when nsplit == 1
+    float *part_acc;  // [n_heads][nsplit][head_dim] otherwise
+    float *part_ml;   // [n_heads][nsplit][2]
+};
+
+hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a);
+
+__device__ __forceinline__ void kv_load8(const float *p, float f[8]) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ void kv_load8(const uint16_t *p, float f[8]) {
+    unpack8(*reinterpret_cast<const uint4 *>(p), f);
+}
+__device__ __forceinline__ float kv_load1(const float *p) { return *p; }
+__device__ __forceinline__ float kv_load1(const uint16_t *p) { return bf16_to_f32(*p); }
+
+}  // namespace th

@@ -1,0 +1,547 @@
+// Fused kernels of one greedy decode step (one token, batch 1), five per layer,
+// captured once into a HIP graph and replayed at every position.
+//
+//   1 x = x_prev (+ y_prev) in every block, RMSNorm, q/k/v GEMV rows
+//   2 per KV head: q/k RMSNorm, RoPE, KV append, attention over the cache
+//   3 o GEMV rows (+ merge of attention splits)
+//   4 x = x1 + o in every block, RMSNorm, gate and up rows, SiLU * up
+//   5 down GEMV rows
+// then the final RMSNorm with the output projection and a per-block argmax,
+// and the pick. The residual stream is never updated in place: each kernel
+// that adds to it reads one buffer and writes another, so every block can
+// recompute the sum it needs.
+//
+// The GEMVs are HBM-bound: each block issues the 16-byte loads of all its
+// weight rows first (they do not depend on the activations), then builds the
+// normalized input in LDS while those loads are in flight, then reduces one
+// row per wave with DPP.
+#include "common.h"
+#include "device_util.h"
+#include "step.h"
+
+namespace th {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+// Builds the block's f32 input in LDS: x = a (+ b), optionally RMSNorm'd with
+// gain g (model/cpu.rs:85-94); block 0 keeps the un-normalized sum in x_out.
+// Every thread issues all its loads (NV float4 of a, of b
+// and 4-element groups of g) before using any, so the input costs one memory
+// round trip rather than one per loop iteration.
+template <bool NORM, int NV>
+__device__ __forceinline__ void build_input(float *xs, const float *a, const float *b, int n, const uint16_t *g,
+                                            float eps, float *x_out, float *red) {
+    const int tid = threadIdx.x;
+    const int n4 = n >> 2;
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    const float4 *b4 = reinterpret_cast<const float4 *>(b);
+    const uint2 *g4 = reinterpret_cast<const uint2 *>(g);
+    float4 va[NV], vb[NV];
+    uint2 vg[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = tid + k * kThreads;
+        if (i < n4) {
+            va[k] = a4[i];
+            if (b) vb[k] = b4[i];
+            if (NORM) vg[k] = g4[i];
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = tid + k * kThreads;
+        if (i < n4) {
+            float4 v = va[k];
+            if (b) {
+                v.x = v.x + vb[k].x;
+                v.y = v.y + vb[k].y;
+                v.z = v.z + vb[k].z;
+                v.w = v.w + vb[k].w;
+            }
+            va[k] = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            if (!NORM) reinterpret_cast<float4 *>(xs)[i] = v;
+        }
+    }
+    if (x_out && blockIdx.x == 0) {  // every block holds the sum; the first keeps it
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < n4) reinterpret_cast<float4 *>(x_out)[i] = va[k];
+        }
+    }
+    if (!NORM) {
+        __syncthreads();
+        return;
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float total = 0.f;
+    for (int w = 0; w < kWaves; ++w) total += red[w];
+    const float scale = 1.0f / sqrtf(total / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = tid + k * kThreads;
+        if (i < n4) {
+            float4 v = va[k];
+            v.x = v.x * (scale * bf16_lo(vg[k].x));
+            v.y = v.y * (scale * bf16_hi(vg[k].x));
+            v.z = v.z * (scale * bf16_lo(vg[k].y));
+            v.w = v.w * (scale * bf16_hi(vg[k].y));
+            reinterpret_cast<float4 *>(xs)[i] = v;
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ float dot8(const float *xs, const uint4 &w, int col, float acc) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs) + col * 2;
+    const float4 a = x4[0], b = x4[1];
+    float wf[8];
+    unpack8(w, wf);
+    acc = fmaf(wf[0], a.x, acc);
+    acc = fmaf(wf[1], a.y, acc);
+    acc = fmaf(wf[2], a.z, acc);
+    acc = fmaf(wf[3], a.w, acc);
+    acc = fmaf(wf[4], b.x, acc);
+    acc = fmaf(wf[5], b.y, acc);
+    acc = fmaf(wf[6], b.z, acc);
+    acc = fmaf(wf[7], b.w, acc);
+    return acc;
+}
+
+// Rows of a GEMV: up to three runs of consecutive rows of row-major matrices
+// with `cols` columns, concatenated.
+struct Rows {
+    const uint16_t *base[3];
+    int count[3];
+};
+
+__device__ __forceinline__ const uint4 *row_at(const Rows &m, int r, int cols) {
+    const uint16_t *p;
+    if (r < m.count[0]) p = m.base[0] + (size_t)r * cols;
+    else if (r < m.count[0] + m.count[1]) p = m.base[1] + (size_t)(r - m.count[0]) * cols;
+    else p = m.base[2] + (size_t)(r - m.count[0] - m.count[1]) * cols;
+    return reinterpret_cast<const uint4 *>(p);
+}
+
+enum Prologue { kNormSum, kPlain };
+enum Epilogue { kStore, kSiluPairs, kLogits };
+
+struct GemvArgs {
+    Rows rows;
+    int n_rows;            // total rows
+    int cols;
+    const float *a, *b;    // input = a (+ b)
+    const uint16_t *gain;  // RMSNorm gains (kNormSum)
+    float eps;
+    float *x_out;          // where the summed input is kept (kNormSum), or null
+    float *out;            // kStore: out[r]; kSiluPairs: out[j] for rows (j, j + n_rows/2); kLogits: logits
+    uint64_t *argmax;      // kLogits: per-block (key, inverted index) maxima
+};
+
+// One block: RPW rows per wave, CPL 16-byte chunks per lane per row.
+template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+    extern __shared__ float xs[];
+    __shared__ float red[kWaves];
+    __shared__ uint64_t red64[kWaves];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    constexpr int RPB = RPW * kWaves;
+    const int r0 = blockIdx.x * RPB + wave * RPW;
+    // For paired rows (gate j, up j), a wave takes j and j + half.
+    const int half = a.n_rows / 2;
+    uint4 w[RPW][CPL];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        int row;
+        if (EPI == kSiluPairs) row = (r & 1) ? (r0 + r - 1) / 2 + half : (r0 + r) / 2;
+        else row = r0 + r;
+        const bool valid = EPI == kSiluPairs ? (r0 + r - (r & 1)) / 2 < half : row < a.n_rows;
+        const uint4 *p = row_at(a.rows, valid ? row : 0, a.cols);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) w[r][c] = p[c * 64 + lane];
+    }
+    build_input<PRO == kNormSum, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out,
+                                                                        red);
+    float res[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) acc = dot8(xs, w[r][c], c * 64 + lane, acc);
+        res[r] = wave_sum_dpp(acc);
+    }
+    if (EPI == kStore) {
+        if (lane < RPW) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+                if (lane == r && r0 + r < a.n_rows) a.out[r0 + r] = res[r];
+        }
+    } else if (EPI == kSiluPairs) {
+        // Rows r0 + 2i and r0 + 2i + 1 of the wave are gate j and up j.
+#pragma unroll
+        for (int r = 0; r + 1 < RPW; r += 2) {
+            const int j = (r0 + r) / 2;
+            if (lane == 0 && j < half) a.out[j] = silu(res[r]) * res[r + 1];
+        }
+    } else {
+        uint64_t best = 0;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            if (r0 + r < a.n_rows) {
+                if (lane == 0) a.out[r0 + r] = res[r];
+                best = max_u64(best, argmax_pack(res[r], (uint32_t)(r0 + r)));
+            }
+        }
+        if (lane == 0) red64[wave] = best;
+        __syncthreads();
+        if (tid == 0) {
+            uint64_t b = 0;
+            for (int i = 0; i < kWaves; ++i) b = max_u64(b, red64[i]);
+            a.argmax[blockIdx.x] = b;
+        }
+    }
+}
+
+template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
+hipError_t gemv_launch(hipStream_t s, const GemvArgs &a) {
+    constexpr int RPB = RPW * kWaves;
+    const int rows = EPI == kSiluPairs ? a.n_rows : a.n_rows;
+    dim3 grid((unsigned)((rows + RPB - 1) / RPB));
+    gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, a.cols * sizeof(float), s>>>(a);
+    return hipGetLastError();
+}
+
+// Dispatch on chunks per lane (cols / 512).
+template <int RPW, Prologue PRO, Epilogue EPI>
+hipError_t gemv_dispatch(hipStream_t s, const GemvArgs &a) {
+    switch (a.cols / 512) {
+    case 1: return gemv_launch<RPW, 1, PRO, EPI>(s, a);
+    case 2: return gemv_launch<RPW, 2, PRO, EPI>(s, a);
+    case 3: return gemv_launch<RPW, 3, PRO, EPI>(s, a);
+    case 4: return gemv_launch<RPW, 4, PRO, EPI>(s, a);
+    case 5: return gemv_launch<RPW, 5, PRO, EPI>(s, a);
+    case 6: return gemv_launch<RPW, 6, PRO, EPI>(s, a);
+    case 8: return gemv_launch<RPW, 8, PRO, EPI>(s, a);
+    case 19: return gemv_launch<(RPW > 1 ? 1 : RPW), 19, PRO, EPI>(s, a);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ---- attention for one token: q/k RMSNorm + RoPE + KV append + split attention ----
+
+constexpr int kStageRows = 64;  // cached positions staged in LDS per pass
+
+__device__ __forceinline__ void dma16(const void *src, void *wave_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)wave_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void lds_row8(const float *row, int sub, float f[8]) {
+    const float4 a = reinterpret_cast<const float4 *>(row)[sub * 2], b = reinterpret_cast<const float4 *>(row)[sub * 2 + 1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ void lds_row8(const uint16_t *row, int sub, float f[8]) {
+    unpack8(reinterpret_cast<const uint4 *>(row)[sub], f);
+}
+__device__ __forceinline__ float lds_at(const float *row, int d) { return row[d]; }
+__device__ __forceinline__ float lds_at(const uint16_t *row, int d) { return bf16_to_f32(row[d]); }
+
+// One block per (KV head, split of the positions 0..pos): the group's q heads
+// and the new k are RMSNorm'd and rotated in LDS, the split holding pos
+// appends k and v to the caches, and cached K/V rows are staged into LDS 64
+// positions at a time (all loads of a pass in flight together) for scores,
+// online softmax and the weighted sum of values.
+template <int HD, int G, typename KV>
+__global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a) {
+    constexpr int LPK = HD / 8, KPW = 64 / LPK, KPB = kWaves * KPW, NP = kThreads / HD;
+    constexpr int ROW16 = HD * (int)sizeof(KV) / 16;  // 16-byte chunks per cached row
+    __shared__ float hq[G * HD], hk[HD], hv[HD];
+    __shared__ float scores[G][kStageRows];
+    __shared__ float st_m[G], st_l[G], st_a[G];
+    __shared__ float red[G][kThreads];
+    __shared__ uint4 kst[kStageRows * ROW16], vst[kStageRows * ROW16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPK;
+    const int split = blockIdx.x % a.nsplit, g = blockIdx.x / a.nsplit;
+    const long long pos = *a.pos;
+    const long long len = pos + 1;
+    const long long chunk = ((len + a.nsplit - 1) / a.nsplit + 15) / 16 * 16;
+    const long long s0 = (long long)split * chunk;
+    const long long s1 = s0 + chunk < len ? s0 + chunk : len;
+    const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
+    const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
+    const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
+
+    // Stage the first pass's cached rows while the q/k/v rows are read and normalized.
+    auto stage = [&](long long c0, int ncache) {
+        const int chunks = ncache * ROW16;
+        const uint4 *ks = reinterpret_cast<const uint4 *>(kc + c0 * HD);
+        const uint4 *vs = reinterpret_cast<const uint4 *>(vc + c0 * HD);
+        for (int base = wave * 64; base < chunks; base += kThreads)
+            if (base + lane < chunks) {
+                dma16(ks + base + lane, kst + base);
+                dma16(vs + base + lane, vst + base);
+            }
+    };
+    auto cached_in = [&](long long c0, int cnt) -> int {
+        const long long nc = pos - c0;
+        return nc <= 0 ? 0 : (nc < cnt ? (int)nc : cnt);
+    };
+    {
+        const int cnt0 = (int)(s1 - s0 < kStageRows ? s1 - s0 : kStageRows);
+        if (s0 < s1) stage(s0, cached_in(s0, cnt0));
+    }
+    // This group's raw q heads, k and v.
+    for (int i = tid; i < G * HD; i += kThreads) hq[i] = a.qkv[(size_t)g * G * HD + i];
+    for (int i = tid; i < HD; i += kThreads) {
+        hk[i] = a.qkv[qd + (size_t)g * HD + i];
+        hv[i] = a.qkv[qd + kvd + (size_t)g * HD + i];
+    }
+    if (tid < G) {
+        st_m[tid] = -INFINITY;
+        st_l[tid] = 0.f;
+    }
+    __syncthreads();
+    // RMSNorm + RoPE per head, one wave each (lane holds pairs (l + 64k, l + 64k + HD/2)).
+    const float *ang = a.rope + pos * HD;
+    for (int h = wave; h <= G; h += kWaves) {
+        float *x = h < G ? hq + h * HD : hk;
+        const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
+        constexpr int HALF = HD / 2;
+        float av[2], bv[2], cs[2], sn[2], ga[2], gb[2], ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = lane + 64 * k;
+            av[k] = i < HALF ? x[i] : 0.f;
+            bv[k] = i < HALF ? x[i + HALF] : 0.f;
+            cs[k] = i < HALF ? ang[2 * i] : 0.f;
+            sn[k] = i < HALF ? ang[2 * i + 1] : 0.f;
+            ga[k] = gain && i < HALF ? bf16_to_f32(gain[i]) : 1.f;
+            gb[k] = gain && i < HALF ? bf16_to_f32(gain[i + HALF]) : 1.f;
+            ss += av[k] * av[k] + bv[k] * bv[k];
+        }
+        if (gain) {
+            ss = wave_sum(ss);
+            const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                av[k] = av[k] * (scale * ga[k]);
+                bv[k] = bv[k] * (scale * gb[k]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = lane + 64 * k;
+            if (i < HALF) {
+                x[i] = av[k] * cs[k] - bv[k] * sn[k];
+                x[i + HALF] = bv[k] * cs[k] + av[k] * sn[k];
+            }
+        }
+    }
+    __syncthreads();
+    // The split holding pos appends the new key and value.
+    if (pos >= s0 && pos < s1) {
+        KV *kw = reinterpret_cast<KV *>(a.k_cache) + (size_t)g * a.head_stride + pos * HD;
+        KV *vw = reinterpret_cast<KV *>(a.v_cache) + (size_t)g * a.head_stride + pos * HD;
+        for (int i = tid; i < HD; i += kThreads) {
+            store_kv(kw + i, hk[i]);
+            store_kv(vw + i, hv[i]);
+        }
+    }
+    float qf[G][8];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[gg][i] = hq[gg * HD + sub * 8 + i];
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int d = tid % HD, pt = tid / HD;
+    const KV *ks_l = reinterpret_cast<const KV *>(kst), *vs_l = reinterpret_cast<const KV *>(vst);
+    float acc[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) acc[gg] = 0.f;
+    for (long long c0 = s0; c0 < s1; c0 += kStageRows) {
+        const int cnt = (int)(s1 - c0 < kStageRows ? s1 - c0 : kStageRows);
+        const int ncache = cached_in(c0, cnt);
+        if (c0 != s0) stage(c0, ncache);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        for (int j0 = 0; j0 < cnt; j0 += KPB) {
+            const int j = j0 + wave * KPW + lane / LPK;
+            float kf[8];
+            if (j < ncache) {
+                lds_row8(ks_l + j * HD, sub, kf);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kf[i] = j < cnt ? hk[sub * 8 + i] : 0.f;
+            }
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+                float sc = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sc = fmaf(qf[gg][i], kf[i], sc);
+                sc = group_sum<LPK>(sc);
+                if (j < cnt && sub == 0) scores[gg][j] = scale * sc;
+            }
+        }
+        __syncthreads();
+        for (int gg = wave; gg < G; gg += kWaves) {
+            float m = -INFINITY;
+            for (int j = lane; j < cnt; j += 64) m = fmaxf(m, scores[gg][j]);
+            m = wave_max(m);
+            const float m_old = st_m[gg], m_new = fmaxf(m_old, m);
+            float l = 0.f;
+            for (int j = lane; j < cnt; j += 64) {
+                const float e = expf(scores[gg][j] - m_new);
+                scores[gg][j] = e;
+                l += e;
+            }
+            l = wave_sum(l);
+            if (lane == 0) {
+                const float al = expf(m_old - m_new);
+                st_a[gg] = al;
+                st_l[gg] = st_l[gg] * al + l;
+                st_m[gg] = m_new;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) acc[gg] *= st_a[gg];
+        for (int j = pt; j < cnt; j += NP) {
+            const float v = j < ncache ? lds_at(vs_l + j * HD, d) : hv[d];
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) acc[gg] = fmaf(scores[gg][j], v, acc[gg]);
+        }
+        __syncthreads();  // the stage and scores are rewritten by the next pass
+    }
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) red[gg][tid] = acc[gg];
+    __syncthreads();
+    if (pt != 0) return;
+    for (int gg = 0; gg < G; ++gg) {
+        float sm = red[gg][d];
+        for (int q = 1; q < NP; ++q) sm += red[gg][q * HD + d];
+        const long long h = (long long)g * G + gg;
+        if (a.nsplit == 1) {
+            a.out[h * HD + d] = sm / st_l[gg];
+        } else {
+            const long long slot = h * a.nsplit + split;
+            a.part_acc[slot * HD + d] = sm;
+            if (d == 0) {
+                a.part_ml[slot * 2] = st_m[gg];
+                a.part_ml[slot * 2 + 1] = st_l[gg];
+            }
+        }
+    }
+}
+
+template <int HD, int G>
+hipError_t attn_launch(hipStream_t s, const StepAttnArgs &a) {
+    dim3 grid((unsigned)(a.n_kv_heads * a.nsplit));
+    if (a.kv_bf16)
+        step_attention_kernel<HD, G, uint16_t><<<grid, kThreads, 0, s>>>(a);
+    else
+        step_attention_kernel<HD, G, float><<<grid, kThreads, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool step_supported(int hidden, int intermediate, int n_heads, int n_kv_heads, int head_dim) {
+    if (head_dim != 128 || n_kv_heads <= 0 || n_heads % n_kv_heads) return false;
+    const int g = n_heads / n_kv_heads;
+    if (g != 1 && g != 2 && g != 4 && g != 8) return false;
+    const int cols[3] = {hidden, n_heads * head_dim, intermediate};
+    for (int c : cols) {
+        if (c % 512) return false;
+        const int cpl = c / 512;
+        if (cpl > 8 && cpl != 19) return false;
+    }
+    return true;
+}
+
+hipError_t launch_step_qkv(hipStream_t s, const StepQkvArgs &q) {
+    GemvArgs a{};
+    a.rows.base[0] = q.wq;
+    a.rows.count[0] = q.q_rows;
+    a.rows.base[1] = q.wk;
+    a.rows.count[1] = q.kv_rows;
+    a.rows.base[2] = q.wv;
+    a.rows.count[2] = q.kv_rows;
+    a.n_rows = q.q_rows + 2 * q.kv_rows;
+    a.cols = q.hidden;
+    a.a = q.x_prev;
+    a.b = q.y_prev;
+    a.gain = q.gain;
+    a.eps = q.eps;
+    a.x_out = q.x_out;
+    a.out = q.qkv;
+    return gemv_dispatch<2, kNormSum, kStore>(s, a);
+}
+
+hipError_t launch_step_gemv(hipStream_t s, const uint16_t *w, int rows, int cols, const float *x, float *out) {
+    GemvArgs a{};
+    a.rows.base[0] = w;
+    a.rows.count[0] = rows;
+    a.n_rows = rows;
+    a.cols = cols;
+    a.a = x;
+    a.out = out;
+    return gemv_dispatch<1, kPlain, kStore>(s, a);
+}
+
+hipError_t launch_step_gate_up(hipStream_t s, const uint16_t *gate, const uint16_t *up, int inter, int hidden,
+                               const float *x1, const float *o, const uint16_t *gain, float eps, float *x_out,
+                               float *h) {
+    GemvArgs a{};
+    a.rows.base[0] = gate;
+    a.rows.count[0] = inter;
+    a.rows.base[1] = up;
+    a.rows.count[1] = inter;
+    a.n_rows = 2 * inter;
+    a.cols = hidden;
+    a.a = x1;
+    a.b = o;
+    a.gain = gain;
+    a.eps = eps;
+    a.x_out = x_out;
+    a.out = h;
+    return gemv_dispatch<2, kNormSum, kSiluPairs>(s, a);
+}
+
+hipError_t launch_step_logits(hipStream_t s, const uint16_t *w, int vocab, int hidden, const float *x,
+                              const float *y, const uint16_t *gain, float eps, float *logits, uint64_t *partials,
+                              int *n_partials) {
+    GemvArgs a{};
+    a.rows.base[0] = w;
+    a.rows.count[0] = vocab;
+    a.n_rows = vocab;
+    a.cols = hidden;
+    a.a = x;
+    a.b = y;
+    a.gain = gain;
+    a.eps = eps;
+    a.out = logits;
+    a.argmax = partials;
+    *n_partials = (vocab + 4 * kWaves - 1) / (4 * kWaves);
+    return gemv_dispatch<4, kNormSum, kLogits>(s, a);
+}
+
+int step_logits_partials(int vocab) { return (vocab + 4 * kWaves - 1) / (4 * kWaves); }
+
+hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a) {
+    switch (a.n_heads / a.n_kv_heads) {
+    case 1: return attn_launch<128, 1>(s, a);
+    case 2: return attn_launch<128, 2>(s, a);
+    case 4: return attn_launch<128, 4>(s, a);
+    case 8: return attn_launch<128, 8>(s, a);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace th
