@@ -71,6 +71,62 @@ def cpu_baseline(cfg, weights, prompt, steps: int, repeats: int) -> dict:
     }
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "decode_traffic.json"
+
+
+def measured_traffic(model: str, kv: str, mode: str):
+    """HBM bytes per decode step (read + write) measured with hardware
+    counters for this workload, if a measurement is on file; else None."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get(f"{model}/{kv}")
+    return None if entry is None else entry.get("traffic_bytes_per_step")
+
+
+def _counter_rows(directory: str):
+    import csv
+
+    files = sorted(Path(directory).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    with open(files[-1], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def pmc_summary(fetch_dir: str, write_dir: str, steps: int, copy_mib: int) -> dict:
+    """Per-step HBM bytes from FETCH_SIZE and WRITE_SIZE (KiB per dispatch):
+    the dispatches after the calibration copy are the timed decode steps; each
+    counter is scaled by copy bytes / what it read for the copy."""
+    if copy_mib <= 0:
+        raise SystemExit("--pmc-summary needs --calibrate-copy MIB (the size the runs used)")
+    copy_bytes = copy_mib * (1 << 20)
+    out = {"steps": steps, "copy_bytes": copy_bytes}
+    total = 0.0
+    for name, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = [r for r in _counter_rows(directory) if r["Counter_Name"] == name]
+        per_dispatch = {}
+        kernel = {}
+        for r in rows:
+            d = int(r["Dispatch_Id"])
+            per_dispatch[d] = per_dispatch.get(d, 0.0) + float(r["Counter_Value"])
+            kernel[d] = r["Kernel_Name"]
+        copies = [d for d in per_dispatch if "copy_kernel" in kernel[d]]
+        if not copies:
+            raise SystemExit(f"{name}: no copy_kernel dispatch in {directory}")
+        c = max(copies)
+        copy_kib = per_dispatch[c]
+        after = sum(v for d, v in per_dispatch.items() if d > c)
+        scale = (copy_bytes / 1024.0) / copy_kib
+        step_bytes = after / steps * 1024.0 * scale
+        out[name] = {"copy_kib": copy_kib, "scale": scale, "kib_per_step_raw": after / steps,
+                     "bytes_per_step": step_bytes, "dispatches": sum(1 for d in per_dispatch if d > c)}
+        total += step_bytes
+    out["traffic_bytes_per_step"] = total
+    return out
+
+
 PHASES = ["norm+qkv", "attention", "o+residual", "norm+gate/up", "down+residual"]
 
 
@@ -120,6 +176,12 @@ def main() -> int:
     ap.add_argument("--model", choices=["qwen3-0.6b", "qwen3-4b"], default="qwen3-0.6b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-repeats", type=int, default=3)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="before the timed steps, copy a MIB-MiB buffer once with the library's copy kernel: a "
+                         "known-size reference for the hardware byte counters (see --pmc-summary)")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="instead of benchmarking, summarize two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                         "'bench.py --calibrate-copy MIB --steps K' into HBM bytes per decode step")
     ap.add_argument("--trace", type=int, default=0,
                     help="trace the first N timed steps of the persistent decode kernel and print a per-phase "
                          "breakdown to stderr")
@@ -127,6 +189,9 @@ def main() -> int:
     if args.trace:
         os.environ["TITANIA_TRACE"] = str(args.trace)
 
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary, steps=args.steps, copy_mib=args.calibrate_copy)))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode path runs on a single MI355X and --gpus {args.gpus} "
               "is not supported (no multi-GPU sharding is built).", file=sys.stderr)
@@ -155,6 +220,13 @@ def main() -> int:
         model.decode(state, args.prompt, W)
     # Timed: the prompt is re-run first (rewriting positions 0..15), then exactly K steps.
     model.forward(state, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        a, b = dev.alloc(n), dev.alloc(n)
+        dev.copy(b, 0, a, 0, n)
+        dev.synchronize()
+        a.free()
+        b.free()
     dev.synchronize()
     dev.timer_begin()
     t0 = time.perf_counter()
@@ -168,6 +240,12 @@ def main() -> int:
     logits_bytes = 4 * cfg.vocab_size
     bytes_per_token = weight_bytes + kvb + logits_bytes
     achieved = bytes_per_token / (gpu_ms / 1000.0 / K) / 1e9
+    mode = os.environ.get("TITANIA_DECODE", "graph")
+    kernel = {
+        "persistent": "decode step inside the persistent decode kernel (one launch for all steps)",
+        "eager": "decode step (one token's kernels launched one by one)",
+    }.get(mode, "decode step (one HIP graph replay: one token's kernels)")
+    traffic = measured_traffic(args.model, args.kv, mode)
 
     out = {
         "metric": "batch-1 decode tokens/s (Qwen3-0.6B shape) + % of HBM GB/s roofline",
@@ -192,12 +270,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode step (HIP graph of one token's kernels)",
+            "kernel": kernel,
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_step": bytes_per_token,
             "gpu_ms_per_step": gpu_ms / K,
         },

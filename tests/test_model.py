@@ -18,6 +18,7 @@ from oracle import ref
 from titania_amd import QWEN3_0_6B, QWEN3_TINY, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS
 from titania_amd import synth
 from titania_amd.model import Model, State
+from util import load_fixture
 
 pytestmark = pytest.mark.gpu
 
@@ -75,6 +76,34 @@ def test_paths_refuse_to_mix(tiny):
     with pytest.raises(Exception):
         m.forward(st, [4], 3, TH_PATH_FUSED)
     st.close()
+
+
+@pytest.mark.parametrize("name", ["tied", "untied"])
+@pytest.mark.parametrize("path", [TH_PATH_OPS, TH_PATH_FUSED])
+def test_forward_matches_transformers(hip, name, path):
+    """The device's logits at every position against transformers'
+    Qwen3ForCausalLM (a fixture made with tests/golden/make_hf_qwen3.py), an
+    implementation independent of both the reference and the oracle; then the
+    device decode loop reproduces the fixture's greedy tokens."""
+    cfg, meta, tokens, logits = load_fixture(name)
+    w = synth.weights(cfg, seed=meta["seed"], random_gains=meta["random_gains"])
+    m = Model(hip, cfg, w)
+    p = meta["prompt_len"]
+    st = State(m, len(tokens))
+    got = m.forward(st, tokens[:p], 0, path)
+    assert float(np.max(np.abs(got - logits[p - 1]))) <= 1e-4
+    for i in range(p, len(tokens)):
+        assert int(np.argmax(got)) == int(tokens[i]), f"greedy token {i}"
+        got = m.forward(st, tokens[i:i + 1], i, path)
+        assert float(np.max(np.abs(got - logits[i]))) <= 1e-4, f"position {i}"
+    st.close()
+    if path == TH_PATH_FUSED:
+        st = State(m, len(tokens))
+        m.forward(st, tokens[:p], 0, TH_PATH_FUSED, want_logits=False)
+        toks = m.decode(st, p, len(tokens) - p)
+        assert list(toks) == [int(t) for t in tokens[p:]]
+        st.close()
+    m.close()
 
 
 @pytest.fixture(scope="module")

@@ -6,6 +6,9 @@ differential tests (model/titania.rs:231-249), so the same cases run here.
 
 from __future__ import annotations
 
+import json
+from pathlib import Path
+
 import numpy as np
 
 from titania_amd.device import Tensor
@@ -47,3 +50,17 @@ def rel_error(actual, expected) -> float:
     a = np.asarray(actual, dtype=np.float64).reshape(-1)
     e = np.asarray(expected, dtype=np.float64).reshape(-1)
     return float(np.linalg.norm(a - e) / max(np.linalg.norm(e), 1e-30))
+
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def load_fixture(name: str):
+    """A Hugging Face Qwen3 fixture (tests/golden/make_hf_qwen3.py): the
+    config, the generator's metadata, the token sequence (prompt then greedy
+    tokens) and the logits at every position."""
+    from titania_amd.config import Config
+
+    f = np.load(GOLDEN / f"hf_qwen3_{name}.npz")
+    meta = json.loads(str(f["meta"]))
+    return Config(**meta["config"]), meta, f["tokens"], f["logits"]

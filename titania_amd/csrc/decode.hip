@@ -32,7 +32,7 @@ namespace {
 
 constexpr int NT = 512;              // threads per block
 constexpr int NW = NT / 64;          // waves per block
-constexpr int NPOLL = 4;             // waves that poll exchange buffers; the others stage weights
+constexpr int NPOLL = NW;            // waves that poll exchange buffers (and stage weights before polling)
 constexpr int PUB = NW - 1;          // the wave that publishes results (it never polls)
 constexpr int STAGE = 4096;          // 16-byte chunks staged in LDS ahead of a wait (64 KB)
 constexpr int MAX_COLS = 10240;      // longest input vector kept in LDS (floats)
@@ -92,29 +92,47 @@ __device__ __forceinline__ void raise_abort(const DecodeParams &p, int protocol)
 }
 
 // Polls n exchange words until all carry `epoch`, copying their values to dst
-// (LDS). Only the first NPOLL waves issue loads, so their polls are not queued
-// behind the staging loads of the other waves. Returns false (block-uniformly)
-// on timeout, abort or a word from a later epoch (a protocol error).
+// (LDS). Each round, a thread issues the loads of all its words still missing
+// before looking at any, so a round costs one memory round trip. Returns false
+// (block-uniformly) on timeout, abort or a word from a later epoch (a protocol
+// error).
 __device__ __forceinline__ bool wait_vec(const DecodeParams &p, const u64 *src, int n, unsigned epoch, float *dst) {
     constexpr int NP = NPOLL * 64;
+    constexpr int KMAX = 24;  // words per thread: n <= KMAX * NP
+    constexpr int KB = 8;
+    static_assert(KMAX * NP >= MAX_COLS && KMAX <= 32, "poll bitmask must cover the longest vector");
     const int tid = threadIdx.x;
     __syncthreads();  // dst may still be read by the previous phase
     const long long t0 = (long long)__builtin_amdgcn_s_memrealtime();
-    u64 done = 0;  // bit k: entry tid + k*NP already taken (n <= 64*NP)
+    unsigned done = 0;  // bit k: word tid + k*NP already taken
     for (int it = 0;; ++it) {
         int ok = 1, bad = 0;
         if (tid < NP) {
-            int k = 0;
-            for (int i = tid; i < n; i += NP, ++k) {
-                if (done & (1ull << k)) continue;
-                const u64 w = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const int d = (int)((unsigned)(w >> 32) - epoch);
-                if (d == 0) {
-                    dst[i] = __uint_as_float((unsigned)w);
-                    done |= 1ull << k;
-                } else {
-                    ok = 0;
-                    if (d > 0) bad = 1;
+            // Batches of KB words: every load of a batch is in flight before
+            // the first is examined (one batch covers n <= KB * NP).
+#pragma unroll 1
+            for (int kb = 0; kb < KMAX; kb += KB) {
+                if (tid + kb * NP >= n) break;
+                u64 w[KB];
+#pragma unroll
+                for (int j = 0; j < KB; ++j) {
+                    const int k = kb + j, i = tid + k * NP;
+                    if (i < n && !(done & (1u << k)))
+                        w[j] = __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int j = 0; j < KB; ++j) {
+                    const int k = kb + j, i = tid + k * NP;
+                    if (i < n && !(done & (1u << k))) {
+                        const int d = (int)((unsigned)(w[j] >> 32) - epoch);
+                        if (d == 0) {
+                            dst[i] = __uint_as_float((unsigned)w[j]);
+                            done |= 1u << k;
+                        } else {
+                            ok = 0;
+                            if (d > 0) bad = 1;
+                        }
+                    }
                 }
             }
         }
@@ -225,8 +243,7 @@ __device__ __forceinline__ const uint4 *gemv_chunk(const GemvPlan &g, const RowM
 // do not depend on the input the block is about to wait for.
 __device__ __forceinline__ void gemv_stage(Shared &sh, const GemvPlan &g, const RowMap &m) {
     const int wave = threadIdx.x >> 6;
-    if (wave < NPOLL) return;
-    for (int q = wave - NPOLL; q < g.staged; q += NW - NPOLL) {
+    for (int q = wave; q < g.staged; q += NW) {
         int col;
         lds_dma16(gemv_chunk(g, m, q, col), sh.stage + q * 64);
     }
@@ -235,17 +252,15 @@ __device__ __forceinline__ void gemv_stage(Shared &sh, const GemvPlan &g, const 
 // Staging waves copy `bytes` (a multiple of 16) from src into LDS at dst.
 __device__ __forceinline__ void stage_small(const void *src, void *dst, int bytes) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave < NPOLL) return;
     const int chunks = bytes >> 4;
-    for (int c0 = (wave - NPOLL) * 64; c0 < chunks; c0 += (NW - NPOLL) * 64)
+    for (int c0 = wave * 64; c0 < chunks; c0 += NW * 64)
         if (c0 + lane < chunks)
             lds_dma16(reinterpret_cast<const uint4 *>(src) + c0 + lane, reinterpret_cast<uint4 *>(dst) + c0);
 }
 
-// The staging waves wait for their loads (only they have any outstanding that
-// matter: the polling waves' stores need no wait), then everyone syncs.
+// Every wave waits for its staging loads, then everyone syncs.
 __device__ __forceinline__ void stage_ready() {
-    if ((threadIdx.x >> 6) >= NPOLL) __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 }
 
@@ -499,8 +514,8 @@ __device__ __forceinline__ bool attention_phase(Shared &sh, const DecodeParams &
         const int npre = (int)(cached < cap ? (cached > 0 ? cached : 0) : cap);
         const int kv_spans = (npre * row_chunks * 2 + 63) / 64;
         __syncthreads();  // the stage may still be read by the previous item
-        if (wave >= NPOLL) {
-            for (int q = wave - NPOLL; q < kv_spans; q += NW - NPOLL) {
+        {
+            for (int q = wave; q < kv_spans; q += NW) {
                 const int idx = q * 64 + (tid & 63);
                 if (idx < npre * row_chunks * 2) {
                     const int half = idx / (npre * row_chunks), rem = idx - half * npre * row_chunks;
@@ -735,8 +750,13 @@ __global__ __launch_bounds__(NT) void decode_kernel(DecodeParams p) {
                     } else {
                         // The first layer's input: the token's embedding row.
                         __syncthreads();
-                        const uint16_t *row = p.embed + (size_t)token * H;
-                        for (int i = tid; i < H; i += NT) sh.xin[i] = bf16_to_f32(row[i]);
+                        const uint4 *row = reinterpret_cast<const uint4 *>(p.embed + (size_t)token * H);
+                        for (int c = tid; c < H / 8; c += NT) {
+                            float f[8];
+                            unpack8(row[c], f);
+#pragma unroll
+                            for (int e8 = 0; e8 < 8; ++e8) sh.xin[c * 8 + e8] = f[e8];
+                        }
                         __syncthreads();
                         for (int i = tid; i < n_own; i += NT) sh.xown[i] = sh.xin[o0 + i];
                     }

@@ -267,18 +267,40 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
     __shared__ float st_m[G], st_l[G], st_a[G];
     __shared__ float red[G][kThreads];
     __shared__ uint4 kst[kStageRows * ROW16], vst[kStageRows * ROW16];
+    static_assert(HD == 128, "one rotation pair per lane");
+    constexpr int HALF = HD / 2, HPW = (G + 1 + kWaves - 1) / kWaves;  // heads (q..., k) per wave
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPK;
     const int split = blockIdx.x % a.nsplit, g = blockIdx.x / a.nsplit;
+    const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
+    // Everything that does not depend on the position is requested first: the
+    // raw q heads and k of this wave (lane holds the pair (lane, lane + HD/2)),
+    // their RMSNorm gains and this thread's element of v.
+    float av[HPW], bv[HPW], ga[HPW], gb[HPW];
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+        const int h = wave + hh * kWaves;
+        av[hh] = bv[hh] = 0.f;
+        ga[hh] = gb[hh] = 1.f;
+        if (h <= G) {
+            const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
+            const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
+            av[hh] = x[lane];
+            bv[hh] = x[lane + HALF];
+            if (gain) {
+                ga[hh] = bf16_to_f32(gain[lane]);
+                gb[hh] = bf16_to_f32(gain[lane + HALF]);
+            }
+        }
+    }
+    const float vnew = tid < HD ? a.qkv[qd + kvd + (size_t)g * HD + tid] : 0.f;
     const long long pos = *a.pos;
     const long long len = pos + 1;
     const long long chunk = ((len + a.nsplit - 1) / a.nsplit + 15) / 16 * 16;
     const long long s0 = (long long)split * chunk;
     const long long s1 = s0 + chunk < len ? s0 + chunk : len;
-    const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
     const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
     const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
 
-    // Stage the first pass's cached rows while the q/k/v rows are read and normalized.
     auto stage = [&](long long c0, int ncache) {
         const int chunks = ncache * ROW16;
         const uint4 *ks = reinterpret_cast<const uint4 *>(kc + c0 * HD);
@@ -293,67 +315,36 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
         const long long nc = pos - c0;
         return nc <= 0 ? 0 : (nc < cnt ? (int)nc : cnt);
     };
+    // Then, once pos is known, the rotation of this position and the first
+    // pass's cached rows; all of it is one memory round trip.
+    const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
     {
         const int cnt0 = (int)(s1 - s0 < kStageRows ? s1 - s0 : kStageRows);
         if (s0 < s1) stage(s0, cached_in(s0, cnt0));
-    }
-    // This group's raw q heads, k and v.
-    for (int i = tid; i < G * HD; i += kThreads) hq[i] = a.qkv[(size_t)g * G * HD + i];
-    for (int i = tid; i < HD; i += kThreads) {
-        hk[i] = a.qkv[qd + (size_t)g * HD + i];
-        hv[i] = a.qkv[qd + kvd + (size_t)g * HD + i];
     }
     if (tid < G) {
         st_m[tid] = -INFINITY;
         st_l[tid] = 0.f;
     }
-    __syncthreads();
-    // RMSNorm + RoPE per head, one wave each (lane holds pairs (l + 64k, l + 64k + HD/2)).
-    const float *ang = a.rope + pos * HD;
-    for (int h = wave; h <= G; h += kWaves) {
+    if (tid < HD) hv[tid] = vnew;
+    // RMSNorm (model.rs:111-116) + RoPE (model.rs:117-118) per head, in registers.
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+        const int h = wave + hh * kWaves;
+        if (h > G) continue;
+        float x0 = av[hh], x1 = bv[hh];
+        if (h < G ? a.q_norm != nullptr : a.k_norm != nullptr) {
+            const float ss = wave_sum(x0 * x0 + x1 * x1);
+            const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
+            x0 = x0 * (sc * ga[hh]);
+            x1 = x1 * (sc * gb[hh]);
+        }
         float *x = h < G ? hq + h * HD : hk;
-        const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
-        constexpr int HALF = HD / 2;
-        float av[2], bv[2], cs[2], sn[2], ga[2], gb[2], ss = 0.f;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int i = lane + 64 * k;
-            av[k] = i < HALF ? x[i] : 0.f;
-            bv[k] = i < HALF ? x[i + HALF] : 0.f;
-            cs[k] = i < HALF ? ang[2 * i] : 0.f;
-            sn[k] = i < HALF ? ang[2 * i + 1] : 0.f;
-            ga[k] = gain && i < HALF ? bf16_to_f32(gain[i]) : 1.f;
-            gb[k] = gain && i < HALF ? bf16_to_f32(gain[i + HALF]) : 1.f;
-            ss += av[k] * av[k] + bv[k] * bv[k];
-        }
-        if (gain) {
-            ss = wave_sum(ss);
-            const float scale = 1.0f / sqrtf(ss / (float)HD + a.eps);
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                av[k] = av[k] * (scale * ga[k]);
-                bv[k] = bv[k] * (scale * gb[k]);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int i = lane + 64 * k;
-            if (i < HALF) {
-                x[i] = av[k] * cs[k] - bv[k] * sn[k];
-                x[i + HALF] = bv[k] * cs[k] + av[k] * sn[k];
-            }
-        }
+        x[lane] = x0 * cs.x - x1 * cs.y;
+        x[lane + HALF] = x1 * cs.x + x0 * cs.y;
     }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    // The split holding pos appends the new key and value.
-    if (pos >= s0 && pos < s1) {
-        KV *kw = reinterpret_cast<KV *>(a.k_cache) + (size_t)g * a.head_stride + pos * HD;
-        KV *vw = reinterpret_cast<KV *>(a.v_cache) + (size_t)g * a.head_stride + pos * HD;
-        for (int i = tid; i < HD; i += kThreads) {
-            store_kv(kw + i, hk[i]);
-            store_kv(vw + i, hv[i]);
-        }
-    }
     float qf[G][8];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg)
@@ -368,9 +359,11 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
     for (long long c0 = s0; c0 < s1; c0 += kStageRows) {
         const int cnt = (int)(s1 - c0 < kStageRows ? s1 - c0 : kStageRows);
         const int ncache = cached_in(c0, cnt);
-        if (c0 != s0) stage(c0, ncache);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        if (c0 != s0) {
+            stage(c0, ncache);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
         for (int j0 = 0; j0 < cnt; j0 += KPB) {
             const int j = j0 + wave * KPW + lane / LPK;
             float kf[8];
@@ -418,6 +411,14 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
             for (int gg = 0; gg < G; ++gg) acc[gg] = fmaf(scores[gg][j], v, acc[gg]);
         }
         __syncthreads();  // the stage and scores are rewritten by the next pass
+    }
+    // The split holding pos appends the new key and value (model.rs:119-120);
+    // no block of this launch reads that position from the caches.
+    if (pos >= s0 && pos < s1 && tid < HD) {
+        KV *kw = reinterpret_cast<KV *>(a.k_cache) + (size_t)g * a.head_stride + pos * HD;
+        KV *vw = reinterpret_cast<KV *>(a.v_cache) + (size_t)g * a.head_stride + pos * HD;
+        store_kv(kw + tid, hk[tid]);
+        store_kv(vw + tid, hv[tid]);
     }
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) red[gg][tid] = acc[gg];
