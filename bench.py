@@ -71,6 +71,45 @@ def cpu_baseline(cfg, weights, prompt, steps: int, repeats: int) -> dict:
     }
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
+
+
+def prefill_flops(c, n: int) -> float:
+    """Algorithmic flops of a forward over n prompt tokens from position 0:
+    the layer GEMMs (2 n rows cols each), causal attention (scores and
+    weighted values over n(n+1)/2 pairs per head) and the last token's lm_head."""
+    H, I, hd = c.hidden_size, c.intermediate_size, c.head_dim()
+    qd, kvd = c.num_attention_heads * hd, c.num_key_value_heads * hd
+    gemm = 2.0 * n * (H * qd + 2 * H * kvd + qd * H + 3 * H * I)
+    attn = 2.0 * 2.0 * hd * c.num_attention_heads * n * (n + 1) / 2
+    return c.num_hidden_layers * (gemm + attn) + 2.0 * H * c.vocab_size
+
+
+def prefill_bench(dev, model, cfg, n: int, kv: int, seed: int) -> dict:
+    """A prompt of n uniform-random tokens through the fused forward (MFMA
+    GEMMs for the projections), timed with HIP events on the device stream;
+    median of 3 runs after one warmup."""
+    from titania_amd import TH_PATH_FUSED, synth
+    from titania_amd.model import State
+
+    prompt = synth.prompt(n, cfg.vocab_size, seed=seed + 1)
+    st = State(model, n, kv)
+    model.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    times = []
+    for _ in range(3):
+        dev.synchronize()
+        dev.timer_begin()
+        model.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+        times.append(dev.timer_end())
+    st.close()
+    ms = sorted(times)[1]
+    fl = prefill_flops(cfg, n)
+    return {"tokens": n, "ms": ms, "tokens_per_s": n / (ms / 1000.0),
+            "roofline": {"bound": "mfma", "achieved": fl / (ms / 1000.0) / 1e12, "peak": MFMA_BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": fl / (ms / 1000.0) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                         "flops": fl}}
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "decode_traffic.json"
 
 
@@ -174,6 +213,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kv", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--model", choices=["qwen3-0.6b", "qwen3-4b"], default="qwen3-0.6b")
+    ap.add_argument("--prefill", type=int, default=512,
+                    help="also time a prefill of this many random prompt tokens (0: skip)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -281,6 +322,8 @@ def main() -> int:
         },
         "synth_s": gen_s,
     }
+    if args.prefill:
+        out["prefill"] = prefill_bench(dev, model, cfg, args.prefill, kv, args.seed)
     if not args.no_cpu:
         cb = cpu_baseline(cfg, weights, prompt, K, args.cpu_repeats)
         out["parity_tokens_match"] = [int(x) for x in tokens] == cb.pop("tokens")

@@ -188,6 +188,34 @@ def test_qwen_gemm(hip, n):
     assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
 
 
+# The prefill GEMM shapes of Qwen3-0.6B ([n x cols] x [cols x rows]); n = 100 is
+# a ragged token tile, n = 512 the 512-token prompt.
+QWEN_GEMM = {"q": (2048, 1024), "k/v": (1024, 1024), "o": (1024, 2048), "gate/up": (3072, 1024),
+             "down": (1024, 3072)}
+
+
+@pytest.mark.parametrize("name", list(QWEN_GEMM))
+@pytest.mark.parametrize("n", [100, 512])
+def test_qwen_prefill_gemm(hip, name, n):
+    """MFMA path with f32 activations that bf16 cannot hold exactly: the
+    relative error bar and an elementwise bound of a few fp32 ulps of the row."""
+    rows, cols = QWEN_GEMM[name]
+    if n == 512 and name not in ("q", "down"):
+        pytest.skip("one 512-token case per K size keeps the oracle fast")
+    rng = np.random.default_rng(n + rows + cols)
+    wbits = normal_bf16(rows * cols, 105, name)
+    x = rng.standard_normal(n * cols).astype(np.float32)
+    expected = ref.matmul(wbits, rows, cols, x)
+    xb = hip.alloc(n * cols)
+    hip.write(xb, x)
+    out = hip.alloc(n * rows)
+    hip.matmul(out, hip.upload(Tensor((rows, cols), wbits)), xb)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-5
+    bound = _row_bound(wbits, rows, cols, x, n)
+    assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
+
+
 def test_qwen_norms_and_rope(hip):
     # RMSNorm over 1024 and per head over 128 (16 q heads + 8 k heads), gains 1 + N(0, .1).
     for rows, dim, seed in [(1, 1024, 110), (16, 128, 111), (8, 128, 112)]:
