@@ -16,6 +16,7 @@ import pytest
 
 from oracle import ref
 from titania_amd import QWEN3_0_6B, QWEN3_TINY, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS
+from titania_amd.config import Config
 from titania_amd import synth
 from titania_amd.model import Model, State
 from util import load_fixture
@@ -176,4 +177,77 @@ def test_tiny_decode_modes(tiny, decode_mode, prompt_len, steps, kv):
     # A second call continues from where the first stopped.
     more = m.decode(st, prompt_len + steps, 3)
     assert len(more) == 3
+    st.close()
+
+
+# Eight KV heads (one per XCD) at a small size, for the XCD-parallel decode kernel.
+QWEN3_TINY8 = Config(hidden_size=1024, intermediate_size=2048, num_hidden_layers=2, num_attention_heads=16,
+                     num_key_value_heads=8, vocab_size=1000, head_dim_=128)
+
+
+@pytest.fixture(scope="module")
+def tiny8(hip):
+    w = synth.weights(QWEN3_TINY8, seed=8, random_gains=True)
+    m = Model(hip, QWEN3_TINY8, w)
+    yield m, ref.RefModel(QWEN3_TINY8, w)
+    m.close()
+
+
+@pytest.mark.parametrize("decode_mode", ["xcd", "graph"], indirect=True)
+@pytest.mark.parametrize("prompt_len,steps,kv", [(9, 24, TH_KV_F32), (300, 16, TH_KV_F32), (300, 12, TH_KV_BF16),
+                                                 (700, 8, TH_KV_F32)])
+def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
+    """Decode with one KV head per XCD against the oracle: one attention split
+    per head, and (700 positions) three splits merged by every block."""
+    m, r = tiny8
+    c = QWEN3_TINY8
+    prompt = synth.prompt(prompt_len, c.vocab_size, seed=prompt_len + 1)
+    st = State(m, prompt_len + steps + 3, kv)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    toks, logits = m.decode(st, prompt_len, steps, keep_logits=True)
+    rtoks, gaps, last = r.generate(r.state(prompt_len + steps + 3), prompt, steps)
+    tol = 1e-4 if kv == TH_KV_F32 else LOGIT_TOL
+    assert float(np.std(last)) > 0.05
+    assert float(np.max(np.abs(logits[-1] - last))) <= tol
+    assert list(toks) == list(rtoks) or np.min(gaps) < tol
+    more = m.decode(st, prompt_len + steps, 3)
+    assert len(more) == 3
+    st.close()
+
+
+def test_xcd_mode_refuses_unsupported_shape(tiny, decode_mode_xcd):
+    """An explicit TITANIA_DECODE=xcd on a model without one KV head per XCD is an error, not a fallback."""
+    m, _ = tiny
+    st = State(m, 32)
+    m.forward(st, [1, 2, 3], 0, TH_PATH_FUSED, want_logits=False)
+    with pytest.raises(Exception, match="XCD"):
+        m.decode(st, 3, 2)
+    st.close()
+
+
+@pytest.fixture
+def decode_mode_xcd():
+    old = os.environ.get("TITANIA_DECODE")
+    os.environ["TITANIA_DECODE"] = "xcd"
+    yield "xcd"
+    if old is None:
+        del os.environ["TITANIA_DECODE"]
+    else:
+        os.environ["TITANIA_DECODE"] = old
+
+
+def test_qwen06_greedy_xcd(qwen06, decode_mode_xcd):
+    """Qwen3-0.6B shape on the XCD-parallel kernel: 32 greedy steps match the oracle."""
+    m, r = qwen06
+    c = QWEN3_0_6B
+    prompt = synth.prompt(16, c.vocab_size, seed=0)
+    steps = 32
+    st = State(m, 16 + steps)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    toks, logits = m.decode(st, 16, steps, keep_logits=True)
+    rtoks, gaps, last = r.generate(r.state(16 + steps), prompt, steps)
+    err = float(np.max(np.abs(logits[-1] - last)))
+    assert err <= LOGIT_TOL, err
+    first_diff = next((i for i in range(steps) if toks[i] != rtoks[i]), None)
+    assert first_diff is None, (first_diff, float(gaps[first_diff]), err)
     st.close()

@@ -40,12 +40,21 @@ struct StepState {
     float *logits_out;     // logits after each fed token, or null
 };
 
+// The embedding row the pick writes for the next step (model/cpu.rs:38-47),
+// when `table` is not null: out[0..dim) = bf16 -> f32 of table[token].
+struct PickEmbed {
+    const uint16_t *table = nullptr;
+    size_t dim = 0;
+    float *out = nullptr;
+};
+
 // argmax of the logits -> st->token and st->tokens_out[st->step]; with
 // `advance`, pos and step move on first.
 hipError_t launch_pick(hipStream_t s, const float *logits, size_t vocab, uint64_t *partials, StepState *st,
-                       int advance);
+                       int advance, const PickEmbed &emb = PickEmbed());
 // The pick from per-block (key, inverted index) maxima already reduced by a kernel.
-hipError_t launch_pick_partials(hipStream_t s, const uint64_t *partials, size_t m, StepState *st, int advance);
+hipError_t launch_pick_partials(hipStream_t s, const uint64_t *partials, size_t m, StepState *st, int advance,
+                                const PickEmbed &emb = PickEmbed());
 hipError_t launch_keep_logits(hipStream_t s, const float *logits, size_t vocab, const StepState *st);
 
 __device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }

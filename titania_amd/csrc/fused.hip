@@ -108,8 +108,9 @@ hipError_t launch_qk_norm_rope_append(hipStream_t s, const QkvPostArgs &a) {
 // token as the step's pick and as the next token to feed, and advances the
 // position when `advance` is set (after a token has been fed).
 __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__ partials, size_t m, StepState *st,
-                                                   int advance) {
+                                                   int advance, PickEmbed emb) {
     __shared__ uint64_t red[16];
+    __shared__ uint32_t picked;
     uint64_t best = 0;
     // Eight loads in flight per thread per round.
     for (size_t i0 = threadIdx.x; i0 < m; i0 += 8 * 1024) {
@@ -132,6 +133,17 @@ __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__
         }
         st->token = tok;
         if (st->tokens_out) st->tokens_out[st->step] = tok;
+        picked = tok;
+    }
+    if (!emb.table) return;
+    __syncthreads();
+    const uint4 *row = reinterpret_cast<const uint4 *>(emb.table + (size_t)picked * emb.dim);
+    for (size_t c = threadIdx.x; c < emb.dim / 8; c += blockDim.x) {
+        float f[8];
+        unpack8(row[c], f);
+        float4 *o = reinterpret_cast<float4 *>(emb.out + c * 8);
+        o[0] = make_float4(f[0], f[1], f[2], f[3]);
+        o[1] = make_float4(f[4], f[5], f[6], f[7]);
     }
 }
 
@@ -145,16 +157,19 @@ __global__ void keep_logits_kernel(const float *__restrict__ logits, size_t voca
 }
 
 hipError_t launch_pick(hipStream_t s, const float *logits, size_t vocab, uint64_t *partials, StepState *st,
-                       int advance) {
+                       int advance, const PickEmbed &emb) {
+    if (emb.table && emb.dim % 8) return hipErrorInvalidValue;
     size_t m = argmax_partials(vocab);
     hipError_t e = launch_argmax_partials(s, logits, vocab, partials);
     if (e != hipSuccess) return e;
-    pick_kernel<<<1, 1024, 0, s>>>(partials, m, st, advance);
+    pick_kernel<<<1, 1024, 0, s>>>(partials, m, st, advance, emb);
     return hipGetLastError();
 }
 
-hipError_t launch_pick_partials(hipStream_t s, const uint64_t *partials, size_t m, StepState *st, int advance) {
-    pick_kernel<<<1, 1024, 0, s>>>(partials, m, st, advance);
+hipError_t launch_pick_partials(hipStream_t s, const uint64_t *partials, size_t m, StepState *st, int advance,
+                                const PickEmbed &emb) {
+    if (emb.table && emb.dim % 8) return hipErrorInvalidValue;
+    pick_kernel<<<1, 1024, 0, s>>>(partials, m, st, advance, emb);
     return hipGetLastError();
 }
 

@@ -20,6 +20,7 @@
 #include "decode.h"
 #include "fused.h"
 #include "step.h"
+#include "xdecode.h"
 
 namespace {
 
@@ -85,11 +86,17 @@ struct th_state {
     unsigned *status = nullptr;
     unsigned epoch_base = 0;
     int chunk = 256, n_splits = 1;
+    // The XCD-parallel decode kernel (TITANIA_DECODE=xcd, when the shape allows it).
+    bool xcd = false;
+    unsigned long long *xx = nullptr;  // all its exchange words, one allocation
+    unsigned long long *xx_x = nullptr, *xx_qkv = nullptr, *xx_att = nullptr, *xx_h = nullptr, *xx_part = nullptr,
+                       *xx_am = nullptr;
     // The captured decode step's buffers (fixed addresses for the graph).
     bool step_fused = false;
     float *sx_a = nullptr, *sx_b = nullptr, *s_y = nullptr, *s_qkv = nullptr, *s_att = nullptr, *s_o = nullptr,
           *s_h = nullptr;
     uint64_t *s_part = nullptr;
+    bool graph_keep = false;                // whether the captured step copies out the logits
     unsigned long long *trace = nullptr;  // per-phase ticks of the last decode (TITANIA_TRACE steps)
     int trace_steps = 0;
     size_t trace_words = 0;
@@ -226,13 +233,46 @@ int ensure_persistent(th_state *s) {
     s->persistent = mode && strcmp(mode, "persistent") == 0 &&
                     th::decode_supported((int)c.hidden_size, (int)c.intermediate_size, (int)c.num_attention_heads,
                                          (int)c.num_key_value_heads, (int)c.head_dim, (int)c.vocab_size, s->blocks);
-    if (!s->persistent) return TH_OK;
+    s->xcd = mode && strcmp(mode, "xcd") == 0 &&
+             th::xdecode_supported((int)c.hidden_size, (int)c.intermediate_size, (int)c.num_attention_heads,
+                                   (int)c.num_key_value_heads, (int)c.head_dim, (int)c.vocab_size, s->blocks);
+    if (!s->persistent && !s->xcd) return TH_OK;
     std::vector<th::LayerWeights> lw;
     for (const Layer &L : m->layers)
         lw.push_back({L.attn_norm->ptr, L.q->ptr, L.k->ptr, L.v->ptr, L.o->ptr, L.q_norm ? L.q_norm->ptr : nullptr,
                       L.k_norm ? L.k_norm->ptr : nullptr, L.mlp_norm->ptr, L.gate->ptr, L.up->ptr, L.down->ptr});
     TH_HIP(hipMalloc(&s->dev_layers, lw.size() * sizeof(th::LayerWeights)));
     TH_HIP(hipMemcpy(s->dev_layers, lw.data(), lw.size() * sizeof(th::LayerWeights), hipMemcpyHostToDevice));
+    TH_HIP(hipMalloc(&s->status, 64));
+    TH_HIP(hipMemset(s->status, 0, 64));
+    s->epoch_base = 0;
+    const char *tr = getenv("TITANIA_TRACE");
+    s->trace_steps = tr ? std::max(0, atoi(tr)) : 0;
+    if (s->trace_steps) {
+        s->trace_words = th::decode_trace_words((int)c.num_hidden_layers, s->trace_steps);
+        TH_HIP(hipMalloc(&s->trace, s->trace_words * sizeof(unsigned long long)));
+        TH_HIP(hipMemset(s->trace, 0, s->trace_words * sizeof(unsigned long long)));
+    }
+    if (s->xcd) {
+        // Exchange words, zeroed (epoch 0 precedes every epoch used). Every
+        // XCD's region is a multiple of 256 bytes, so no cache line is written
+        // by two XCDs.
+        const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
+        const size_t G = (size_t)(c.num_attention_heads / c.num_key_value_heads), X = th::kXcds;
+        const size_t nx = X * H, nqkv = X * (G + 2) * hd, natt = X * th::kXBlocksPerXcd * G * (hd + 2),
+                     nh = I, npart = 2 * X * H, nam = 2 * (size_t)s->blocks;
+        auto up = [](size_t n) { return (n + 31) / 32 * 32; };
+        const size_t total = up(nx) + up(nqkv) + up(natt) + up(nh) + up(npart) + up(nam);
+        TH_HIP(hipMalloc(&s->xx, total * sizeof(unsigned long long)));
+        TH_HIP(hipMemset(s->xx, 0, total * sizeof(unsigned long long)));
+        s->xx_x = s->xx;
+        s->xx_qkv = s->xx_x + up(nx);
+        s->xx_att = s->xx_qkv + up(nqkv);
+        s->xx_h = s->xx_att + up(natt);
+        s->xx_part = s->xx_h + up(nh);
+        s->xx_am = s->xx_part + up(npart);
+        return TH_OK;
+    }
     const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
     const size_t qd = (size_t)c.num_attention_heads * hd, kvd = (size_t)c.num_key_value_heads * hd;
     const size_t R = th::kReplicas;
@@ -251,16 +291,6 @@ int ensure_persistent(th_state *s) {
     const size_t ncount = (size_t)c.num_hidden_layers * (size_t)c.num_key_value_heads;
     TH_HIP(hipMalloc(&s->att_count, ncount * sizeof(unsigned)));
     TH_HIP(hipMemset(s->att_count, 0, ncount * sizeof(unsigned)));
-    TH_HIP(hipMalloc(&s->status, 64));
-    TH_HIP(hipMemset(s->status, 0, 64));
-    s->epoch_base = 0;
-    const char *tr = getenv("TITANIA_TRACE");
-    s->trace_steps = tr ? std::max(0, atoi(tr)) : 0;
-    if (s->trace_steps) {
-        s->trace_words = th::decode_trace_words((int)c.num_hidden_layers, s->trace_steps);
-        TH_HIP(hipMalloc(&s->trace, s->trace_words * sizeof(unsigned long long)));
-        TH_HIP(hipMemset(s->trace, 0, s->trace_words * sizeof(unsigned long long)));
-    }
     return TH_OK;
 }
 
@@ -301,8 +331,21 @@ int ensure_fused_state(th_state *s) {
                   {&s->s_o, H}, {&s->s_h, I}};
         for (auto &b : sb) TH_HIP(hipMalloc(b.p, b.n * sizeof(float)));
         TH_HIP(hipMalloc(&s->s_part, (size_t)th::step_logits_partials((int)c.vocab_size) * sizeof(uint64_t)));
+
     }
     return ensure_persistent(s);
+}
+
+// What a pick writes for the next step of the fused step kernels: the picked
+// token's embedding row, in sx_b.
+th::PickEmbed step_embed(th_state *s) {
+    th::PickEmbed e;
+    if (s->step_fused) {
+        e.table = s->m->embed->ptr;
+        e.dim = (size_t)s->m->c.hidden_size;
+        e.out = s->sx_b;
+    }
+    return e;
 }
 
 // Queues one decode step with the fused step kernels: the token and position
@@ -318,7 +361,7 @@ int enqueue_step(th_state *s) {
     const int nsplit = th::attention_splits(1, (size_t)nkv, s->max_len);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
-    TH_HIP(th::launch_embed(st, s->sx_b, m->embed->ptr, (size_t)H, &s->step->token, 1));
+    // sx_b holds the token's embedding row: the previous pick wrote it.
     const float *y_prev = nullptr;
     for (size_t l = 0; l < m->layers.size(); ++l) {
         const Layer &L = m->layers[l];
@@ -335,7 +378,6 @@ int enqueue_step(th_state *s) {
         q.eps = eps;
         q.x_out = s->sx_a;
         q.qkv = s->s_qkv;
-        TH_HIP(th::launch_step_qkv(st, q));
         th::StepAttnArgs a{};
         a.qkv = s->s_qkv;
         a.q_norm = L.q_norm ? L.q_norm->ptr : nullptr;
@@ -353,6 +395,7 @@ int enqueue_step(th_state *s) {
         a.out = s->s_att;
         a.part_acc = s->attn_part;
         a.part_ml = s->attn_part ? s->attn_part + (size_t)nh * nsplit * hd : nullptr;
+        TH_HIP(th::launch_step_qkv(st, q));
         TH_HIP(th::launch_step_attention(st, a));
         if (nsplit > 1) TH_HIP(th::launch_attn_combine(st, s->s_att, a.part_acc, a.part_ml, (size_t)nh, nsplit, hd));
         TH_HIP(th::launch_step_gemv(st, L.o->ptr, H, qd, s->s_att, s->s_o));
@@ -364,8 +407,8 @@ int enqueue_step(th_state *s) {
     int np = 0;
     TH_HIP(th::launch_step_logits(st, m->out_proj()->ptr, V, H, s->sx_b, y_prev, m->norm->ptr, eps,
                                   s->logits->ptr, s->s_part, &np));
-    TH_HIP(th::launch_keep_logits(st, s->logits->ptr, (size_t)V, s->step));
-    TH_HIP(th::launch_pick_partials(st, s->s_part, (size_t)np, s->step, 1));
+    if (s->graph_keep) TH_HIP(th::launch_keep_logits(st, s->logits->ptr, (size_t)V, s->step));
+    TH_HIP(th::launch_pick_partials(st, s->s_part, (size_t)np, s->step, 1, step_embed(s)));
     return TH_OK;
 }
 
@@ -493,7 +536,7 @@ int capture_step(th_state *s) {
         const uint32_t *tok_dev = &s->step->token;
         rc = enqueue_fused(s, tok_dev, 1, 0, pos_dev);
         if (rc == TH_OK) {
-            hipError_t e = th::launch_keep_logits(st, s->logits->ptr, vocab, s->step);
+            hipError_t e = s->graph_keep ? th::launch_keep_logits(st, s->logits->ptr, vocab, s->step) : hipSuccess;
             if (e == hipSuccess) e = th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 1);
             if (e != hipSuccess) rc = fail(TH_ERR_HIP, "capture: %s", hipGetErrorString(e));
         }
@@ -560,6 +603,57 @@ int decode_persistent(th_state *s, size_t steps) {
     if (status[0] || status[1])
         return fail(TH_ERR_HIP, "persistent decode stopped: %u timeouts/aborts, %u protocol errors", status[0],
                     status[1]);
+    return TH_OK;
+}
+
+// All `steps` decode steps in one launch of the XCD-parallel kernel; the first
+// pick (from the logits the last forward left) runs just before it.
+int decode_xcd(th_state *s, size_t steps) {
+    th_model *m = s->m;
+    const th_config &c = m->c;
+    hipStream_t st = m->dev->stream;
+    TH_HIP(th::launch_pick(st, s->logits->ptr, (size_t)c.vocab_size, s->argmax_part, s->step, 0));
+    TH_HIP(hipMemsetAsync(s->status, 0, 64, st));
+    th::XDecodeParams p{};
+    p.layers = s->dev_layers;
+    p.embed = m->embed->ptr;
+    p.norm = m->norm->ptr;
+    p.lm_head = m->out_proj()->ptr;
+    p.rope = s->rope->ptr;
+    p.kv = s->kv;
+    p.kv_bf16 = s->kv_dtype == TH_KV_BF16;
+    p.logits = s->logits->ptr;
+    p.step = s->step;
+    p.x_loc = s->xx_x;
+    p.qkv_loc = s->xx_qkv;
+    p.att_loc = s->xx_att;
+    p.h_loc = s->xx_h;
+    p.part = s->xx_part;
+    p.am = s->xx_am;
+    p.status = s->status;
+    p.epoch_base = s->epoch_base;
+    p.steps = (int)steps;
+    p.hidden = (int)c.hidden_size;
+    p.intermediate = (int)c.intermediate_size;
+    p.n_layers = (int)c.num_hidden_layers;
+    p.n_heads = (int)c.num_attention_heads;
+    p.n_kv_heads = (int)c.num_key_value_heads;
+    p.head_dim = (int)c.head_dim;
+    p.vocab = (int)c.vocab_size;
+    p.max_len = (int)s->max_len;
+    p.eps = c.rms_norm_eps;
+    p.timeout_ticks = 200000000LL;  // 2 s at the 100 MHz reference clock
+    p.trace = s->trace;
+    p.trace_steps = s->trace_steps;
+    TH_HIP(th::launch_xdecode(st, p, s->blocks));
+    s->epoch_base += (unsigned)steps * th::xdecode_epochs_per_step((int)c.num_hidden_layers);
+    unsigned status[3] = {0, 0, 0};
+    TH_HIP(hipMemcpyAsync(status, s->status, sizeof status, hipMemcpyDeviceToHost, st));
+    TH_HIP(hipStreamSynchronize(st));
+    if (status[2])
+        return fail(TH_ERR_HIP, "XCD decode: %u blocks ran on another XCD than their index implies", status[2]);
+    if (status[0] || status[1])
+        return fail(TH_ERR_HIP, "XCD decode stopped: %u timeouts/aborts, %u protocol errors", status[0], status[1]);
     return TH_OK;
 }
 
@@ -656,7 +750,7 @@ void th_state_destroy(th_state *s) {
     void *ptrs[] = {s->fx,      s->fxb,        s->fq,   s->fk,         s->fv,         s->fatt,
                     s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
                     s->step,    s->tokens_dev, s->logits_dev, s->dev_layers, s->xchg, s->att_part,
-                    s->att_count, s->status, s->trace, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
+                    s->att_count, s->status, s->trace, s->xx, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
                     s->s_att, s->s_o, s->s_h, s->s_part};
     for (void *p : ptrs) free_dev(p);
     delete s;
@@ -724,17 +818,30 @@ int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_
     TH_HIP(hipMemcpyAsync(s->step, &init, sizeof init, hipMemcpyHostToDevice, st));
     TH_HIP(hipStreamSynchronize(st));  // `init` is a stack temporary
     const char *mode = getenv("TITANIA_DECODE");
-    if (s->persistent) {
+    if (mode && strcmp(mode, "xcd") == 0 && !s->xcd)
+        return fail(TH_ERR_INVALID, "TITANIA_DECODE=xcd: the XCD-parallel kernel does not support this model's shape");
+    if (s->xcd) {
+        TRY(decode_xcd(s, steps));
+    } else if (s->persistent) {
         TRY(decode_persistent(s, steps));
     } else if (mode && strcmp(mode, "eager") == 0 && s->step_fused) {
         // The same step kernels launched one by one (no graph): for profilers
         // that do not follow graph launches.
-        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0));
+        s->graph_keep = out_logits != nullptr;
+        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0, step_embed(s)));
         for (size_t i = 0; i < steps; ++i) TRY(enqueue_step(s));
     } else {
+        // The captured step copies out the logits only if this call wants them.
+        if (s->graph_exec && s->graph_keep != (out_logits != nullptr)) {
+            TH_HIP(hipGraphExecDestroy(s->graph_exec));
+            TH_HIP(hipGraphDestroy(s->graph));
+            s->graph_exec = nullptr;
+            s->graph = nullptr;
+        }
+        s->graph_keep = out_logits != nullptr;
         TRY(capture_step(s));
         // The first pick comes from the logits the last forward left.
-        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0));
+        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0, step_embed(s)));
         for (size_t i = 0; i < steps; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
     }
     TH_HIP(hipMemcpyAsync(out_tokens, s->tokens_dev, steps * sizeof(uint32_t), hipMemcpyDeviceToHost, st));

@@ -272,6 +272,18 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPK;
     const int split = blockIdx.x % a.nsplit, g = blockIdx.x / a.nsplit;
     const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
+    const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
+    const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
+    auto stage = [&](long long c0, int rows) {
+        const int chunks = rows * ROW16;
+        const uint4 *ks = reinterpret_cast<const uint4 *>(kc + c0 * HD);
+        const uint4 *vs = reinterpret_cast<const uint4 *>(vc + c0 * HD);
+        for (int base = wave * 64; base < chunks; base += kThreads)
+            if (base + lane < chunks) {
+                dma16(ks + base + lane, kst + base);
+                dma16(vs + base + lane, vst + base);
+            }
+    };
     // Everything that does not depend on the position is requested first: the
     // raw q heads and k of this wave (lane holds the pair (lane, lane + HD/2)),
     // their RMSNorm gains and this thread's element of v.
@@ -298,25 +310,12 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
     const long long chunk = ((len + a.nsplit - 1) / a.nsplit + 15) / 16 * 16;
     const long long s0 = (long long)split * chunk;
     const long long s1 = s0 + chunk < len ? s0 + chunk : len;
-    const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
-    const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
-
-    auto stage = [&](long long c0, int ncache) {
-        const int chunks = ncache * ROW16;
-        const uint4 *ks = reinterpret_cast<const uint4 *>(kc + c0 * HD);
-        const uint4 *vs = reinterpret_cast<const uint4 *>(vc + c0 * HD);
-        for (int base = wave * 64; base < chunks; base += kThreads)
-            if (base + lane < chunks) {
-                dma16(ks + base + lane, kst + base);
-                dma16(vs + base + lane, vst + base);
-            }
-    };
     auto cached_in = [&](long long c0, int cnt) -> int {
         const long long nc = pos - c0;
         return nc <= 0 ? 0 : (nc < cnt ? (int)nc : cnt);
     };
     // Then, once pos is known, the rotation of this position and the first
-    // pass's cached rows; all of it is one memory round trip.
+    // pass's cached rows: one more memory round trip.
     const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
     {
         const int cnt0 = (int)(s1 - s0 < kStageRows ? s1 - s0 : kStageRows);
