@@ -276,6 +276,26 @@ def test_prefill_attention(hip):
     assert_close(hip.read(out), expected, rel=1e-4, abs_=1e-5, what="prefill attention")
 
 
+@pytest.mark.parametrize("n,pos,H,KVH", [(33, 0, 16, 8), (512, 0, 16, 8), (64, 300, 32, 8), (8, 5, 4, 1)])
+def test_prefill_attention_tiles(hip, n, pos, H, KVH):
+    """The query-tiled prefill kernel: a ragged tile, a 512-token prompt, a
+    4-query-head group after a long prefix, the smallest tiled launch."""
+    hd = 128
+    L = pos + n
+    kv = bf16_to_f32(normal_bf16(L * KVH * hd, n, "tk"))
+    vv = bf16_to_f32(normal_bf16(L * KVH * hd, n, "tv"))
+    q = bf16_to_f32(normal_bf16(n * H * hd, n, "tq"))
+    expected = ref.attention(q, kv, vv, pos, H, hd, KVH)
+    bk, bv, bq, out = hip.alloc(kv.size), hip.alloc(vv.size), hip.alloc(q.size), hip.alloc(q.size)
+    hip.write(bk, kv)
+    hip.write(bv, vv)
+    hip.write(bq, q)
+    hip.attention(out, bq, bk, bv, pos, H, hd, KVH)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-5
+    assert_close(got, expected, rel=1e-4, abs_=1e-5, what=f"prefill attention n={n} pos={pos}")
+
+
 # ---- fused extensions ----
 
 def test_add_rmsnorm(hip):

@@ -19,6 +19,7 @@ namespace th {
 
 constexpr int kAttnMaxGroup = 8;   // query heads per KV head
 constexpr int kAttnSub = 256;      // positions scored per sub-chunk
+constexpr size_t kAttnTileMin = 8; // tokens from which a launch uses the query-tiled kernel
 
 template <typename KV>
 __device__ __forceinline__ void load8(const KV *p, float f[8]);
@@ -225,6 +226,123 @@ hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc,
     return hipGetLastError();
 }
 
+// Prefill (several tokens, head_dim 128): one block per (tile of QT
+// consecutive tokens, query head). The block stages the tile's queries once and
+// walks the KV head's positions in tiles of KT rows staged in LDS, so each key
+// and value row is read once per query tile rather than once per token. Thread
+// t scores key t % 32 against queries 4 (t / 32) .. +3, the 32 lanes of a
+// half-wave that share those queries reduce the row statistics with shuffles
+// (online softmax, the causal mask per query), and the same thread then
+// accumulates dims 4 (t % 32) .. +3 of those queries' outputs. All arithmetic
+// is f32.
+constexpr int kQT = 32, kKT = 32;
+
+__device__ __forceinline__ float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ float4 load4(const uint16_t *p) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+}
+
+template <typename KV>
+__global__ __launch_bounds__(256) void attn_tile_kernel(AttnKernelArgs a, int n) {
+    constexpr int HD = 128, QS = HD + 4;  // padded row stride of the Q and K tiles
+    __shared__ float qs[kQT * QS];
+    __shared__ float ks[kKT * QS];
+    __shared__ float vs[kKT * HD];
+    __shared__ float ps[kQT * kKT];
+    const int tid = threadIdx.x;
+    const int h = blockIdx.y, g = h / a.group;
+    const int t0 = blockIdx.x * kQT;
+    const int nq = n - t0 < kQT ? n - t0 : kQT;
+    const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
+    for (int i = tid; i < kQT * HD / 4; i += 256) {
+        const int row = i / (HD / 4), c4 = i % (HD / 4);
+        const float4 v = row < nq ? load4(a.q + ((long long)(t0 + row) * a.n_heads + h) * HD + c4 * 4)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4 *>(qs + row * QS + c4 * 4) = v;
+    }
+    const KV *kb = reinterpret_cast<const KV *>(a.k) + (long long)g * a.head_stride;
+    const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
+    const int j = tid & 31, qi0 = (tid >> 5) * 4, d0 = (tid & 31) * 4;
+    float m[4], l[4], acc[4][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        m[q] = -INFINITY;
+        l[q] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[q][e] = 0.f;
+    }
+    const long long last = pos + t0 + nq - 1;  // the last position a query of the tile attends
+    for (long long c0 = 0; c0 <= last; c0 += kKT) {
+        __syncthreads();  // the previous tile's rows are consumed (and the queries stored)
+        for (int i = tid; i < kKT * HD / 4; i += 256) {
+            const int row = i / (HD / 4), c4 = i % (HD / 4);
+            const long long p = c0 + row;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (p <= last) {
+                kv = load4(kb + p * a.pos_stride + c4 * 4);
+                vv = load4(vb + p * a.pos_stride + c4 * 4);
+            }
+            *reinterpret_cast<float4 *>(ks + row * QS + c4 * 4) = kv;
+            *reinterpret_cast<float4 *>(vs + row * HD + c4 * 4) = vv;
+        }
+        __syncthreads();
+        float sc[4] = {0.f, 0.f, 0.f, 0.f};
+        const float *kr = ks + j * QS;
+#pragma unroll 8
+        for (int c = 0; c < HD; c += 4) {
+            const float4 kk = *reinterpret_cast<const float4 *>(kr + c);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 qv = *reinterpret_cast<const float4 *>(qs + (qi0 + q) * QS + c);
+                sc[q] = fmaf(qv.x, kk.x, sc[q]);
+                sc[q] = fmaf(qv.y, kk.y, sc[q]);
+                sc[q] = fmaf(qv.z, kk.z, sc[q]);
+                sc[q] = fmaf(qv.w, kk.w, sc[q]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const long long qp = pos + t0 + qi0 + q;  // the query's position
+            const bool valid = qi0 + q < nq && c0 + j <= qp;
+            const float sv = valid ? a.scale * sc[q] : -INFINITY;
+            float mx = sv;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+            const float mn = fmaxf(m[q], mx);
+            const float pv = sv == -INFINITY ? 0.f : expf(sv - mn);
+            float sum = pv;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+            const float al = m[q] == -INFINITY ? 0.f : expf(m[q] - mn);
+            l[q] = l[q] * al + sum;
+            m[q] = mn;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[q][e] *= al;
+            ps[(qi0 + q) * kKT + j] = pv;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int jj = 0; jj < kKT; ++jj) {
+            const float4 v4 = *reinterpret_cast<const float4 *>(vs + jj * HD + d0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float pj = ps[(qi0 + q) * kKT + jj];
+                acc[q][0] = fmaf(pj, v4.x, acc[q][0]);
+                acc[q][1] = fmaf(pj, v4.y, acc[q][1]);
+                acc[q][2] = fmaf(pj, v4.z, acc[q][2]);
+                acc[q][3] = fmaf(pj, v4.w, acc[q][3]);
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if (qi0 + q < nq) {
+            float4 o = make_float4(acc[q][0] / l[q], acc[q][1] / l[q], acc[q][2] / l[q], acc[q][3] / l[q]);
+            *reinterpret_cast<float4 *>(a.out + ((long long)(t0 + qi0 + q) * a.n_heads + h) * HD + d0) = o;
+        }
+}
+
 template <int HD>
 static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
     dim3 grid((unsigned)(n * (size_t)k.n_kv_heads * (size_t)k.nsplit));
@@ -241,6 +359,14 @@ static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
 
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim) {
     if (n == 0) return hipSuccess;
+    if (head_dim == 128 && n >= kAttnTileMin) {
+        dim3 grid((unsigned)((n + kQT - 1) / kQT), (unsigned)k.n_heads);
+        if (k.kv_bf16)
+            attn_tile_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
+        else
+            attn_tile_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
+        return hipGetLastError();
+    }
     switch (head_dim) {
     case 64: return attn_launch<64>(s, k, n);
     case 128: return attn_launch<128>(s, k, n);

@@ -35,7 +35,7 @@ struct StepState {
     long long pos;         // position of the token to feed next
     long long step;        // tokens fed so far in this decode call
     uint32_t token;        // token to feed next
-    uint32_t pad;
+    uint32_t epoch;        // decode steps ever advanced on this state (tags exchange words)
     uint32_t *tokens_out;  // picks, indexed by step
     float *logits_out;     // logits after each fed token, or null
 };

@@ -130,6 +130,7 @@ __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__
         if (advance) {
             st->pos += 1;
             st->step += 1;
+            st->epoch += 1;
         }
         st->token = tok;
         if (st->tokens_out) st->tokens_out[st->step] = tok;

@@ -96,6 +96,9 @@ struct th_state {
     float *sx_a = nullptr, *sx_b = nullptr, *s_y = nullptr, *s_qkv = nullptr, *s_att = nullptr, *s_o = nullptr,
           *s_h = nullptr;
     uint64_t *s_part = nullptr;
+    unsigned long long *s_words = nullptr;  // q/k/v words of the single-launch q/k/v + attention
+    unsigned *s_err = nullptr;              // its attention blocks whose poll gave up
+    uint32_t step_epoch = 0;                // StepState::epoch at the next decode call
     bool graph_keep = false;                // whether the captured step copies out the logits
     unsigned long long *trace = nullptr;  // per-phase ticks of the last decode (TITANIA_TRACE steps)
     int trace_steps = 0;
@@ -331,6 +334,10 @@ int ensure_fused_state(th_state *s) {
                   {&s->s_o, H}, {&s->s_h, I}};
         for (auto &b : sb) TH_HIP(hipMalloc(b.p, b.n * sizeof(float)));
         TH_HIP(hipMalloc(&s->s_part, (size_t)th::step_logits_partials((int)c.vocab_size) * sizeof(uint64_t)));
+        TH_HIP(hipMalloc(&s->s_words, (qd + 2 * kvd) * sizeof(unsigned long long)));
+        TH_HIP(hipMemset(s->s_words, 0, (qd + 2 * kvd) * sizeof(unsigned long long)));
+        TH_HIP(hipMalloc(&s->s_err, sizeof(unsigned)));
+        TH_HIP(hipMemset(s->s_err, 0, sizeof(unsigned)));
 
     }
     return ensure_persistent(s);
@@ -361,6 +368,8 @@ int enqueue_step(th_state *s) {
     const int nsplit = th::attention_splits(1, (size_t)nkv, s->max_len);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
+    // One launch for q/k/v and attention while one split covers the context.
+    const bool fuse_attn = nsplit == 1 && th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64;
     // sx_b holds the token's embedding row: the previous pick wrote it.
     const float *y_prev = nullptr;
     for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -395,9 +404,21 @@ int enqueue_step(th_state *s) {
         a.out = s->s_att;
         a.part_acc = s->attn_part;
         a.part_ml = s->attn_part ? s->attn_part + (size_t)nh * nsplit * hd : nullptr;
-        TH_HIP(th::launch_step_qkv(st, q));
-        TH_HIP(th::launch_step_attention(st, a));
-        if (nsplit > 1) TH_HIP(th::launch_attn_combine(st, s->s_att, a.part_acc, a.part_ml, (size_t)nh, nsplit, hd));
+        if (fuse_attn) {
+            th::StepQkvAttnArgs f{};
+            f.qkv = q;
+            f.at = a;
+            f.words = s->s_words;
+            f.err = s->s_err;
+            f.st = s->step;
+            f.layer = (int)l;
+            TH_HIP(th::launch_step_qkv_attn(st, f));
+        } else {
+            TH_HIP(th::launch_step_qkv(st, q));
+            TH_HIP(th::launch_step_attention(st, a));
+            if (nsplit > 1)
+                TH_HIP(th::launch_attn_combine(st, s->s_att, a.part_acc, a.part_ml, (size_t)nh, nsplit, hd));
+        }
         TH_HIP(th::launch_step_gemv(st, L.o->ptr, H, qd, s->s_att, s->s_o));
         TH_HIP(th::launch_step_gate_up(st, L.gate->ptr, L.up->ptr, I, H, s->sx_a, s->s_o, L.mlp_norm->ptr, eps,
                                        s->sx_b, s->s_h));
@@ -751,7 +772,7 @@ void th_state_destroy(th_state *s) {
                     s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
                     s->step,    s->tokens_dev, s->logits_dev, s->dev_layers, s->xchg, s->att_part,
                     s->att_count, s->status, s->trace, s->xx, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
-                    s->s_att, s->s_o, s->s_h, s->s_part};
+                    s->s_att, s->s_o, s->s_h, s->s_part, s->s_words, s->s_err};
     for (void *p : ptrs) free_dev(p);
     delete s;
 }
@@ -815,6 +836,7 @@ int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_
     init.step = 0;
     init.tokens_out = s->tokens_dev;
     init.logits_out = out_logits ? s->logits_dev : nullptr;
+    init.epoch = s->step_epoch;
     TH_HIP(hipMemcpyAsync(s->step, &init, sizeof init, hipMemcpyHostToDevice, st));
     TH_HIP(hipStreamSynchronize(st));  // `init` is a stack temporary
     const char *mode = getenv("TITANIA_DECODE");
@@ -844,10 +866,15 @@ int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_
         TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0, step_embed(s)));
         for (size_t i = 0; i < steps; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
     }
+    s->step_epoch += (uint32_t)steps;
     TH_HIP(hipMemcpyAsync(out_tokens, s->tokens_dev, steps * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     if (out_logits)
         TH_HIP(hipMemcpyAsync(out_logits, s->logits_dev, steps * vocab * sizeof(float), hipMemcpyDeviceToHost, st));
+    unsigned poll_failures = 0;
+    if (s->s_err) TH_HIP(hipMemcpyAsync(&poll_failures, s->s_err, sizeof poll_failures, hipMemcpyDeviceToHost, st));
     TH_HIP(hipStreamSynchronize(st));
+    if (poll_failures)
+        return fail(TH_ERR_HIP, "decode: %u attention blocks gave up waiting for their q/k/v", poll_failures);
     return TH_OK;
 }
 

@@ -60,6 +60,22 @@ struct StepAttnArgs {
 
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a);
 
+// The q/k/v GEMV (as launch_step_qkv) and single-split attention in one launch:
+// the GEMV blocks publish the rows as (value | epoch << 32) words, epoch =
+// st->epoch * 64 + layer + 1; one extra block per KV head stages its cached
+// rows meanwhile, then attends from the words. For contexts one split covers.
+struct StepQkvAttnArgs {
+    StepQkvArgs qkv;               // x_out as launch_step_qkv; qkv unused
+    StepAttnArgs at;               // qkv and partials unused, nsplit 1
+    unsigned long long *words;     // [q_rows + 2 kv_rows]
+    unsigned *err;                 // counts attention blocks whose poll gave up
+    const StepState *st;
+    int layer;
+};
+
+bool step_qkv_attn_supported(int hidden, int n_heads, int n_kv_heads);
+hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &a);
+
 __device__ __forceinline__ void kv_load8(const float *p, float f[8]) {
     const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
     f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;

@@ -253,24 +253,30 @@ __device__ __forceinline__ void lds_row8(const uint16_t *row, int sub, float f[8
 __device__ __forceinline__ float lds_at(const float *row, int d) { return row[d]; }
 __device__ __forceinline__ float lds_at(const uint16_t *row, int d) { return bf16_to_f32(row[d]); }
 
-// One block per (KV head, split of the positions 0..pos): the group's q heads
-// and the new k are RMSNorm'd and rotated in LDS, the split holding pos
-// appends k and v to the caches, and cached K/V rows are staged into LDS 64
-// positions at a time (all loads of a pass in flight together) for scores,
-// online softmax and the weighted sum of values.
-template <int HD, int G, typename KV>
-__global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a) {
+// Attention of one (KV head g, split of the positions 0..pos) by one block:
+// the group's q heads and the new k are RMSNorm'd and rotated in LDS, the split
+// holding pos appends k and v to the caches, and cached K/V rows are staged
+// into LDS 64 positions at a time (all loads of a pass in flight together) for
+// scores, online softmax and the weighted sum of values.
+//
+// The raw q/k/v come from a.qkv, or (WORDS) from (value | epoch << 32) words
+// that other blocks of the same launch are writing: then the block first
+// stages the cached rows (they do not depend on the q/k/v), then polls until
+// every word it needs carries `epoch` (bounded: about 2 s, then *err counts
+// the failure and the block goes on with what it has).
+template <int HD, int G, typename KV, bool WORDS, int ROWS>
+__device__ __forceinline__ void attend(const StepAttnArgs &a, int g, int split, const unsigned long long *words,
+                                       unsigned epoch, unsigned *err) {
     constexpr int LPK = HD / 8, KPW = 64 / LPK, KPB = kWaves * KPW, NP = kThreads / HD;
     constexpr int ROW16 = HD * (int)sizeof(KV) / 16;  // 16-byte chunks per cached row
     __shared__ float hq[G * HD], hk[HD], hv[HD];
-    __shared__ float scores[G][kStageRows];
+    __shared__ float scores[G][ROWS];
     __shared__ float st_m[G], st_l[G], st_a[G];
     __shared__ float red[G][kThreads];
-    __shared__ uint4 kst[kStageRows * ROW16], vst[kStageRows * ROW16];
+    __shared__ uint4 kst[ROWS * ROW16], vst[ROWS * ROW16];
     static_assert(HD == 128, "one rotation pair per lane");
     constexpr int HALF = HD / 2, HPW = (G + 1 + kWaves - 1) / kWaves;  // heads (q..., k) per wave
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPK;
-    const int split = blockIdx.x % a.nsplit, g = blockIdx.x / a.nsplit;
     const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
     const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
     const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
@@ -284,27 +290,31 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
                 dma16(vs + base + lane, vst + base);
             }
     };
-    // Everything that does not depend on the position is requested first: the
-    // raw q heads and k of this wave (lane holds the pair (lane, lane + HD/2)),
-    // their RMSNorm gains and this thread's element of v.
+    // The raw q heads and k of this wave (lane holds the pair (lane, lane +
+    // HD/2)), their RMSNorm gains and this thread's element of v; from a.qkv
+    // they are requested first, with everything else that does not depend on
+    // the position.
     float av[HPW], bv[HPW], ga[HPW], gb[HPW];
+    float vnew = 0.f;
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
         const int h = wave + hh * kWaves;
         av[hh] = bv[hh] = 0.f;
         ga[hh] = gb[hh] = 1.f;
         if (h <= G) {
-            const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
             const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
-            av[hh] = x[lane];
-            bv[hh] = x[lane + HALF];
             if (gain) {
                 ga[hh] = bf16_to_f32(gain[lane]);
                 gb[hh] = bf16_to_f32(gain[lane + HALF]);
             }
+            if (!WORDS) {
+                const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
+                av[hh] = x[lane];
+                bv[hh] = x[lane + HALF];
+            }
         }
     }
-    const float vnew = tid < HD ? a.qkv[qd + kvd + (size_t)g * HD + tid] : 0.f;
+    if (!WORDS && tid < HD) vnew = a.qkv[qd + kvd + (size_t)g * HD + tid];
     const long long pos = *a.pos;
     const long long len = pos + 1;
     const long long chunk = ((len + a.nsplit - 1) / a.nsplit + 15) / 16 * 16;
@@ -318,8 +328,44 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
     // pass's cached rows: one more memory round trip.
     const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
     {
-        const int cnt0 = (int)(s1 - s0 < kStageRows ? s1 - s0 : kStageRows);
+        const int cnt0 = (int)(s1 - s0 < ROWS ? s1 - s0 : ROWS);
         if (s0 < s1) stage(s0, cached_in(s0, cnt0));
+    }
+    if (WORDS) {
+        for (int it = 0;; ++it) {
+            int ok = 1;
+            unsigned long long wa[HPW], wb[HPW], wv = 0;
+#pragma unroll
+            for (int hh = 0; hh < HPW; ++hh) {
+                const int h = wave + hh * kWaves;
+                if (h <= G) {
+                    const unsigned long long *x = h < G ? words + (size_t)(g * G + h) * HD : words + qd + (size_t)g * HD;
+                    wa[hh] = __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    wb[hh] = __hip_atomic_load(x + lane + HALF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            if (tid < HD)
+                wv = __hip_atomic_load(words + qd + kvd + (size_t)g * HD + tid, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int hh = 0; hh < HPW; ++hh) {
+                const int h = wave + hh * kWaves;
+                if (h <= G) {
+                    ok &= (unsigned)(wa[hh] >> 32) == epoch && (unsigned)(wb[hh] >> 32) == epoch;
+                    av[hh] = __uint_as_float((unsigned)wa[hh]);
+                    bv[hh] = __uint_as_float((unsigned)wb[hh]);
+                }
+            }
+            if (tid < HD) {
+                ok &= (unsigned)(wv >> 32) == epoch;
+                vnew = __uint_as_float((unsigned)wv);
+            }
+            if (__syncthreads_and(ok)) break;
+            if (it >= (1 << 21)) {
+                if (tid == 0) atomicAdd(err, 1u);
+                break;
+            }
+        }
     }
     if (tid < G) {
         st_m[tid] = -INFINITY;
@@ -355,8 +401,8 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
     float acc[G];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) acc[gg] = 0.f;
-    for (long long c0 = s0; c0 < s1; c0 += kStageRows) {
-        const int cnt = (int)(s1 - c0 < kStageRows ? s1 - c0 : kStageRows);
+    for (long long c0 = s0; c0 < s1; c0 += ROWS) {
+        const int cnt = (int)(s1 - c0 < ROWS ? s1 - c0 : ROWS);
         const int ncache = cached_in(c0, cnt);
         if (c0 != s0) {
             stage(c0, ncache);
@@ -437,6 +483,73 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
                 a.part_ml[slot * 2 + 1] = st_l[gg];
             }
         }
+    }
+}
+
+template <int HD, int G, typename KV>
+__global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a) {
+    attend<HD, G, KV, false, kStageRows>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, nullptr, 0, nullptr);
+}
+
+// The q/k/v rows of launch_step_qkv (two per wave) published as epoch words by
+// the first blocks, and after them one block per KV head that attends for its
+// group from those words. Blocks start in index order and the GEMV blocks
+// never wait, so the attention blocks' polls always end.
+template <int CPL, int G, typename KV>
+__global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
+    constexpr int RPW = 2, RPB = RPW * kWaves, HD = 128;
+    const int ngemv = (a.n_rows + RPB - 1) / RPB;
+    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
+    if ((int)blockIdx.x >= ngemv) {
+        // Half-size passes keep the launch's LDS per block low enough for all
+        // of its blocks to be resident at once.
+        attend<HD, G, KV, true, kStageRows / 2>(q.at, blockIdx.x - ngemv, 0, q.words, epoch, q.err);
+        return;
+    }
+    extern __shared__ float xs[];
+    __shared__ float red[kWaves];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int r0 = blockIdx.x * RPB + wave * RPW;
+    uint4 w[RPW][CPL];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const uint4 *p = row_at(a.rows, r0 + r < a.n_rows ? r0 + r : 0, a.cols);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) w[r][c] = p[c * 64 + lane];
+    }
+    build_input<true, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out, red);
+    float res[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) acc = dot8(xs, w[r][c], c * 64 + lane, acc);
+        res[r] = wave_sum_dpp(acc);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+        if (lane == r && r0 + r < a.n_rows)
+            __hip_atomic_store(q.words + r0 + r, ((unsigned long long)epoch << 32) | __float_as_uint(res[r]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int CPL, int G>
+hipError_t qkv_attn_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a) {
+    dim3 grid((unsigned)((a.n_rows + 7) / 8 + q.at.n_kv_heads));
+    const size_t lds = (size_t)a.cols * sizeof(float);
+    if (q.at.kv_bf16)
+        qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(q, a);
+    else
+        qkv_attn_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(q, a);
+    return hipGetLastError();
+}
+
+template <int CPL>
+hipError_t qkv_attn_g(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a) {
+    switch (q.at.n_heads / q.at.n_kv_heads) {
+    case 2: return qkv_attn_launch<CPL, 2>(s, q, a);
+    case 4: return qkv_attn_launch<CPL, 4>(s, q, a);
+    default: return hipErrorInvalidValue;
     }
 }
 
@@ -533,6 +646,38 @@ hipError_t launch_step_logits(hipStream_t s, const uint16_t *w, int vocab, int h
 }
 
 int step_logits_partials(int vocab) { return (vocab + 4 * kWaves - 1) / (4 * kWaves); }
+
+bool step_qkv_attn_supported(int hidden, int n_heads, int n_kv_heads) {
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads) return false;
+    const int g = n_heads / n_kv_heads, cpl = hidden / 512;
+    return hidden % 512 == 0 && (g == 2 || g == 4) && (cpl == 1 || cpl == 2 || cpl == 5);
+}
+
+hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
+    const StepQkvArgs &k = q.qkv;
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit != 1)
+        return hipErrorInvalidValue;
+    GemvArgs a{};
+    a.rows.base[0] = k.wq;
+    a.rows.count[0] = k.q_rows;
+    a.rows.base[1] = k.wk;
+    a.rows.count[1] = k.kv_rows;
+    a.rows.base[2] = k.wv;
+    a.rows.count[2] = k.kv_rows;
+    a.n_rows = k.q_rows + 2 * k.kv_rows;
+    a.cols = k.hidden;
+    a.a = k.x_prev;
+    a.b = k.y_prev;
+    a.gain = k.gain;
+    a.eps = k.eps;
+    a.x_out = k.x_out;
+    switch (k.hidden / 512) {
+    case 1: return qkv_attn_g<1>(s, q, a);
+    case 2: return qkv_attn_g<2>(s, q, a);
+    case 5: return qkv_attn_g<5>(s, q, a);
+    default: return hipErrorInvalidValue;
+    }
+}
 
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a) {
     switch (a.n_heads / a.n_kv_heads) {
