@@ -273,20 +273,33 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnKernelArgs a, int n)
         for (int e = 0; e < 4; ++e) acc[q][e] = 0.f;
     }
     const long long last = pos + t0 + nq - 1;  // the last position a query of the tile attends
+    // Key/value rows travel through registers one tile ahead: the loads of
+    // tile c0 + KT are in flight while tile c0 is scored.
+    constexpr int PER = kKT * HD / 4 / 256;  // float4 of K (and of V) per thread per tile
+    float4 kr4[PER], vr4[PER];
+    auto fetch = [&](long long c0) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
+            const long long p = c0 + row;
+            kr4[u] = vr4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p <= last) {
+                kr4[u] = load4(kb + p * a.pos_stride + c4 * 4);
+                vr4[u] = load4(vb + p * a.pos_stride + c4 * 4);
+            }
+        }
+    };
+    fetch(0);
     for (long long c0 = 0; c0 <= last; c0 += kKT) {
         __syncthreads();  // the previous tile's rows are consumed (and the queries stored)
-        for (int i = tid; i < kKT * HD / 4; i += 256) {
-            const int row = i / (HD / 4), c4 = i % (HD / 4);
-            const long long p = c0 + row;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (p <= last) {
-                kv = load4(kb + p * a.pos_stride + c4 * 4);
-                vv = load4(vb + p * a.pos_stride + c4 * 4);
-            }
-            *reinterpret_cast<float4 *>(ks + row * QS + c4 * 4) = kv;
-            *reinterpret_cast<float4 *>(vs + row * HD + c4 * 4) = vv;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
+            *reinterpret_cast<float4 *>(ks + row * QS + c4 * 4) = kr4[u];
+            *reinterpret_cast<float4 *>(vs + row * HD + c4 * 4) = vr4[u];
         }
         __syncthreads();
+        if (c0 + kKT <= last) fetch(c0 + kKT);
         float sc[4] = {0.f, 0.f, 0.f, 0.f};
         const float *kr = ks + j * QS;
 #pragma unroll 8

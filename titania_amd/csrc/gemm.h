@@ -6,6 +6,8 @@
 #include <cstddef>
 #include <cstdint>
 
+#include <algorithm>
+
 namespace th {
 
 // Batches of at least this many tokens go to the MFMA GEMM.
@@ -17,5 +19,20 @@ bool gemm_supported(size_t rows, size_t cols);
 // out[t*rows + r] = w[r] . x[t] for t < n, on the matrix cores.
 hipError_t launch_gemm(hipStream_t s, float *out, const uint16_t *w, size_t rows, size_t cols, const float *x,
                        size_t n);
+
+// One weight matrix of a multi-matrix GEMM: out[t*rows + r] = w[r] . x[t].
+struct GemmOut {
+    const uint16_t *w;
+    size_t rows;
+    float *out;
+};
+
+// Bytes of scratch launch_gemm_multi needs for n tokens of `cols` columns.
+size_t gemm_scratch_bytes(size_t n, size_t cols);
+
+// Up to three matrices that share the input x [n][cols], in two launches (the
+// activation split into `scratch`, then one GEMM over all their rows).
+hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t cols, const GemmOut *outs, int n_outs,
+                             void *scratch);
 
 }  // namespace th

@@ -19,6 +19,7 @@
 #include "common.h"
 #include "decode.h"
 #include "fused.h"
+#include "gemm.h"
 #include "step.h"
 #include "xdecode.h"
 
@@ -61,6 +62,8 @@ struct th_state {
     size_t fb = 0;  // token capacity of the fused buffers
     float *fx = nullptr, *fxb = nullptr, *fq = nullptr, *fk = nullptr, *fv = nullptr, *fatt = nullptr,
           *fgate = nullptr, *fup = nullptr, *fy = nullptr;
+    void *fsplit = nullptr;   // bf16 hi/lo halves of a GEMM input (fb tokens x fsplit_cols)
+    size_t fsplit_cols = 0;
     void *kv = nullptr;  // all caches, one allocation
     size_t kv_elem = 4;
     float *attn_part = nullptr;  // attention partials for the fused path
@@ -310,6 +313,10 @@ int ensure_fused_state(th_state *s) {
     } bufs[] = {{&s->fx, H}, {&s->fxb, H}, {&s->fq, qd}, {&s->fk, kvd}, {&s->fv, kvd},
                 {&s->fatt, qd}, {&s->fgate, I}, {&s->fup, I}, {&s->fy, H}};
     for (auto &b : bufs) TH_HIP(hipMalloc(b.p, s->fb * b.n * sizeof(float)));
+    if (s->fb >= th::kGemmMinTokens) {
+        s->fsplit_cols = std::max(std::max(H, qd), I);
+        TH_HIP(hipMalloc(&s->fsplit, th::gemm_scratch_bytes(s->fb, s->fsplit_cols)));
+    }
     s->kv_elem = s->kv_dtype == TH_KV_BF16 ? 2 : 4;
     size_t kv_bytes = (size_t)c.num_hidden_layers * 2 * kvd * s->max_len * s->kv_elem;
     TH_HIP(hipMalloc(&s->kv, kv_bytes));
@@ -451,15 +458,23 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
     const int nsplit = th::attention_splits(n, nkv, max_ctx);
     if (th::attention_scratch(n, nh, hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
+    // Chunks of kGemmMinTokens or more go through the MFMA GEMM (activations
+    // split once per input into fsplit).
+    auto use_gemm = [&](size_t cols) { return n >= th::kGemmMinTokens && s->fsplit && cols <= s->fsplit_cols; };
 
     TH_HIP(th::launch_embed(st, s->fx, m->embed->ptr, H, tokens, n));
     for (size_t i = 0; i < m->layers.size(); ++i) {
         const Layer &L = m->layers[i];
         // Residual add of the previous layer's MLP output, then the attention norm.
         TH_HIP(th::launch_add_rmsnorm(st, s->fx, i ? s->fy : nullptr, s->fxb, n, L.attn_norm->ptr, H, eps));
-        TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
-        TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
-        TH_HIP(th::launch_matmul(st, s->fv, L.v->ptr, nkv * hd, H, s->fxb, n));
+        if (use_gemm(H) && th::gemm_supported(qd, H) && th::gemm_supported(nkv * hd, H)) {
+            const th::GemmOut o[3] = {{L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
+            TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 3, s->fsplit));
+        } else {
+            TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
+            TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
+            TH_HIP(th::launch_matmul(st, s->fv, L.v->ptr, nkv * hd, H, s->fxb, n));
+        }
         th::QkvPostArgs qa{};
         qa.q = s->fq;
         qa.k = s->fk;
@@ -500,12 +515,27 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         aa.part_ml = s->attn_part ? s->attn_part + n * nh * (size_t)nsplit * hd : nullptr;
         TH_HIP(th::launch_attention(st, aa, n, hd));
 
-        TH_HIP(th::launch_matmul(st, s->fy, L.o->ptr, H, qd, s->fatt, n));
+        if (use_gemm(qd) && th::gemm_supported(H, qd)) {
+            const th::GemmOut o{L.o->ptr, H, s->fy};
+            TH_HIP(th::launch_gemm_multi(st, s->fatt, n, qd, &o, 1, s->fsplit));
+        } else {
+            TH_HIP(th::launch_matmul(st, s->fy, L.o->ptr, H, qd, s->fatt, n));
+        }
         TH_HIP(th::launch_add_rmsnorm(st, s->fx, s->fy, s->fxb, n, L.mlp_norm->ptr, H, eps));
-        TH_HIP(th::launch_matmul(st, s->fgate, L.gate->ptr, I, H, s->fxb, n));
-        TH_HIP(th::launch_matmul(st, s->fup, L.up->ptr, I, H, s->fxb, n));
+        if (use_gemm(H) && th::gemm_supported(I, H)) {
+            const th::GemmOut o[2] = {{L.gate->ptr, I, s->fgate}, {L.up->ptr, I, s->fup}};
+            TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 2, s->fsplit));
+        } else {
+            TH_HIP(th::launch_matmul(st, s->fgate, L.gate->ptr, I, H, s->fxb, n));
+            TH_HIP(th::launch_matmul(st, s->fup, L.up->ptr, I, H, s->fxb, n));
+        }
         TH_HIP(th::launch_silu_mul(st, s->fgate, s->fup, n * I));
-        TH_HIP(th::launch_matmul(st, s->fy, L.down->ptr, H, I, s->fgate, n));
+        if (use_gemm(I) && th::gemm_supported(H, I)) {
+            const th::GemmOut o{L.down->ptr, H, s->fy};
+            TH_HIP(th::launch_gemm_multi(st, s->fgate, n, I, &o, 1, s->fsplit));
+        } else {
+            TH_HIP(th::launch_matmul(st, s->fy, L.down->ptr, H, I, s->fgate, n));
+        }
     }
     // Only the last token's logits are wanted (model.rs:143-147).
     float *xl = s->fx + (n - 1) * H;
@@ -772,7 +802,7 @@ void th_state_destroy(th_state *s) {
                     s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
                     s->step,    s->tokens_dev, s->logits_dev, s->dev_layers, s->xchg, s->att_part,
                     s->att_count, s->status, s->trace, s->xx, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
-                    s->s_att, s->s_o, s->s_h, s->s_part, s->s_words, s->s_err};
+                    s->s_att, s->s_o, s->s_h, s->s_part, s->s_words, s->s_err, s->fsplit};
     for (void *p : ptrs) free_dev(p);
     delete s;
 }
