@@ -53,6 +53,35 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// v from another lane of the same 16-lane row (or across rows for the
+// row_bcast controls); lanes whose row is not in ROW_MASK get `old`.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_get(float v, float old) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over each 16-lane row, left in every lane of the row (the association
+// differs between lanes, so callers use one lane's value).
+__device__ __forceinline__ float row_sum_dpp(float v) {
+    v += dpp_get<0xB1>(v, 0.f);   // quad_perm [1,0,3,2]
+    v += dpp_get<0x4E>(v, 0.f);   // quad_perm [2,3,0,1]
+    v += dpp_get<0x124>(v, 0.f);  // row_ror:4
+    v += dpp_get<0x128>(v, 0.f);  // row_ror:8
+    return v;
+}
+
+// Wave64 maximum through DPP, returned to every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_get<0xB1>(v, -INFINITY));
+    v = fmaxf(v, dpp_get<0x4E>(v, -INFINITY));
+    v = fmaxf(v, dpp_get<0x124>(v, -INFINITY));
+    v = fmaxf(v, dpp_get<0x128>(v, -INFINITY));
+    v = fmaxf(v, dpp_get<0x142, 0xa>(v, -INFINITY));  // row_bcast:15
+    v = fmaxf(v, dpp_get<0x143, 0xc>(v, -INFINITY));  // row_bcast:31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

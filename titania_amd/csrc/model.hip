@@ -319,7 +319,9 @@ int ensure_fused_state(th_state *s) {
     }
     s->kv_elem = s->kv_dtype == TH_KV_BF16 ? 2 : 4;
     size_t kv_bytes = (size_t)c.num_hidden_layers * 2 * kvd * s->max_len * s->kv_elem;
-    TH_HIP(hipMalloc(&s->kv, kv_bytes));
+    // Tail rows that the decode step's attention may read (and ignore) past
+    // the last head's max_len positions.
+    TH_HIP(hipMalloc(&s->kv, kv_bytes + (size_t)th::kStepKvTailRows * hd * sizeof(float)));
     // Attention partials: enough for any chunk of up to fb tokens at any context
     // up to max_len (the split count only grows with the context).
     s->attn_part_floats = 0;
@@ -341,6 +343,7 @@ int ensure_fused_state(th_state *s) {
                   {&s->s_o, H}, {&s->s_h, I}};
         for (auto &b : sb) TH_HIP(hipMalloc(b.p, b.n * sizeof(float)));
         TH_HIP(hipMalloc(&s->s_part, (size_t)th::step_logits_partials((int)c.vocab_size) * sizeof(uint64_t)));
+        // Zeroed: epoch 0 precedes every epoch a step uses.
         TH_HIP(hipMalloc(&s->s_words, (qd + 2 * kvd) * sizeof(unsigned long long)));
         TH_HIP(hipMemset(s->s_words, 0, (qd + 2 * kvd) * sizeof(unsigned long long)));
         TH_HIP(hipMalloc(&s->s_err, sizeof(unsigned)));

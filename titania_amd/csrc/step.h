@@ -73,6 +73,11 @@ struct StepQkvAttnArgs {
     int layer;
 };
 
+// The attention blocks of launch_step_qkv_attn read cached rows in passes of
+// up to this many positions without clamping to the context: the caches'
+// allocation must extend this many rows (of head_dim f32) past the last head.
+constexpr int kStepKvTailRows = 128;
+
 bool step_qkv_attn_supported(int hidden, int n_heads, int n_kv_heads);
 hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &a);
 

@@ -18,117 +18,11 @@
 #include "common.h"
 #include "device_util.h"
 #include "step.h"
+#include "step_dev.h"
 
 namespace th {
 
 namespace {
-
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
-
-// Builds the block's f32 input in LDS: x = a (+ b), optionally RMSNorm'd with
-// gain g (model/cpu.rs:85-94); block 0 keeps the un-normalized sum in x_out.
-// Every thread issues all its loads (NV float4 of a, of b
-// and 4-element groups of g) before using any, so the input costs one memory
-// round trip rather than one per loop iteration.
-template <bool NORM, int NV>
-__device__ __forceinline__ void build_input(float *xs, const float *a, const float *b, int n, const uint16_t *g,
-                                            float eps, float *x_out, float *red) {
-    const int tid = threadIdx.x;
-    const int n4 = n >> 2;
-    const float4 *a4 = reinterpret_cast<const float4 *>(a);
-    const float4 *b4 = reinterpret_cast<const float4 *>(b);
-    const uint2 *g4 = reinterpret_cast<const uint2 *>(g);
-    float4 va[NV], vb[NV];
-    uint2 vg[NV];
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int i = tid + k * kThreads;
-        if (i < n4) {
-            va[k] = a4[i];
-            if (b) vb[k] = b4[i];
-            if (NORM) vg[k] = g4[i];
-        }
-    }
-    float ss = 0.f;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int i = tid + k * kThreads;
-        if (i < n4) {
-            float4 v = va[k];
-            if (b) {
-                v.x = v.x + vb[k].x;
-                v.y = v.y + vb[k].y;
-                v.z = v.z + vb[k].z;
-                v.w = v.w + vb[k].w;
-            }
-            va[k] = v;
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            if (!NORM) reinterpret_cast<float4 *>(xs)[i] = v;
-        }
-    }
-    if (x_out && blockIdx.x == 0) {  // every block holds the sum; the first keeps it
-#pragma unroll
-        for (int k = 0; k < NV; ++k) {
-            const int i = tid + k * kThreads;
-            if (i < n4) reinterpret_cast<float4 *>(x_out)[i] = va[k];
-        }
-    }
-    if (!NORM) {
-        __syncthreads();
-        return;
-    }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    float total = 0.f;
-    for (int w = 0; w < kWaves; ++w) total += red[w];
-    const float scale = 1.0f / sqrtf(total / (float)n + eps);
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int i = tid + k * kThreads;
-        if (i < n4) {
-            float4 v = va[k];
-            v.x = v.x * (scale * bf16_lo(vg[k].x));
-            v.y = v.y * (scale * bf16_hi(vg[k].x));
-            v.z = v.z * (scale * bf16_lo(vg[k].y));
-            v.w = v.w * (scale * bf16_hi(vg[k].y));
-            reinterpret_cast<float4 *>(xs)[i] = v;
-        }
-    }
-    __syncthreads();
-}
-
-__device__ __forceinline__ float dot8(const float *xs, const uint4 &w, int col, float acc) {
-    const float4 *x4 = reinterpret_cast<const float4 *>(xs) + col * 2;
-    const float4 a = x4[0], b = x4[1];
-    float wf[8];
-    unpack8(w, wf);
-    acc = fmaf(wf[0], a.x, acc);
-    acc = fmaf(wf[1], a.y, acc);
-    acc = fmaf(wf[2], a.z, acc);
-    acc = fmaf(wf[3], a.w, acc);
-    acc = fmaf(wf[4], b.x, acc);
-    acc = fmaf(wf[5], b.y, acc);
-    acc = fmaf(wf[6], b.z, acc);
-    acc = fmaf(wf[7], b.w, acc);
-    return acc;
-}
-
-// Rows of a GEMV: up to three runs of consecutive rows of row-major matrices
-// with `cols` columns, concatenated.
-struct Rows {
-    const uint16_t *base[3];
-    int count[3];
-};
-
-__device__ __forceinline__ const uint4 *row_at(const Rows &m, int r, int cols) {
-    const uint16_t *p;
-    if (r < m.count[0]) p = m.base[0] + (size_t)r * cols;
-    else if (r < m.count[0] + m.count[1]) p = m.base[1] + (size_t)(r - m.count[0]) * cols;
-    else p = m.base[2] + (size_t)(r - m.count[0] - m.count[1]) * cols;
-    return reinterpret_cast<const uint4 *>(p);
-}
 
 enum Prologue { kNormSum, kPlain };
 enum Epilogue { kStore, kSiluPairs, kLogits };
@@ -242,14 +136,6 @@ __device__ __forceinline__ void dma16(const void *src, void *wave_base) {
     __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)wave_base, 16, 0, 0);
 }
 
-__device__ __forceinline__ void lds_row8(const float *row, int sub, float f[8]) {
-    const float4 a = reinterpret_cast<const float4 *>(row)[sub * 2], b = reinterpret_cast<const float4 *>(row)[sub * 2 + 1];
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-}
-__device__ __forceinline__ void lds_row8(const uint16_t *row, int sub, float f[8]) {
-    unpack8(reinterpret_cast<const uint4 *>(row)[sub], f);
-}
 __device__ __forceinline__ float lds_at(const float *row, int d) { return row[d]; }
 __device__ __forceinline__ float lds_at(const uint16_t *row, int d) { return bf16_to_f32(row[d]); }
 
@@ -268,6 +154,7 @@ template <int HD, int G, typename KV, bool WORDS, int ROWS>
 __device__ __forceinline__ void attend(const StepAttnArgs &a, int g, int split, const unsigned long long *words,
                                        unsigned epoch, unsigned *err) {
     constexpr int LPK = HD / 8, KPW = 64 / LPK, KPB = kWaves * KPW, NP = kThreads / HD;
+    static_assert(LPK == 16, "one key per 16-lane row");
     constexpr int ROW16 = HD * (int)sizeof(KV) / 16;  // 16-byte chunks per cached row
     __shared__ float hq[G * HD], hk[HD], hv[HD];
     __shared__ float scores[G][ROWS];
@@ -379,7 +266,7 @@ __device__ __forceinline__ void attend(const StepAttnArgs &a, int g, int split, 
         if (h > G) continue;
         float x0 = av[hh], x1 = bv[hh];
         if (h < G ? a.q_norm != nullptr : a.k_norm != nullptr) {
-            const float ss = wave_sum(x0 * x0 + x1 * x1);
+            const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
             const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
             x0 = x0 * (sc * ga[hh]);
             x1 = x1 * (sc * gb[hh]);
@@ -423,7 +310,7 @@ __device__ __forceinline__ void attend(const StepAttnArgs &a, int g, int split, 
                 float sc = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) sc = fmaf(qf[gg][i], kf[i], sc);
-                sc = group_sum<LPK>(sc);
+                sc = row_sum_dpp(sc);
                 if (j < cnt && sub == 0) scores[gg][j] = scale * sc;
             }
         }
@@ -431,7 +318,7 @@ __device__ __forceinline__ void attend(const StepAttnArgs &a, int g, int split, 
         for (int gg = wave; gg < G; gg += kWaves) {
             float m = -INFINITY;
             for (int j = lane; j < cnt; j += 64) m = fmaxf(m, scores[gg][j]);
-            m = wave_max(m);
+            m = wave_max_dpp(m);
             const float m_old = st_m[gg], m_new = fmaxf(m_old, m);
             float l = 0.f;
             for (int j = lane; j < cnt; j += 64) {
@@ -439,7 +326,7 @@ __device__ __forceinline__ void attend(const StepAttnArgs &a, int g, int split, 
                 scores[gg][j] = e;
                 l += e;
             }
-            l = wave_sum(l);
+            l = wave_sum_dpp(l);
             if (lane == 0) {
                 const float al = expf(m_old - m_new);
                 st_a[gg] = al;
@@ -497,13 +384,11 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
 // never wait, so the attention blocks' polls always end.
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
-    constexpr int RPW = 2, RPB = RPW * kWaves, HD = 128;
+    constexpr int RPW = 2, RPB = RPW * kWaves;
     const int ngemv = (a.n_rows + RPB - 1) / RPB;
     const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
-        // Half-size passes keep the launch's LDS per block low enough for all
-        // of its blocks to be resident at once.
-        attend<HD, G, KV, true, kStageRows / 2>(q.at, blockIdx.x - ngemv, 0, q.words, epoch, q.err);
+        attend_words<G, KV>(q.at, blockIdx.x - ngemv, q.words, epoch, q.err);
         return;
     }
     extern __shared__ float xs[];

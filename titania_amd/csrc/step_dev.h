@@ -1,0 +1,383 @@
+// Device code of the decode-step kernels: the GEMV input builder, row tables,
+// and the register-resident attention of one KV head over the whole context.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "device_util.h"
+#include "fused.h"
+#include "step.h"
+
+namespace th {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+// Builds the block's f32 input in LDS: x = a (+ b), optionally RMSNorm'd with
+// gain g (model/cpu.rs:85-94); block 0 keeps the un-normalized sum in x_out.
+// Every thread issues all its loads (NV float4 of a, of b
+// and 4-element groups of g) before using any, so the input costs one memory
+// round trip rather than one per loop iteration.
+template <bool NORM, int NV>
+__device__ __forceinline__ void build_input(float *xs, const float *a, const float *b, int n, const uint16_t *g,
+                                            float eps, float *x_out, float *red) {
+    const int tid = threadIdx.x;
+    const int n4 = n >> 2;
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    const float4 *b4 = reinterpret_cast<const float4 *>(b);
+    const uint2 *g4 = reinterpret_cast<const uint2 *>(g);
+    float4 va[NV], vb[NV];
+    uint2 vg[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = tid + k * kThreads;
+        if (i < n4) {
+            va[k] = a4[i];
+            if (b) vb[k] = b4[i];
+            if (NORM) vg[k] = g4[i];
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = tid + k * kThreads;
+        if (i < n4) {
+            float4 v = va[k];
+            if (b) {
+                v.x = v.x + vb[k].x;
+                v.y = v.y + vb[k].y;
+                v.z = v.z + vb[k].z;
+                v.w = v.w + vb[k].w;
+            }
+            va[k] = v;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            if (!NORM) reinterpret_cast<float4 *>(xs)[i] = v;
+        }
+    }
+    if (x_out && blockIdx.x == 0) {  // every block holds the sum; the first keeps it
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < n4) reinterpret_cast<float4 *>(x_out)[i] = va[k];
+        }
+    }
+    if (!NORM) {
+        __syncthreads();
+        return;
+    }
+    ss = wave_sum_dpp(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float total = 0.f;
+    for (int w = 0; w < kWaves; ++w) total += red[w];
+    const float scale = 1.0f / sqrtf(total / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = tid + k * kThreads;
+        if (i < n4) {
+            float4 v = va[k];
+            v.x = v.x * (scale * bf16_lo(vg[k].x));
+            v.y = v.y * (scale * bf16_hi(vg[k].x));
+            v.z = v.z * (scale * bf16_lo(vg[k].y));
+            v.w = v.w * (scale * bf16_hi(vg[k].y));
+            reinterpret_cast<float4 *>(xs)[i] = v;
+        }
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ float dot8(const float *xs, const uint4 &w, int col, float acc) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs) + col * 2;
+    const float4 a = x4[0], b = x4[1];
+    float wf[8];
+    unpack8(w, wf);
+    acc = fmaf(wf[0], a.x, acc);
+    acc = fmaf(wf[1], a.y, acc);
+    acc = fmaf(wf[2], a.z, acc);
+    acc = fmaf(wf[3], a.w, acc);
+    acc = fmaf(wf[4], b.x, acc);
+    acc = fmaf(wf[5], b.y, acc);
+    acc = fmaf(wf[6], b.z, acc);
+    acc = fmaf(wf[7], b.w, acc);
+    return acc;
+}
+
+// Rows of a GEMV: up to three runs of consecutive rows of row-major matrices
+// with `cols` columns, concatenated.
+struct Rows {
+    const uint16_t *base[3];
+    int count[3];
+};
+
+__device__ __forceinline__ const uint4 *row_at(const Rows &m, int r, int cols) {
+    const uint16_t *p;
+    if (r < m.count[0]) p = m.base[0] + (size_t)r * cols;
+    else if (r < m.count[0] + m.count[1]) p = m.base[1] + (size_t)(r - m.count[0]) * cols;
+    else p = m.base[2] + (size_t)(r - m.count[0] - m.count[1]) * cols;
+    return reinterpret_cast<const uint4 *>(p);
+}
+
+__device__ __forceinline__ void lds_row8(const float *row, int sub, float f[8]) {
+    const float4 a = reinterpret_cast<const float4 *>(row)[sub * 2], b = reinterpret_cast<const float4 *>(row)[sub * 2 + 1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ void lds_row8(const uint16_t *row, int sub, float f[8]) {
+    unpack8(reinterpret_cast<const uint4 *>(row)[sub], f);
+}
+// Cached K/V rows held in registers: in the score pass a lane holds dims
+// [8*sub, 8*sub + 8) of its keys, in the value pass dims [4*d4, 4*d4 + 4).
+template <typename KV> struct KvRegs;
+template <> struct KvRegs<float> {
+    struct K { float4 a, b; };
+    using V = float4;
+    static constexpr int kRows = 64;  // positions per pass
+    __device__ static K load_k(const float *row, int sub) {
+        const float4 *p = reinterpret_cast<const float4 *>(row) + sub * 2;
+        return K{p[0], p[1]};
+    }
+    __device__ static void unpack_k(const K &k, float f[8]) {
+        f[0] = k.a.x; f[1] = k.a.y; f[2] = k.a.z; f[3] = k.a.w;
+        f[4] = k.b.x; f[5] = k.b.y; f[6] = k.b.z; f[7] = k.b.w;
+    }
+    __device__ static V load_v(const float *row, int d4) { return reinterpret_cast<const float4 *>(row)[d4]; }
+    __device__ static void unpack_v(const V &v, float f[4]) {
+        f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+    }
+};
+template <> struct KvRegs<uint16_t> {
+    using K = uint4;
+    using V = uint2;
+    static constexpr int kRows = 128;
+    __device__ static K load_k(const uint16_t *row, int sub) { return reinterpret_cast<const uint4 *>(row)[sub]; }
+    __device__ static void unpack_k(const K &k, float f[8]) { unpack8(k, f); }
+    __device__ static V load_v(const uint16_t *row, int d4) { return reinterpret_cast<const uint2 *>(row)[d4]; }
+    __device__ static void unpack_v(const V &v, float f[4]) {
+        f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x);
+        f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+    }
+};
+
+// Attention of one KV head over the whole context by one block, from q/k/v
+// (value | epoch << 32) words that other blocks of the same launch write.
+// The first pass's cached rows are requested before anything else, without
+// waiting for the position: rows past the context are read (always inside the
+// cache's max_len rows) and then ignored. Later passes request their rows as
+// soon as the previous pass has used the registers. Reductions are DPP.
+template <int G, typename KV>
+__device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const unsigned long long *words,
+                                             unsigned epoch, unsigned *err) {
+    using R = KvRegs<KV>;
+    constexpr int HD = 128, HALF = HD / 2, ROWS = R::kRows;
+    constexpr int NK = ROWS / 16;  // keys per lane in the score pass
+    constexpr int NV = ROWS / 8;   // keys per lane in the value pass
+    constexpr int HPW = (G + 1 + kWaves - 1) / kWaves;
+    static_assert(G <= kWaves, "one wave per q head in the softmax");
+    __shared__ float hq[G * HD], hk[HD], hv[HD];
+    __shared__ float scores[G][ROWS];
+    __shared__ float st_m[G], st_l[G], st_a[G];
+    __shared__ float red[G][kWaves][HD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane & 15, kq = wave * 4 + (lane >> 4);  // score pass: dims 8*sub.., key kq of 16
+    const int d4 = tid & 31, pv = tid >> 5;                   // value pass: dims 4*d4.., key pv of 8
+    const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
+    const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
+    const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
+    typename R::K kr[NK];
+    typename R::V vr[NV];
+    // A pass reads up to ROWS - 1 rows past the context; the caches' allocation
+    // extends kStepKvTailRows rows past the last head, so this stays inside it.
+    static_assert(ROWS <= kStepKvTailRows, "pass longer than the caches' tail");
+    auto load_k = [&](long long c0) {
+#pragma unroll
+        for (int i = 0; i < NK; ++i) kr[i] = R::load_k(kc + (c0 + i * 16) * HD + kq * HD, sub);
+    };
+    auto load_v = [&](long long c0) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) vr[i] = R::load_v(vc + (c0 + i * 8) * HD + pv * HD, d4);
+    };
+    load_k(0);
+    load_v(0);
+    // RMSNorm gains of this wave's heads (q heads 0..G-1, then k).
+    float ga[HPW], gb[HPW];
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+        const int h = wave + hh * kWaves;
+        ga[hh] = gb[hh] = 1.f;
+        const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
+        if (h <= G && gain) {
+            ga[hh] = bf16_to_f32(gain[lane]);
+            gb[hh] = bf16_to_f32(gain[lane + HALF]);
+        }
+    }
+    const long long pos = *a.pos;
+    const long long len = pos + 1;
+    const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
+    // Poll until every q/k/v word this block needs carries `epoch` (bounded:
+    // about 2 s, then *err counts the failure and the block goes on).
+    float av[HPW], bv[HPW], vnew = 0.f;
+    for (int it = 0;; ++it) {
+        int ok = 1;
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh) {
+            const int h = wave + hh * kWaves;
+            av[hh] = bv[hh] = 0.f;
+            if (h <= G) {
+                const unsigned long long *x = h < G ? words + (size_t)(g * G + h) * HD : words + qd + (size_t)g * HD;
+                const unsigned long long wa = __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const unsigned long long wb =
+                    __hip_atomic_load(x + lane + HALF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok &= (unsigned)(wa >> 32) == epoch && (unsigned)(wb >> 32) == epoch;
+                av[hh] = __uint_as_float((unsigned)wa);
+                bv[hh] = __uint_as_float((unsigned)wb);
+            }
+        }
+        if (tid < HD) {
+            const unsigned long long wv =
+                __hip_atomic_load(words + qd + kvd + (size_t)g * HD + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok &= (unsigned)(wv >> 32) == epoch;
+            vnew = __uint_as_float((unsigned)wv);
+        }
+        if (__syncthreads_and(ok)) break;
+        if (it >= (1 << 21)) {
+            if (tid == 0) atomicAdd(err, 1u);
+            break;
+        }
+    }
+    if (tid < G) {
+        st_m[tid] = -INFINITY;
+        st_l[tid] = 0.f;
+    }
+    if (tid < HD) hv[tid] = vnew;
+    // RMSNorm (model.rs:111-116) + RoPE (model.rs:117-118), one head per wave.
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+        const int h = wave + hh * kWaves;
+        if (h > G) continue;
+        float x0 = av[hh], x1 = bv[hh];
+        if (h < G ? a.q_norm != nullptr : a.k_norm != nullptr) {
+            const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
+            const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
+            x0 = x0 * (sc * ga[hh]);
+            x1 = x1 * (sc * gb[hh]);
+        }
+        float *x = h < G ? hq + h * HD : hk;
+        x[lane] = x0 * cs.x - x1 * cs.y;
+        x[lane + HALF] = x1 * cs.x + x0 * cs.y;
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)HD);
+    float acc[G][4];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[gg][i] = 0.f;
+    for (long long c0 = 0; c0 < len; c0 += ROWS) {
+        const int cnt = (int)(len - c0 < ROWS ? len - c0 : ROWS);
+        const bool more = c0 + ROWS < len;
+        // Scores: positions below pos come from the cache, pos itself is the
+        // new key. q is read from LDS once per pass, all heads together.
+        float qf[G][8];
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) lds_row8(hq + gg * HD, sub, qf[gg]);
+#pragma unroll
+        for (int i = 0; i < NK; ++i) {
+            const int j = i * 16 + kq;
+            float kf[8];
+            R::unpack_k(kr[i], kf);
+            if (c0 + j == pos) lds_row8(hk, sub, kf);
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) s = fmaf(qf[gg][e], kf[e], s);
+                s = row_sum_dpp(s);
+                if (sub == 0 && j < cnt) scores[gg][j] = scale * s;
+            }
+        }
+        if (more) load_k(c0 + ROWS);
+        __syncthreads();
+        // Online softmax, one wave per q head.
+        if (wave < G) {
+            float m = -INFINITY;
+            for (int j = lane; j < cnt; j += 64) m = fmaxf(m, scores[wave][j]);
+            m = wave_max_dpp(m);
+            const float m_old = st_m[wave], m_new = fmaxf(m_old, m);
+            float l = 0.f;
+            for (int j = lane; j < cnt; j += 64) {
+                const float e = expf(scores[wave][j] - m_new);
+                scores[wave][j] = e;
+                l += e;
+            }
+            l = wave_sum_dpp(l);
+            if (lane == 0) {
+                const float al = expf(m_old - m_new);
+                st_a[wave] = al;
+                st_l[wave] = st_l[wave] * al + l;
+                st_m[wave] = m_new;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const float al = st_a[gg];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[gg][i] *= al;
+        }
+        // Weights of this lane's keys, all read before any is used (0 past the
+        // context, where the value registers hold rows that are not used).
+        float pw[NV][G];
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) pw[i][gg] = i * 8 + pv < cnt ? scores[gg][i * 8 + pv] : 0.f;
+        const int fresh = (int)(pos - c0) - pv;  // slot * 8 of the key at pos, if this lane holds it
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = i * 8 + pv;
+            if (j < cnt) {
+                float vf[4];
+                R::unpack_v(vr[i], vf);
+                if (fresh == i * 8) {
+                    const float4 n = reinterpret_cast<const float4 *>(hv)[d4];
+                    vf[0] = n.x; vf[1] = n.y; vf[2] = n.z; vf[3] = n.w;
+                }
+#pragma unroll
+                for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[gg][e] = fmaf(pw[i][gg], vf[e], acc[gg][e]);
+            }
+        }
+        if (more) load_v(c0 + ROWS);
+        __syncthreads();  // scores are rewritten by the next pass
+    }
+    // The new key and value at pos (model.rs:119-120); no block of this launch
+    // reads that position from the caches.
+    if (tid < HD) {
+        store_kv(const_cast<KV *>(kc) + pos * HD + tid, hk[tid]);
+        store_kv(const_cast<KV *>(vc) + pos * HD + tid, hv[tid]);
+    }
+    // Sum the 8 key groups: lanes l and l + 32 of a wave, then the 4 waves.
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[gg][i] += __shfl_xor(acc[gg][i], 32, 64);
+            if (lane < 32) red[gg][wave][d4 * 4 + i] = acc[gg][i];
+        }
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += kThreads) {
+        const int gg = idx / HD, d = idx % HD;
+        const float sm = ((red[gg][0][d] + red[gg][1][d]) + red[gg][2][d]) + red[gg][3][d];
+        a.out[((size_t)g * G + gg) * HD + d] = sm / st_l[gg];
+    }
+}
+
+}  // namespace
+
+}  // namespace th
