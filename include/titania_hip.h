@@ -106,6 +106,17 @@ TH_API int th_add_rmsnorm(th_device *dev, th_buffer *x, const th_buffer *y, th_b
 /* Greedy choice (model/sampler.rs:21-33 at temperature 0): index of the largest
  * of the buffer's values under IEEE total order, lowest index on ties. */
 TH_API int th_argmax(th_device *dev, const th_buffer *logits, uint32_t *token);
+/* model/sampler.rs:21-59 `Sampler::sample` over a device buffer: the top_k
+ * largest values (top_k clamped to [1, len], at most 256 on the device; len at
+ * most 262144); at temperature 0 the largest, as th_argmax; otherwise a softmax
+ * at the temperature over the top_k, the shortest prefix of them whose
+ * probability reaches top_p, and a draw from that prefix with the xorshift64*
+ * generator whose state is *rng (sampler.rs:62-76; Sampler::new seeds it with
+ * max(seed, 1)); *rng advances by one draw. Equal values rank by lower index
+ * (the reference leaves their order unspecified). At a nonzero temperature
+ * top_p must be > 0 (the reference panics otherwise). */
+TH_API int th_sample(th_device *dev, const th_buffer *logits, float temperature, size_t top_k, float top_p,
+                     uint64_t *rng, uint32_t *token);
 
 /* ---- the forward pass (model/model.rs) ---- */
 
@@ -160,6 +171,13 @@ TH_API int th_forward(th_model *model, th_state *state, const uint32_t *tokens, 
  * not NULL, the logits after each fed token (steps * vocab_size floats). One
  * step is one HIP graph replay; the host waits once, at the end. */
 TH_API int th_decode(th_model *model, th_state *state, size_t pos, size_t steps, uint32_t *out_tokens, float *out_logits);
+
+/* th_decode with every pick drawn as th_sample draws it (model/chat.rs:149-178
+ * driving a Sampler from model/sampler.rs), kept on the device: *rng is the
+ * generator state before the first draw and is left after the last. The
+ * logits never leave the device. Temperature 0 is th_decode. */
+TH_API int th_decode_sample(th_model *model, th_state *state, size_t pos, size_t steps, float temperature,
+                            size_t top_k, float top_p, uint64_t *rng, uint32_t *out_tokens);
 
 /* Phase trace of the last th_decode on the persistent path, when the state was
  * created with TITANIA_TRACE=<steps> in the environment: word 0 is the kernel's

@@ -24,6 +24,11 @@
  *   ref_attention  len 1 -> V row exactly; equal keys -> mean of V; float64 softmax
  *   ref_silu_mul   torch float64 silu; g = 0 -> 0
  *   ref_argmax     brute force, lowest index on ties
+ *   ref_sample     temperature 0 / top_k 1 / small top_p -> the argmax; tokens
+ *                  outside the top-k or the top-p prefix never drawn; draw
+ *                  frequencies against the float64 softmax (chi-square); the
+ *                  xorshift64* generator against a float64-free integer
+ *                  restatement of its published recurrence (Vigna 2016)
  *   ref_forward    HF transformers Qwen3ForCausalLM on the same weights (fixture)
  * Unpinned at the bit level: glibc expf/powf/sinf/cosf themselves (no reference
  * test holds their outputs), which tolerance-based checks make moot.
@@ -233,6 +238,76 @@ EXPORT uint32_t ref_argmax(const float *logits, size_t n) {
     return (uint32_t)best;
 }
 
+/* ---- sampling (model/sampler.rs) ---- */
+
+/* model/sampler.rs:62-76: xorshift64*; next_f32 is uniform in [0, 1). */
+static uint64_t rng_next_u64(uint64_t *s) {
+    uint64_t x = *s;
+    x ^= x >> 12;
+    x ^= x << 25;
+    x ^= x >> 27;
+    *s = x;
+    return x * 0x2545F4914F6CDD1DULL;
+}
+
+static float rng_next_f32(uint64_t *s) { return (float)(rng_next_u64(s) >> 40) / (float)(1u << 24); }
+
+EXPORT uint64_t ref_rng_next_u64(uint64_t *s) { return rng_next_u64(s); }
+
+typedef struct { int32_t key; uint32_t token; } cand_t;
+
+/* Larger logit first under total order; equal logits by lower token (the
+ * reference's select_nth_unstable leaves their order unspecified). */
+static int cand_cmp(const void *a, const void *b) {
+    const cand_t *x = (const cand_t *)a, *y = (const cand_t *)b;
+    if (x->key != y->key) return x->key > y->key ? -1 : 1;
+    return x->token < y->token ? -1 : (x->token > y->token);
+}
+
+/* model/sampler.rs:21-59: the top_k largest logits (top_k clamped to
+ * [1, n]), sorted; at temperature 0 the first; otherwise softmax at the
+ * temperature over the k, the shortest prefix whose probability reaches
+ * top_p, and a draw from the prefix with the generator in *rng. */
+EXPORT uint32_t ref_sample(const float *logits, size_t n, float temperature, size_t top_k, float top_p,
+                           uint64_t *rng) {
+    size_t k = top_k < 1 ? 1 : (top_k > n ? n : top_k);
+    cand_t *c = (cand_t *)malloc(n * sizeof(cand_t));
+    for (size_t i = 0; i < n; ++i) {
+        c[i].key = total_key(logits[i]);
+        c[i].token = (uint32_t)i;
+    }
+    qsort(c, n, sizeof(cand_t), cand_cmp);
+    uint32_t tok = c[0].token;
+    if (temperature != 0.0f) {
+        float *probs = (float *)malloc(k * sizeof(float));
+        const float max = logits[c[0].token];
+        for (size_t i = 0; i < k; ++i) probs[i] = expf((logits[c[i].token] - max) / temperature);
+        float sum = 0.0f;
+        for (size_t i = 0; i < k; ++i) sum += probs[i];
+        float cumulative = 0.0f;
+        size_t m = 0;
+        for (size_t i = 0; i < k; ++i) {
+            probs[i] /= sum;
+            if (cumulative < top_p) {
+                cumulative += probs[i];
+                m += 1;
+            }
+        }
+        float r = rng_next_f32(rng) * cumulative;
+        tok = c[m - 1].token;
+        for (size_t i = 0; i < m; ++i) {
+            r -= probs[i];
+            if (r <= 0.0f) {
+                tok = c[i].token;
+                break;
+            }
+        }
+        free(probs);
+    }
+    free(c);
+    return tok;
+}
+
 /* ---- the forward pass (model/model.rs:83-149, State model/model.rs:156-233) ---- */
 
 typedef struct {
@@ -379,5 +454,22 @@ EXPORT int ref_generate(const ref_model *m, ref_state *s, const uint32_t *prompt
         pos += 1;
     }
     if (last_logits) memcpy(last_logits, s->logits, V * sizeof(float));
+    return 0;
+}
+
+/* model/chat.rs:149-178 with a Sampler (model/sampler.rs): the prompt, then
+ * `steps` tokens each drawn from the logits of the token before. */
+EXPORT int ref_generate_sampled(const ref_model *m, ref_state *s, const uint32_t *prompt, size_t n_prompt,
+                                size_t steps, float temperature, size_t top_k, float top_p, uint64_t *rng,
+                                uint32_t *out_tokens) {
+    size_t V = (size_t)m->c.vocab;
+    if (ref_forward(m, s, prompt, n_prompt, 0, NULL) != 0) return -1;
+    size_t pos = n_prompt;
+    for (size_t i = 0; i < steps; ++i) {
+        uint32_t tok = ref_sample(s->logits, V, temperature, top_k, top_p, rng);
+        out_tokens[i] = tok;
+        if (ref_forward(m, s, &tok, 1, pos, NULL) != 0) return -1;
+        pos += 1;
+    }
     return 0;
 }

@@ -68,6 +68,10 @@ def lib() -> C.CDLL:
             "ref_state_v_cache": (_P, [_P, C.c_int64]),
             "ref_forward": (C.c_int, [C.POINTER(RefModelC), _P, _P, _SZ, _SZ, _P]),
             "ref_generate": (C.c_int, [C.POINTER(RefModelC), _P, _P, _SZ, _SZ, _P, _P, _P]),
+            "ref_rng_next_u64": (C.c_uint64, [C.POINTER(C.c_uint64)]),
+            "ref_sample": (C.c_uint32, [_P, _SZ, C.c_float, _SZ, C.c_float, C.POINTER(C.c_uint64)]),
+            "ref_generate_sampled": (C.c_int, [C.POINTER(RefModelC), _P, _P, _SZ, _SZ, C.c_float, _SZ, C.c_float,
+                                               C.POINTER(C.c_uint64), _P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -164,6 +168,30 @@ def argmax(logits) -> int:
     return int(lib().ref_argmax(x.ctypes.data, x.size))
 
 
+class Sampler:
+    """model/sampler.rs:1-59: top-k, then top-p, at a temperature, drawing with
+    xorshift64* seeded by max(seed, 1). `state` is the generator's state."""
+
+    def __init__(self, temperature: float, top_k: int, top_p: float, seed: int):
+        self.temperature, self.top_k, self.top_p = temperature, top_k, top_p
+        self.state = max(int(seed), 1) & 0xFFFFFFFFFFFFFFFF
+
+    def sample(self, logits) -> int:
+        x = _f32(logits).reshape(-1)
+        st = C.c_uint64(self.state)
+        tok = lib().ref_sample(x.ctypes.data, x.size, self.temperature, max(int(self.top_k), 0), self.top_p,
+                               C.byref(st))
+        self.state = st.value
+        return int(tok)
+
+
+def rng_next_u64(state: int) -> tuple[int, int]:
+    """One step of the oracle's xorshift64*: (output, new state)."""
+    st = C.c_uint64(state)
+    out = lib().ref_rng_next_u64(C.byref(st))
+    return int(out), st.value
+
+
 # ---- the forward pass ----
 
 class RefModel:
@@ -223,6 +251,19 @@ class RefModel:
         if rc != 0:
             raise ValueError("oracle generate: tokens past the end of the cache")
         return toks, gaps, last
+
+    def generate_sampled(self, state: "RefState", prompt, steps: int, sampler: Sampler):
+        """The prompt, then `steps` tokens drawn by `sampler` (whose state advances)."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        toks = np.empty(steps, dtype=np.uint32)
+        st = C.c_uint64(sampler.state)
+        rc = lib().ref_generate_sampled(C.byref(self.c_model), state.handle, p.ctypes.data, p.size, steps,
+                                        sampler.temperature, max(int(sampler.top_k), 0), sampler.top_p,
+                                        C.byref(st), toks.ctypes.data)
+        if rc != 0:
+            raise ValueError("oracle generate: tokens past the end of the cache")
+        sampler.state = st.value
+        return toks
 
 
 class RefState:

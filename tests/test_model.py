@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from oracle import ref
-from titania_amd import QWEN3_0_6B, QWEN3_TINY, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS
+from titania_amd import QWEN3_0_6B, QWEN3_TINY, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, Sampler
 from titania_amd.config import Config
 from titania_amd import synth
 from titania_amd.model import Model, State
@@ -318,3 +318,47 @@ def test_qwen4b_bf16_cache_drift(qwen4b):
     assert drift <= 0.25
     a.close()
     b.close()
+
+
+# ---- sampled decode (model/chat.rs:149-178 with model/sampler.rs) ----
+
+@pytest.mark.parametrize("t,k,p", [(0.7, 20, 0.8), (1.5, 256, 1.0), (0.9, 40, 0.9)])
+def test_tiny_decode_sampled(tiny, t, k, p):
+    """Draws on the device across a decode, against the oracle's chat-style
+    loop; a second call continues the generator where the first left it, and
+    a greedy decode on the same state afterwards is unaffected. f32 caches:
+    bf16 caches move the logits by up to ~2e-2, enough to move draws."""
+    kv = TH_KV_F32
+    m, r = tiny
+    c = QWEN3_TINY
+    prompt = synth.prompt(12, c.vocab_size, seed=5)
+    st = State(m, 12 + 40 + 8, kv)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    dev = Sampler(t, k, p, 1234)
+    got = list(m.decode(st, 12, 24, sampler=dev)) + list(m.decode(st, 36, 16, sampler=dev))
+    cpu = ref.Sampler(t, k, p, 1234)
+    exp = list(r.generate_sampled(r.state(12 + 40 + 8), prompt, 40, cpu))
+    assert got == exp
+    assert dev.rng == cpu.state
+    more = m.decode(st, 52, 4)
+    assert len(more) == 4
+    st.close()
+
+
+def test_qwen06_decode_sampled(qwen06):
+    """Qwen3-0.6B shape at the reference CLI's sampler (0.7, 20, 0.8): 24
+    draws on the device match the oracle."""
+    m, r = qwen06
+    c = QWEN3_0_6B
+    prompt = synth.prompt(16, c.vocab_size, seed=0)
+    steps = 24
+    st = State(m, 16 + steps)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    dev = Sampler(0.7, 20, 0.8, 77)
+    got = list(m.decode(st, 16, steps, sampler=dev))
+    cpu = ref.Sampler(0.7, 20, 0.8, 77)
+    exp = list(r.generate_sampled(r.state(16 + steps), prompt, steps, cpu))
+    assert got == exp
+    assert dev.rng == cpu.state
+    st.close()
+

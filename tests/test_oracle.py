@@ -328,3 +328,76 @@ def test_generate_is_the_forward_loop():
         lg = m.forward(st, [t], 5 + i)
     assert np.array_equal(lg, last)
 
+
+
+# ---- sampling (model/sampler.rs) ----
+
+M64 = (1 << 64) - 1
+
+
+def test_xorshift64star_published_recurrence():
+    """The generator against Vigna's xorshift64* (2016): the 64-bit state
+    recurrence x ^= x >> 12; x ^= x << 25; x ^= x >> 27 and the output
+    x * 2685821657736338717 mod 2^64, in Python integers."""
+    for seed in (1, 42, 0xDEADBEEFCAFEF00D):
+        x = seed
+        state = seed
+        for _ in range(1000):
+            x ^= x >> 12
+            x = (x ^ (x << 25)) & M64
+            x ^= x >> 27
+            out, state = ref.rng_next_u64(state)
+            assert state == x
+            assert out == (x * 2685821657736338717) & M64
+
+
+def test_sampler_seed_zero_is_one():
+    """Sampler::new seeds with seed.max(1): seeds 0 and 1 draw alike."""
+    logits = rng.standard_normal(500).astype(np.float32)
+    a, b = ref.Sampler(1.0, 50, 0.95, 0), ref.Sampler(1.0, 50, 0.95, 1)
+    assert [a.sample(logits) for _ in range(50)] == [b.sample(logits) for _ in range(50)]
+
+
+def test_sampler_greedy_cases_are_argmax():
+    """Temperature 0, top_k 1 (and 0, clamped to 1), or a top_p below the
+    largest probability all return the argmax, lowest index on ties."""
+    logits = rng.standard_normal(3000).astype(np.float32)
+    logits[[17, 2900]] = logits.max() + 1.0  # a tie for first place
+    best = 17
+    for t, k, p in [(0.0, 40, 0.9), (0.8, 1, 0.9), (0.8, 0, 0.9), (1.0, 40, 1e-6)]:
+        s = ref.Sampler(t, k, p, 7)
+        assert {s.sample(logits) for _ in range(30)} == {best}, (t, k, p)
+
+
+def _softmax64(x: np.ndarray, t: float) -> np.ndarray:
+    z = (x.astype(np.float64) - x.max()) / t
+    e = np.exp(z)
+    return e / e.sum()
+
+
+@pytest.mark.parametrize("t,k,p", [(0.7, 8, 1.0), (1.3, 20, 0.8), (0.5, 12, 0.6)])
+def test_sampler_frequencies_match_float64(t, k, p):
+    """Draw frequencies against the float64 softmax of the top k at the
+    temperature, restricted to the shortest prefix whose mass reaches top_p
+    and renormalised (the draw scales by that prefix's mass). Tokens outside
+    the prefix never appear. Logits are spaced so that no prefix boundary is
+    within float32 rounding of top_p."""
+    logits = (np.linspace(3.0, -2.0, 400) + rng.uniform(-0.01, 0.01, 400)).astype(np.float32)
+    order = rng.permutation(400)
+    logits = logits[order]
+    top = np.argsort(-logits.astype(np.float64), kind="stable")[:k]
+    probs = _softmax64(logits[top], t)
+    cum = np.cumsum(probs)
+    m = int(np.searchsorted(cum, p, side="left")) + 1 if p < 1.0 else k
+    m = min(m, k)
+    assert p >= 1.0 or abs(cum[m - 1] - p) > 1e-4
+    expected = probs[:m] / probs[:m].sum()
+    s = ref.Sampler(t, k, p, 1234)
+    n = 20000
+    draws = np.array([s.sample(logits) for _ in range(n)])
+    allowed = set(int(x) for x in top[:m])
+    assert set(np.unique(draws).tolist()) <= allowed
+    counts = np.array([(draws == tok).sum() for tok in top[:m]], dtype=np.float64)
+    chi2 = float((((counts - n * expected) ** 2) / (n * expected)).sum())
+    from scipy.stats import chi2 as chi2_dist
+    assert chi2_dist.sf(chi2, m - 1) > 1e-4, (chi2, m)

@@ -76,12 +76,14 @@ SIGNATURES: dict[str, tuple] = {
     "th_silu_mul": (_I, [_P, _P, _P]),
     "th_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, C.c_float]),
     "th_argmax": (_I, [_P, _P, C.POINTER(C.c_uint32)]),
+    "th_sample": (_I, [_P, _P, C.c_float, _SZ, C.c_float, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)]),
     "th_model_create": (_I, [_P, C.POINTER(ThConfig), C.POINTER(_P), _SZ, C.POINTER(_P)]),
     "th_model_destroy": (None, [_P]),
     "th_state_create": (_I, [_P, _SZ, _I, C.POINTER(_P)]),
     "th_state_destroy": (None, [_P]),
     "th_forward": (_I, [_P, _P, _P, _SZ, _SZ, _P, _I]),
     "th_decode": (_I, [_P, _P, _SZ, _SZ, _P, _P]),
+    "th_decode_sample": (_I, [_P, _P, _SZ, _SZ, C.c_float, _SZ, C.c_float, C.POINTER(C.c_uint64), _P]),
     "th_decode_trace": (_I, [_P, _P, _SZ, C.POINTER(_SZ)]),
 }
 

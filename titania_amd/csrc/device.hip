@@ -8,6 +8,7 @@
 #include <string>
 
 #include "common.h"
+#include "sample.h"
 
 namespace {
 thread_local std::string g_error;
@@ -372,6 +373,32 @@ int th_argmax(th_device *dev, const th_buffer *logits, uint32_t *token) {
     TH_HIP(th::launch_argmax(dev->stream, logits->ptr, logits->len, partials, dev->token_out));
     TH_HIP(hipMemcpyAsync(token, dev->token_out, sizeof(uint32_t), hipMemcpyDeviceToHost, dev->stream));
     TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_sample(th_device *dev, const th_buffer *logits, float temperature, size_t top_k, float top_p, uint64_t *rng,
+              uint32_t *token) {
+    TH_REQUIRE(dev && logits && rng && token, "th_sample: null argument");
+    TH_REQUIRE(logits->len > 0, "sampling from an empty buffer");
+    if (temperature == 0.0f) return th_argmax(dev, logits, token);
+    const size_t k = std::min(std::max<size_t>(top_k, 1), logits->len);
+    TH_REQUIRE(k <= (size_t)th::kSampleMaxTopK, "top_k %zu: the device samples from at most %d candidates", k,
+               th::kSampleMaxTopK);
+    TH_REQUIRE(logits->len <= th::kSampleMaxVocab, "sampling over %zu values: at most %zu", logits->len,
+               th::kSampleMaxVocab);
+    TH_REQUIRE(top_p > 0.0f, "top_p must be greater than 0");
+    // The sampler's state, then the candidate keys.
+    constexpr size_t head = 256;
+    char *sc = static_cast<char *>(th::scratch(dev, head + th::sample_scratch_bytes(logits->len)));
+    if (!sc) return fail(TH_ERR_NOMEM, "no scratch for sampling");
+    auto *ss_dev = reinterpret_cast<th::SampleState *>(sc);
+    th::SampleState ss{*rng, *rng, temperature, top_p, (int)k, 0};
+    TH_HIP(hipMemcpyAsync(ss_dev, &ss, sizeof ss, hipMemcpyHostToDevice, dev->stream));
+    TH_HIP(th::launch_sample(dev->stream, logits->ptr, logits->len, sc + head, ss_dev, nullptr, 0));
+    TH_HIP(hipMemcpyAsync(&ss, ss_dev, sizeof ss, hipMemcpyDeviceToHost, dev->stream));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    *rng = ss.rng;
+    *token = ss.token;
     return TH_OK;
 }
 

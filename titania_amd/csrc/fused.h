@@ -48,6 +48,30 @@ struct PickEmbed {
     float *out = nullptr;
 };
 
+// Records the step's pick: with `advance` (a token has been fed) the position,
+// step and epoch move on first; then st->token and st->tokens_out[st->step].
+__device__ __forceinline__ void step_record(StepState *st, int advance, uint32_t tok) {
+    if (advance) {
+        st->pos += 1;
+        st->step += 1;
+        st->epoch += 1;
+    }
+    st->token = tok;
+    if (st->tokens_out) st->tokens_out[st->step] = tok;
+}
+
+// emb.out = the embedding row of `tok` (model/cpu.rs:38-47), by the block.
+__device__ __forceinline__ void write_embedding(const PickEmbed &emb, uint32_t tok) {
+    const uint4 *row = reinterpret_cast<const uint4 *>(emb.table + (size_t)tok * emb.dim);
+    for (size_t c = threadIdx.x; c < emb.dim / 8; c += blockDim.x) {
+        float f[8];
+        unpack8(row[c], f);
+        float4 *o = reinterpret_cast<float4 *>(emb.out + c * 8);
+        o[0] = make_float4(f[0], f[1], f[2], f[3]);
+        o[1] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+}
+
 // argmax of the logits -> st->token and st->tokens_out[st->step]; with
 // `advance`, pos and step move on first.
 hipError_t launch_pick(hipStream_t s, const float *logits, size_t vocab, uint64_t *partials, StepState *st,

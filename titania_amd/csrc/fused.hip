@@ -127,25 +127,12 @@ __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__
         uint64_t b = 0;
         for (int w = 0; w < 16; ++w) b = max_u64(b, red[w]);
         uint32_t tok = argmax_index(b);
-        if (advance) {
-            st->pos += 1;
-            st->step += 1;
-            st->epoch += 1;
-        }
-        st->token = tok;
-        if (st->tokens_out) st->tokens_out[st->step] = tok;
+        step_record(st, advance, tok);
         picked = tok;
     }
     if (!emb.table) return;
     __syncthreads();
-    const uint4 *row = reinterpret_cast<const uint4 *>(emb.table + (size_t)picked * emb.dim);
-    for (size_t c = threadIdx.x; c < emb.dim / 8; c += blockDim.x) {
-        float f[8];
-        unpack8(row[c], f);
-        float4 *o = reinterpret_cast<float4 *>(emb.out + c * 8);
-        o[0] = make_float4(f[0], f[1], f[2], f[3]);
-        o[1] = make_float4(f[4], f[5], f[6], f[7]);
-    }
+    write_embedding(emb, picked);
 }
 
 // Copies the logits into row `step` of the caller's logits array (the logits

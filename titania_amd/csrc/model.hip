@@ -20,6 +20,7 @@
 #include "decode.h"
 #include "fused.h"
 #include "gemm.h"
+#include "sample.h"
 #include "step.h"
 #include "xdecode.h"
 
@@ -103,6 +104,11 @@ struct th_state {
     unsigned *s_err = nullptr;              // its attention blocks whose poll gave up
     uint32_t step_epoch = 0;                // StepState::epoch at the next decode call
     bool graph_keep = false;                // whether the captured step copies out the logits
+    // Sampled decode (th_decode_sample): the sampler's device state and
+    // candidate scratch; whether the step draws instead of picking the argmax.
+    th::SampleState *s_sample = nullptr;
+    void *s_cand = nullptr;
+    bool sampling = false;
     unsigned long long *trace = nullptr;  // per-phase ticks of the last decode (TITANIA_TRACE steps)
     int trace_steps = 0;
     size_t trace_words = 0;
@@ -439,7 +445,10 @@ int enqueue_step(th_state *s) {
     TH_HIP(th::launch_step_logits(st, m->out_proj()->ptr, V, H, s->sx_b, y_prev, m->norm->ptr, eps,
                                   s->logits->ptr, s->s_part, &np));
     if (s->graph_keep) TH_HIP(th::launch_keep_logits(st, s->logits->ptr, (size_t)V, s->step));
-    TH_HIP(th::launch_pick_partials(st, s->s_part, (size_t)np, s->step, 1, step_embed(s)));
+    if (s->sampling)
+        TH_HIP(th::launch_sample(st, s->logits->ptr, (size_t)V, s->s_cand, s->s_sample, s->step, 1, step_embed(s)));
+    else
+        TH_HIP(th::launch_pick_partials(st, s->s_part, (size_t)np, s->step, 1, step_embed(s)));
     return TH_OK;
 }
 
@@ -591,7 +600,9 @@ int capture_step(th_state *s) {
         rc = enqueue_fused(s, tok_dev, 1, 0, pos_dev);
         if (rc == TH_OK) {
             hipError_t e = s->graph_keep ? th::launch_keep_logits(st, s->logits->ptr, vocab, s->step) : hipSuccess;
-            if (e == hipSuccess) e = th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 1);
+            if (e == hipSuccess)
+                e = s->sampling ? th::launch_sample(st, s->logits->ptr, vocab, s->s_cand, s->s_sample, s->step, 1)
+                                : th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 1);
             if (e != hipSuccess) rc = fail(TH_ERR_HIP, "capture: %s", hipGetErrorString(e));
         }
     }
@@ -805,7 +816,8 @@ void th_state_destroy(th_state *s) {
                     s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
                     s->step,    s->tokens_dev, s->logits_dev, s->dev_layers, s->xchg, s->att_part,
                     s->att_count, s->status, s->trace, s->xx, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
-                    s->s_att, s->s_o, s->s_h, s->s_part, s->s_words, s->s_err, s->fsplit};
+                    s->s_att, s->s_o, s->s_h, s->s_part, s->s_words, s->s_err, s->fsplit, s->s_sample,
+                    s->s_cand};
     for (void *p : ptrs) free_dev(p);
     delete s;
 }
@@ -839,7 +851,14 @@ int th_decode_trace(th_state *s, uint64_t *out, size_t cap, size_t *n) {
     return TH_OK;
 }
 
-int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tokens, float *out_logits) {
+}  // extern "C"
+
+namespace {
+
+// th_decode, and th_decode_sample when `sp` (the sampler's parameters and
+// generator state, updated on return) is not null.
+int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tokens, float *out_logits,
+           th::SampleState *sp) {
     TH_REQUIRE(m && s && s->m == m && out_tokens, "th_decode: null argument or a state of another model");
     TH_REQUIRE(s->path == TH_PATH_FUSED, "decode continues a fused-path forward; run th_forward first");
     TH_REQUIRE(pos + steps <= s->max_len, "tokens past the end of the cache");
@@ -848,6 +867,12 @@ int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_
     hipStream_t st = d->stream;
     const size_t vocab = (size_t)m->c.vocab_size;
     TRY(ensure_fused_state(s));
+    const bool sampling = sp != nullptr;
+    if (sampling && !s->s_sample) {
+        TH_HIP(hipStreamSynchronize(st));
+        TH_HIP(hipMalloc(&s->s_sample, sizeof(th::SampleState)));
+        TH_HIP(hipMalloc(&s->s_cand, th::sample_scratch_bytes(vocab)));
+    }
     if (steps + 1 > s->tokens_dev_cap) {
         TH_HIP(hipStreamSynchronize(st));
         free_dev(s->tokens_dev);
@@ -871,32 +896,41 @@ int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_
     init.logits_out = out_logits ? s->logits_dev : nullptr;
     init.epoch = s->step_epoch;
     TH_HIP(hipMemcpyAsync(s->step, &init, sizeof init, hipMemcpyHostToDevice, st));
+    if (sampling) TH_HIP(hipMemcpyAsync(s->s_sample, sp, sizeof *sp, hipMemcpyHostToDevice, st));
     TH_HIP(hipStreamSynchronize(st));  // `init` is a stack temporary
     const char *mode = getenv("TITANIA_DECODE");
     if (mode && strcmp(mode, "xcd") == 0 && !s->xcd)
         return fail(TH_ERR_INVALID, "TITANIA_DECODE=xcd: the XCD-parallel kernel does not support this model's shape");
-    if (s->xcd) {
+    // The first pick comes from the logits the last forward left.
+    auto first_pick = [&]() {
+        return sampling ? th::launch_sample(st, s->logits->ptr, vocab, s->s_cand, s->s_sample, s->step, 0,
+                                            step_embed(s))
+                        : th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0, step_embed(s));
+    };
+    if (s->xcd && !sampling) {
         TRY(decode_xcd(s, steps));
-    } else if (s->persistent) {
+    } else if (s->persistent && !sampling) {
         TRY(decode_persistent(s, steps));
     } else if (mode && strcmp(mode, "eager") == 0 && s->step_fused) {
         // The same step kernels launched one by one (no graph): for profilers
         // that do not follow graph launches.
         s->graph_keep = out_logits != nullptr;
-        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0, step_embed(s)));
+        s->sampling = sampling;
+        TH_HIP(first_pick());
         for (size_t i = 0; i < steps; ++i) TRY(enqueue_step(s));
     } else {
-        // The captured step copies out the logits only if this call wants them.
-        if (s->graph_exec && s->graph_keep != (out_logits != nullptr)) {
+        // The captured step copies out the logits only if this call wants
+        // them, and draws or picks as this call does.
+        if (s->graph_exec && (s->graph_keep != (out_logits != nullptr) || s->sampling != sampling)) {
             TH_HIP(hipGraphExecDestroy(s->graph_exec));
             TH_HIP(hipGraphDestroy(s->graph));
             s->graph_exec = nullptr;
             s->graph = nullptr;
         }
         s->graph_keep = out_logits != nullptr;
+        s->sampling = sampling;
         TRY(capture_step(s));
-        // The first pick comes from the logits the last forward left.
-        TH_HIP(th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0, step_embed(s)));
+        TH_HIP(first_pick());
         for (size_t i = 0; i < steps; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
     }
     s->step_epoch += (uint32_t)steps;
@@ -905,9 +939,38 @@ int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_
         TH_HIP(hipMemcpyAsync(out_logits, s->logits_dev, steps * vocab * sizeof(float), hipMemcpyDeviceToHost, st));
     unsigned poll_failures = 0;
     if (s->s_err) TH_HIP(hipMemcpyAsync(&poll_failures, s->s_err, sizeof poll_failures, hipMemcpyDeviceToHost, st));
+    if (sampling) TH_HIP(hipMemcpyAsync(sp, s->s_sample, sizeof *sp, hipMemcpyDeviceToHost, st));
     TH_HIP(hipStreamSynchronize(st));
     if (poll_failures)
         return fail(TH_ERR_HIP, "decode: %u attention blocks gave up waiting for their q/k/v", poll_failures);
+    return TH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int th_decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tokens, float *out_logits) {
+    return decode(m, s, pos, steps, out_tokens, out_logits, nullptr);
+}
+
+int th_decode_sample(th_model *m, th_state *s, size_t pos, size_t steps, float temperature, size_t top_k,
+                     float top_p, uint64_t *rng, uint32_t *out_tokens) {
+    TH_REQUIRE(rng, "th_decode_sample: null generator state");
+    if (temperature == 0.0f) return decode(m, s, pos, steps, out_tokens, nullptr, nullptr);
+    TH_REQUIRE(m, "th_decode_sample: null model");
+    const size_t vocab = (size_t)m->c.vocab_size;
+    const size_t k = std::min(std::max<size_t>(top_k, 1), vocab);
+    TH_REQUIRE(k <= (size_t)th::kSampleMaxTopK, "top_k %zu: the device samples from at most %d candidates", k,
+               th::kSampleMaxTopK);
+    TH_REQUIRE(vocab <= th::kSampleMaxVocab, "sampling over %zu values: at most %zu", vocab, th::kSampleMaxVocab);
+    TH_REQUIRE(top_p > 0.0f, "top_p must be greater than 0");
+    th::SampleState ss{*rng, *rng, temperature, top_p, (int)k, 0};
+    TRY(decode(m, s, pos, steps, out_tokens, nullptr, &ss));
+    // The device drew once more than `steps` (the pick after the last fed
+    // token, which the next call draws again): hand back the state after the
+    // steps-th draw, as the reference's sampler would have it.
+    *rng = steps ? ss.rng_prev : ss.rng;
     return TH_OK;
 }
 

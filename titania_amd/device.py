@@ -170,5 +170,15 @@ class Hip:
         check(lib().th_argmax(self.handle, logits.handle, C.byref(tok)))
         return int(tok.value)
 
+    def sample(self, logits: Buffer, sampler) -> int:
+        """A draw of `sampler` (titania_amd.sampler.Sampler) from the buffer's
+        values (th_sample); advances sampler.rng."""
+        tok = C.c_uint32()
+        st = C.c_uint64(sampler.rng)
+        check(lib().th_sample(self.handle, logits.handle, sampler.temperature, max(sampler.top_k, 0),
+                              sampler.top_p, C.byref(st), C.byref(tok)))
+        sampler.rng = st.value
+        return int(tok.value)
+
 
 __all__ = ["Hip", "Tensor", "Weight", "Buffer", "_lib"]

@@ -64,10 +64,20 @@ class Model:
                                logits.ctypes.data if want_logits else None, int(path)))
         return logits
 
-    def decode(self, state: "State", pos: int, steps: int, keep_logits: bool = False):
-        """Greedy decode on the device from position `pos`: returns the `steps`
-        picked tokens (and, with keep_logits, the logits after each fed token)."""
+    def decode(self, state: "State", pos: int, steps: int, keep_logits: bool = False, sampler=None):
+        """Decode on the device from position `pos`: returns the `steps`
+        tokens (and, with keep_logits, the logits after each fed token).
+        Greedy, or drawn by `sampler` (titania_amd.sampler.Sampler, whose rng
+        advances by `steps` draws)."""
         toks = np.empty(steps, dtype=np.uint32)
+        if sampler is not None:
+            if keep_logits:
+                raise ValueError("a sampled decode keeps its logits on the device")
+            st = C.c_uint64(sampler.rng)
+            check(lib().th_decode_sample(self.handle, state.handle, int(pos), int(steps), sampler.temperature,
+                                         max(sampler.top_k, 0), sampler.top_p, C.byref(st), toks.ctypes.data))
+            sampler.rng = st.value
+            return toks
         logits = np.empty((steps, self.config.vocab_size), dtype=np.float32) if keep_logits else None
         check(lib().th_decode(self.handle, state.handle, int(pos), int(steps), toks.ctypes.data,
                               logits.ctypes.data if keep_logits else None))
