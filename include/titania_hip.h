@@ -147,6 +147,21 @@ TH_API int th_model_create(th_device *dev, const th_config *config, const th_wei
                     th_model **out);
 TH_API void th_model_destroy(th_model *model);
 
+/* model/config.rs:29-35 `Config::load`: the architecture from a Hugging Face
+ * config.json as serde reads it (unsigned sizes from integer literals, the two
+ * f32 fields from any number, head_dim absent or null -> hidden_size /
+ * num_attention_heads, tie_word_embeddings absent -> false, other keys
+ * ignored). Needs no GPU. */
+TH_API int th_config_load(const char *path, th_config *out);
+/* model/model.rs:40-77 `Model::load`: config.json and model.safetensors from
+ * `dir` (model/weights.rs:19-81: every tensor BF16; q_norm / k_norm optional;
+ * lm_head.weight only when not tied), uploaded to `dev`. Errors name the file,
+ * or the tensor that is missing or not BF16. The model owns these weights and
+ * frees them in th_model_destroy. */
+TH_API int th_model_load(th_device *dev, const char *dir, th_model **out);
+/* The architecture a model was built with. */
+TH_API int th_model_config(const th_model *model, th_config *out);
+
 #define TH_KV_F32 0  /* f32 caches, as the reference stores them (model/model.rs:206-207) */
 #define TH_KV_BF16 1 /* bf16 caches: half the bytes per position */
 

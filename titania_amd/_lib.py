@@ -79,6 +79,9 @@ SIGNATURES: dict[str, tuple] = {
     "th_sample": (_I, [_P, _P, C.c_float, _SZ, C.c_float, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)]),
     "th_model_create": (_I, [_P, C.POINTER(ThConfig), C.POINTER(_P), _SZ, C.POINTER(_P)]),
     "th_model_destroy": (None, [_P]),
+    "th_config_load": (_I, [C.c_char_p, C.POINTER(ThConfig)]),
+    "th_model_load": (_I, [_P, C.c_char_p, C.POINTER(_P)]),
+    "th_model_config": (_I, [_P, C.POINTER(ThConfig)]),
     "th_state_create": (_I, [_P, _SZ, _I, C.POINTER(_P)]),
     "th_state_destroy": (None, [_P]),
     "th_forward": (_I, [_P, _P, _P, _SZ, _SZ, _P, _I]),

@@ -32,6 +32,22 @@ class Config:
             1 if self.tie_word_embeddings else 0,
         )
 
+    @classmethod
+    def from_c(cls, c: ThConfig, qk_norm: bool = True) -> "Config":
+        return cls(int(c.hidden_size), int(c.intermediate_size), int(c.num_hidden_layers),
+                   int(c.num_attention_heads), int(c.num_key_value_heads), int(c.vocab_size),
+                   float(c.rms_norm_eps), float(c.rope_theta), bool(c.tie_word_embeddings), int(c.head_dim), qk_norm)
+
+    @classmethod
+    def load(cls, path) -> "Config":
+        """model/config.rs:29-31 `Config::load` of a Hugging Face config.json
+        (th_config_load; no GPU needed)."""
+        from ._lib import check, lib
+        import ctypes as C
+        out = ThConfig()
+        check(lib().th_config_load(str(path).encode(), C.byref(out)))
+        return cls.from_c(out)
+
     def with_layers(self, n: int) -> "Config":
         return replace(self, num_hidden_layers=n)
 

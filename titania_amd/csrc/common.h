@@ -27,6 +27,10 @@ struct th_device {
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
 };
 
+// A model takes ownership of weight handles it frees on destruction (the
+// handles th_model_load uploads); null entries are skipped.
+void th_model_own_weights(th_model *m, th_weight *const *w, size_t n);
+
 struct th_buffer {
     float *ptr = nullptr;
     size_t len = 0;  // current length
@@ -62,6 +66,13 @@ void *scratch(th_device *dev, size_t bytes);
 #define TH_REQUIRE(cond, ...)                                  \
     do {                                                       \
         if (!(cond)) return th::fail(TH_ERR_INVALID, __VA_ARGS__); \
+    } while (0)
+
+// Returns the status of `call` from the enclosing function unless it is TH_OK.
+#define TRY(call)                 \
+    do {                          \
+        int rc_ = (call);         \
+        if (rc_ != TH_OK) return rc_; \
     } while (0)
 
 // Kernel launchers (host functions defined next to their kernels). Each queues

@@ -42,7 +42,13 @@ struct th_model {
     std::vector<Layer> layers;
     const th_weight *embed = nullptr, *norm = nullptr, *lm_head = nullptr;
     const th_weight *out_proj() const { return lm_head ? lm_head : embed; }  // model.rs:147
+    std::vector<th_weight *> owned;  // freed with the model (th_model_load)
 };
+
+void th_model_own_weights(th_model *m, th_weight *const *w, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if (w[i]) m->owned.push_back(w[i]);
+}
 
 struct th_state {
     th_model *m = nullptr;
@@ -179,12 +185,6 @@ int ensure_ops_state(th_state *s) {
     }
     return TH_OK;
 }
-
-#define TRY(call)                 \
-    do {                          \
-        int rc_ = (call);         \
-        if (rc_ != TH_OK) return rc_; \
-    } while (0)
 
 // model/model.rs:93-149, one primitive per step, for n <= BATCH tokens.
 int forward_batch_ops(th_state *s, const uint32_t *tokens, size_t n, size_t pos) {
@@ -779,7 +779,17 @@ int th_model_create(th_device *dev, const th_config *config, const th_weight *co
     return TH_OK;
 }
 
-void th_model_destroy(th_model *m) { delete m; }
+void th_model_destroy(th_model *m) {
+    if (!m) return;
+    for (th_weight *w : m->owned) th_weight_free(m->dev, w);
+    delete m;
+}
+
+int th_model_config(const th_model *m, th_config *out) {
+    TH_REQUIRE(m && out, "th_model_config: null argument");
+    *out = m->c;
+    return TH_OK;
+}
 
 int th_state_create(th_model *m, size_t max_len, int kv_dtype, th_state **out) {
     TH_REQUIRE(m && out, "th_state_create: null argument");

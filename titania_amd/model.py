@@ -9,7 +9,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, check, lib
+from ._lib import TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, ThConfig, check, lib
 from .config import Config
 from .device import Hip, Tensor, Weight
 from .synth import layer_names
@@ -44,6 +44,21 @@ class Model:
         out = C.c_void_p()
         check(lib().th_model_create(device.handle, C.byref(cfg), arr, len(self._weights), C.byref(out)))
         self.handle = out.value
+
+    @classmethod
+    def load(cls, device: Hip, directory) -> "Model":
+        """model/model.rs:40-77 `Model::load`: config.json and model.safetensors
+        from `directory`, read and uploaded by the library (th_model_load)."""
+        out = C.c_void_p()
+        check(lib().th_model_load(device.handle, str(directory).encode(), C.byref(out)))
+        cfg = ThConfig()
+        check(lib().th_model_config(out.value, C.byref(cfg)))
+        self = cls.__new__(cls)
+        self.device = device
+        self.config = Config.from_c(cfg)
+        self._weights = []  # owned by the library's model
+        self.handle = out.value
+        return self
 
     def close(self) -> None:
         if self.handle:
