@@ -183,24 +183,57 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnKernelArgs a) {
 
 // Merges the splits of one (token, head): rescales each split's sum and
 // accumulator by exp(m_split - m_max); empty splits (m = -inf) add nothing.
-__global__ void attn_combine_kernel(float *__restrict__ out, const float *__restrict__ part_acc,
-                                    const float *__restrict__ part_ml, int nsplit, int hd) {
+// Every split's statistics and accumulator rows are read in parallel (threads
+// over splits, then over (dimension, group of splits)), not one after another.
+constexpr int kCombineThreads = 256, kMaxSplits = 256;
+
+__global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__restrict__ out,
+                                                                      const float *__restrict__ part_acc,
+                                                                      const float *__restrict__ part_ml, int nsplit,
+                                                                      int hd) {
+    __shared__ float w[kMaxSplits];
+    __shared__ float red[kCombineThreads / 64];
+    __shared__ float acc_red[kCombineThreads];
     const long long th = blockIdx.x;  // token * n_heads + head
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *ml = part_ml + th * nsplit * 2;
     float m = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) m = fmaxf(m, ml[2 * s]);
+    for (int s = tid; s < nsplit; s += kCombineThreads) m = fmaxf(m, ml[2 * s]);
+    m = wave_max_dpp(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
     float l = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-        float ms = ml[2 * s];
-        if (ms != -INFINITY) l += ml[2 * s + 1] * expf(ms - m);
+    for (int s = tid; s < nsplit; s += kCombineThreads) {
+        const float ms = ml[2 * s];
+        const float ws = ms != -INFINITY ? expf(ms - m) : 0.f;
+        w[s] = ws;
+        l += ml[2 * s + 1] * ws;
     }
-    for (int dd = threadIdx.x; dd < hd; dd += blockDim.x) {
+    l = wave_sum_dpp(l);
+    if (lane == 0) red[wave] = l;
+    __syncthreads();
+    l = ((red[0] + red[1]) + red[2]) + red[3];
+    // groups of splits per dimension: thread t takes dimension t % hd of the
+    // splits s = t / hd, + groups, ...
+    const int groups = hd < kCombineThreads ? kCombineThreads / hd : 1;
+    for (int d0 = 0; d0 < hd; d0 += kCombineThreads) {
+        const int d = d0 + tid % hd, grp = tid / hd;
         float acc = 0.f;
-        for (int s = 0; s < nsplit; ++s) {
-            float ms = ml[2 * s];
-            if (ms != -INFINITY) acc += part_acc[(th * nsplit + s) * hd + dd] * expf(ms - m);
+        if (d < hd && grp < groups) {
+            const float *pa = part_acc + th * nsplit * hd + d;
+#pragma unroll 8
+            for (int s = grp; s < nsplit; s += groups) acc += pa[(size_t)s * hd] * w[s];
         }
-        out[th * hd + dd] = acc / l;
+        acc_red[tid] = acc;
+        __syncthreads();
+        if (grp == 0 && d < hd) {
+            float sum = 0.f;
+            for (int gi = 0; gi < groups; ++gi) sum += acc_red[gi * hd + tid % hd];
+            out[th * hd + d] = sum / l;
+        }
+        __syncthreads();
     }
 }
 
@@ -222,7 +255,8 @@ size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit) 
 
 hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,
                                int nsplit, int hd) {
-    attn_combine_kernel<<<dim3((unsigned)heads), dim3(hd), 0, s>>>(out, part_acc, part_ml, nsplit, hd);
+    if (nsplit > kMaxSplits) return hipErrorInvalidValue;
+    attn_combine_kernel<<<dim3((unsigned)heads), dim3(kCombineThreads), 0, s>>>(out, part_acc, part_ml, nsplit, hd);
     return hipGetLastError();
 }
 
@@ -365,9 +399,7 @@ static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
         attn_split_kernel<HD, float><<<grid, 256, 0, s>>>(k);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || k.nsplit == 1) return e;
-    attn_combine_kernel<<<dim3((unsigned)(n * (size_t)k.n_heads)), dim3(HD), 0, s>>>(k.out, k.part_acc, k.part_ml,
-                                                                                     k.nsplit, HD);
-    return hipGetLastError();
+    return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, HD);
 }
 
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim) {

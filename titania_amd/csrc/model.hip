@@ -330,7 +330,8 @@ int ensure_fused_state(th_state *s) {
     TH_HIP(hipMalloc(&s->kv, kv_bytes + (size_t)th::kStepKvTailRows * hd * sizeof(float)));
     // Attention partials: enough for any chunk of up to fb tokens at any context
     // up to max_len (the split count only grows with the context).
-    s->attn_part_floats = 0;
+    s->attn_part_floats = th::attention_scratch(1, (size_t)c.num_attention_heads, hd,
+                                                th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16));
     for (size_t n = 1; n <= s->fb; ++n) {
         int ns = th::attention_splits(n, (size_t)c.num_key_value_heads, s->max_len);
         s->attn_part_floats =
@@ -381,7 +382,7 @@ int enqueue_step(th_state *s) {
     const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads;
     const int qd = nh * hd, kvd = nkv * hd, V = (int)c.vocab_size;
     const float eps = c.rms_norm_eps;
-    const int nsplit = th::attention_splits(1, (size_t)nkv, s->max_len);
+    const int nsplit = th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
     // One launch for q/k/v and attention while one split covers the context.

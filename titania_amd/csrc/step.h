@@ -58,6 +58,10 @@ struct StepAttnArgs {
     float *part_ml;   // [n_heads][nsplit][2]
 };
 
+// Splits of the context launch_step_attention wants for caches of max_len
+// positions: one up to 512, else one per register pass of rows (128 bf16 or
+// 64 f32 positions), at most 256.
+int step_attention_splits(size_t max_len, int kv_bf16);
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a);
 
 // The q/k/v GEMV (as launch_step_qkv) and single-split attention in one launch:

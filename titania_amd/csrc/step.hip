@@ -15,6 +15,8 @@
 // weight rows first (they do not depend on the activations), then builds the
 // normalized input in LDS while those loads are in flight, then reduces one
 // row per wave with DPP.
+#include <algorithm>
+
 #include "common.h"
 #include "device_util.h"
 #include "step.h"
@@ -388,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
     const int ngemv = (a.n_rows + RPB - 1) / RPB;
     const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
-        attend_words<G, KV>(q.at, blockIdx.x - ngemv, q.words, epoch, q.err);
+        attend_regs<G, KV, true>(q.at, blockIdx.x - ngemv, 0, q.at.head_stride / 128, q.words, epoch, q.err);
         return;
     }
     extern __shared__ float xs[];
@@ -436,6 +438,26 @@ hipError_t qkv_attn_g(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a
     case 4: return qkv_attn_launch<CPL, 4>(s, q, a);
     default: return hipErrorInvalidValue;
     }
+}
+
+// One block per (KV head, split of `chunk` positions), cached rows in registers.
+template <int G, typename KV>
+__global__ __launch_bounds__(kThreads) void step_attention_regs_kernel(StepAttnArgs a, long long chunk) {
+    attend_regs<G, KV, false>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, chunk, nullptr, 0, nullptr);
+}
+
+template <int G>
+hipError_t attn_regs_launch(hipStream_t s, const StepAttnArgs &a) {
+    const long long max_len = a.head_stride / 128;
+    const int rows = a.kv_bf16 ? KvRegs<uint16_t>::kRows : KvRegs<float>::kRows;
+    long long chunk = (max_len + a.nsplit - 1) / a.nsplit;
+    chunk = (chunk + rows - 1) / rows * rows;
+    dim3 grid((unsigned)(a.n_kv_heads * a.nsplit));
+    if (a.kv_bf16)
+        step_attention_regs_kernel<G, uint16_t><<<grid, kThreads, 0, s>>>(a, chunk);
+    else
+        step_attention_regs_kernel<G, float><<<grid, kThreads, 0, s>>>(a, chunk);
+    return hipGetLastError();
 }
 
 template <int HD, int G>
@@ -564,11 +586,17 @@ hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
     }
 }
 
+int step_attention_splits(size_t max_len, int kv_bf16) {
+    if (max_len <= 512) return 1;
+    const size_t rows = kv_bf16 ? KvRegs<uint16_t>::kRows : KvRegs<float>::kRows;
+    return (int)std::min<size_t>((max_len + rows - 1) / rows, 256);
+}
+
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a) {
     switch (a.n_heads / a.n_kv_heads) {
     case 1: return attn_launch<128, 1>(s, a);
-    case 2: return attn_launch<128, 2>(s, a);
-    case 4: return attn_launch<128, 4>(s, a);
+    case 2: return attn_regs_launch<2>(s, a);
+    case 4: return attn_regs_launch<4>(s, a);
     case 8: return attn_launch<128, 8>(s, a);
     default: return hipErrorInvalidValue;
     }

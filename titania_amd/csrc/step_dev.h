@@ -163,21 +163,28 @@ template <> struct KvRegs<uint16_t> {
     }
 };
 
-// Attention of one KV head over the whole context by one block, from q/k/v
-// (value | epoch << 32) words that other blocks of the same launch write.
-// The first pass's cached rows are requested before anything else, without
-// waiting for the position: rows past the context are read (always inside the
-// cache's max_len rows) and then ignored. Later passes request their rows as
-// soon as the previous pass has used the registers. Reductions are DPP.
-template <int G, typename KV>
-__device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const unsigned long long *words,
-                                             unsigned epoch, unsigned *err) {
+// Attention of one KV head by one block over the positions [s0, s0 + chunk)
+// of the context, s0 = split * chunk: the whole context (split 0, chunk
+// max_len) or one split of it. The raw q/k/v come from a.qkv, or (WORDS) from
+// (value | epoch << 32) words that other blocks of the same launch write,
+// polled until they all carry `epoch` (bounded: about 2 s, then *err counts
+// the failure and the block goes on). The first pass's cached rows are
+// requested before anything else, without waiting for the position: rows past
+// the context are read and then ignored (a pass starts below max_len and the
+// caches' allocation extends kStepKvTailRows rows past the last head). Later
+// passes request their rows as soon as the previous pass has used the
+// registers. Reductions are DPP. The output goes to a.out with one split,
+// else (sum, max, denominator) partials for launch_attn_combine.
+template <int G, typename KV, bool WORDS>
+__device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int split, long long chunk,
+                                            const unsigned long long *words, unsigned epoch, unsigned *err) {
     using R = KvRegs<KV>;
     constexpr int HD = 128, HALF = HD / 2, ROWS = R::kRows;
     constexpr int NK = ROWS / 16;  // keys per lane in the score pass
     constexpr int NV = ROWS / 8;   // keys per lane in the value pass
     constexpr int HPW = (G + 1 + kWaves - 1) / kWaves;
     static_assert(G <= kWaves, "one wave per q head in the softmax");
+    static_assert(ROWS <= kStepKvTailRows, "pass longer than the caches' tail");
     __shared__ float hq[G * HD], hk[HD], hv[HD];
     __shared__ float scores[G][ROWS];
     __shared__ float st_m[G], st_l[G], st_a[G];
@@ -186,13 +193,12 @@ __device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const
     const int sub = lane & 15, kq = wave * 4 + (lane >> 4);  // score pass: dims 8*sub.., key kq of 16
     const int d4 = tid & 31, pv = tid >> 5;                   // value pass: dims 4*d4.., key pv of 8
     const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
+    const long long max_len = a.head_stride / HD;
+    const long long s0 = (long long)split * chunk;
     const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
     const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
     typename R::K kr[NK];
     typename R::V vr[NV];
-    // A pass reads up to ROWS - 1 rows past the context; the caches' allocation
-    // extends kStepKvTailRows rows past the last head, so this stays inside it.
-    static_assert(ROWS <= kStepKvTailRows, "pass longer than the caches' tail");
     auto load_k = [&](long long c0) {
 #pragma unroll
         for (int i = 0; i < NK; ++i) kr[i] = R::load_k(kc + (c0 + i * 16) * HD + kq * HD, sub);
@@ -201,52 +207,62 @@ __device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const
 #pragma unroll
         for (int i = 0; i < NV; ++i) vr[i] = R::load_v(vc + (c0 + i * 8) * HD + pv * HD, d4);
     };
-    load_k(0);
-    load_v(0);
-    // RMSNorm gains of this wave's heads (q heads 0..G-1, then k).
-    float ga[HPW], gb[HPW];
+    if (s0 < max_len) {
+        load_k(s0);
+        load_v(s0);
+    }
+    // RMSNorm gains of this wave's heads (q heads 0..G-1, then k), and, from
+    // a.qkv, the raw rows: all requested before the position is known.
+    float ga[HPW], gb[HPW], av[HPW], bv[HPW], vnew = 0.f;
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
         const int h = wave + hh * kWaves;
         ga[hh] = gb[hh] = 1.f;
+        av[hh] = bv[hh] = 0.f;
         const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
         if (h <= G && gain) {
             ga[hh] = bf16_to_f32(gain[lane]);
             gb[hh] = bf16_to_f32(gain[lane + HALF]);
         }
+        if (!WORDS && h <= G) {
+            const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
+            av[hh] = x[lane];
+            bv[hh] = x[lane + HALF];
+        }
     }
+    if (!WORDS && tid < HD) vnew = a.qkv[qd + kvd + (size_t)g * HD + tid];
     const long long pos = *a.pos;
     const long long len = pos + 1;
     const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
-    // Poll until every q/k/v word this block needs carries `epoch` (bounded:
-    // about 2 s, then *err counts the failure and the block goes on).
-    float av[HPW], bv[HPW], vnew = 0.f;
-    for (int it = 0;; ++it) {
-        int ok = 1;
+    if (WORDS) {
+        for (int it = 0;; ++it) {
+            int ok = 1;
 #pragma unroll
-        for (int hh = 0; hh < HPW; ++hh) {
-            const int h = wave + hh * kWaves;
-            av[hh] = bv[hh] = 0.f;
-            if (h <= G) {
-                const unsigned long long *x = h < G ? words + (size_t)(g * G + h) * HD : words + qd + (size_t)g * HD;
-                const unsigned long long wa = __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const unsigned long long wb =
-                    __hip_atomic_load(x + lane + HALF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok &= (unsigned)(wa >> 32) == epoch && (unsigned)(wb >> 32) == epoch;
-                av[hh] = __uint_as_float((unsigned)wa);
-                bv[hh] = __uint_as_float((unsigned)wb);
+            for (int hh = 0; hh < HPW; ++hh) {
+                const int h = wave + hh * kWaves;
+                if (h <= G) {
+                    const unsigned long long *x =
+                        h < G ? words + (size_t)(g * G + h) * HD : words + qd + (size_t)g * HD;
+                    const unsigned long long wa =
+                        __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const unsigned long long wb =
+                        __hip_atomic_load(x + lane + HALF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok &= (unsigned)(wa >> 32) == epoch && (unsigned)(wb >> 32) == epoch;
+                    av[hh] = __uint_as_float((unsigned)wa);
+                    bv[hh] = __uint_as_float((unsigned)wb);
+                }
             }
-        }
-        if (tid < HD) {
-            const unsigned long long wv =
-                __hip_atomic_load(words + qd + kvd + (size_t)g * HD + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            ok &= (unsigned)(wv >> 32) == epoch;
-            vnew = __uint_as_float((unsigned)wv);
-        }
-        if (__syncthreads_and(ok)) break;
-        if (it >= (1 << 21)) {
-            if (tid == 0) atomicAdd(err, 1u);
-            break;
+            if (tid < HD) {
+                const unsigned long long wv = __hip_atomic_load(words + qd + kvd + (size_t)g * HD + tid,
+                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok &= (unsigned)(wv >> 32) == epoch;
+                vnew = __uint_as_float((unsigned)wv);
+            }
+            if (__syncthreads_and(ok)) break;
+            if (it >= (1 << 21)) {
+                if (tid == 0) atomicAdd(err, 1u);
+                break;
+            }
         }
     }
     if (tid < G) {
@@ -277,9 +293,10 @@ __device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const
     for (int gg = 0; gg < G; ++gg)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[gg][i] = 0.f;
-    for (long long c0 = 0; c0 < len; c0 += ROWS) {
-        const int cnt = (int)(len - c0 < ROWS ? len - c0 : ROWS);
-        const bool more = c0 + ROWS < len;
+    const long long s1 = s0 + chunk < len ? s0 + chunk : len;
+    for (long long c0 = s0; c0 < s1; c0 += ROWS) {
+        const int cnt = (int)(s1 - c0 < ROWS ? s1 - c0 : ROWS);
+        const bool more = c0 + ROWS < s1;
         // Scores: positions below pos come from the cache, pos itself is the
         // new key. q is read from LDS once per pass, all heads together.
         float qf[G][8];
@@ -293,11 +310,11 @@ __device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const
             if (c0 + j == pos) lds_row8(hk, sub, kf);
 #pragma unroll
             for (int gg = 0; gg < G; ++gg) {
-                float s = 0.f;
+                float sc = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) s = fmaf(qf[gg][e], kf[e], s);
-                s = row_sum_dpp(s);
-                if (sub == 0 && j < cnt) scores[gg][j] = scale * s;
+                for (int e = 0; e < 8; ++e) sc = fmaf(qf[gg][e], kf[e], sc);
+                sc = row_sum_dpp(sc);
+                if (sub == 0 && j < cnt) scores[gg][j] = scale * sc;
             }
         }
         if (more) load_k(c0 + ROWS);
@@ -336,7 +353,7 @@ __device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const
         for (int i = 0; i < NV; ++i)
 #pragma unroll
             for (int gg = 0; gg < G; ++gg) pw[i][gg] = i * 8 + pv < cnt ? scores[gg][i * 8 + pv] : 0.f;
-        const int fresh = (int)(pos - c0) - pv;  // slot * 8 of the key at pos, if this lane holds it
+        const long long fresh = pos - c0 - pv;  // slot * 8 of the key at pos, if this lane holds it
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int j = i * 8 + pv;
@@ -356,9 +373,9 @@ __device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const
         if (more) load_v(c0 + ROWS);
         __syncthreads();  // scores are rewritten by the next pass
     }
-    // The new key and value at pos (model.rs:119-120); no block of this launch
-    // reads that position from the caches.
-    if (tid < HD) {
+    // The split holding pos appends the new key and value (model.rs:119-120);
+    // no block of this launch reads that position from the caches.
+    if (pos >= s0 && pos < s0 + chunk && tid < HD) {
         store_kv(const_cast<KV *>(kc) + pos * HD + tid, hk[tid]);
         store_kv(const_cast<KV *>(vc) + pos * HD + tid, hv[tid]);
     }
@@ -374,7 +391,17 @@ __device__ __forceinline__ void attend_words(const StepAttnArgs &a, int g, const
     for (int idx = tid; idx < G * HD; idx += kThreads) {
         const int gg = idx / HD, d = idx % HD;
         const float sm = ((red[gg][0][d] + red[gg][1][d]) + red[gg][2][d]) + red[gg][3][d];
-        a.out[((size_t)g * G + gg) * HD + d] = sm / st_l[gg];
+        const long long h = (long long)g * G + gg;
+        if (a.nsplit == 1) {
+            a.out[h * HD + d] = sm / st_l[gg];
+        } else {
+            const long long slot = h * a.nsplit + split;
+            a.part_acc[slot * HD + d] = sm;
+            if (d == 0) {
+                a.part_ml[slot * 2] = st_m[gg];
+                a.part_ml[slot * 2 + 1] = st_l[gg];
+            }
+        }
     }
 }
 
