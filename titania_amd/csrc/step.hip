@@ -440,9 +440,11 @@ hipError_t qkv_attn_g(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a
     }
 }
 
-// One block per (KV head, split of `chunk` positions), cached rows in registers.
+// One block per (KV head, split of `chunk` positions), cached rows in
+// registers; at most 168 VGPRs, so that three blocks fit on a CU.
 template <int G, typename KV>
-__global__ __launch_bounds__(kThreads) void step_attention_regs_kernel(StepAttnArgs a, long long chunk) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void step_attention_regs_kernel(StepAttnArgs a, long long chunk) {
     attend_regs<G, KV, false>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, chunk, nullptr, 0, nullptr);
 }
 

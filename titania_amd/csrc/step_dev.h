@@ -346,28 +346,33 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int sp
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[gg][i] *= al;
         }
-        // Weights of this lane's keys, all read before any is used (0 past the
-        // context, where the value registers hold rows that are not used).
-        float pw[NV][G];
-#pragma unroll
-        for (int i = 0; i < NV; ++i)
-#pragma unroll
-            for (int gg = 0; gg < G; ++gg) pw[i][gg] = i * 8 + pv < cnt ? scores[gg][i * 8 + pv] : 0.f;
+        // Weights of this lane's keys, eight keys at a time, all of a chunk
+        // read before any is used (0 past the context, where the value
+        // registers hold rows that are not used).
         const long long fresh = pos - c0 - pv;  // slot * 8 of the key at pos, if this lane holds it
+        constexpr int PC = NV < 8 ? NV : 8;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = i * 8 + pv;
-            if (j < cnt) {
-                float vf[4];
-                R::unpack_v(vr[i], vf);
-                if (fresh == i * 8) {
-                    const float4 n = reinterpret_cast<const float4 *>(hv)[d4];
-                    vf[0] = n.x; vf[1] = n.y; vf[2] = n.z; vf[3] = n.w;
-                }
+        for (int i0 = 0; i0 < NV; i0 += PC) {
+            float pw[PC][G];
+#pragma unroll
+            for (int i = 0; i < PC; ++i)
 #pragma unroll
                 for (int gg = 0; gg < G; ++gg)
+                    pw[i][gg] = (i0 + i) * 8 + pv < cnt ? scores[gg][(i0 + i) * 8 + pv] : 0.f;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[gg][e] = fmaf(pw[i][gg], vf[e], acc[gg][e]);
+            for (int i = 0; i < PC; ++i) {
+                if ((i0 + i) * 8 + pv < cnt) {
+                    float vf[4];
+                    R::unpack_v(vr[i0 + i], vf);
+                    if (fresh == (i0 + i) * 8) {
+                        const float4 n = reinterpret_cast<const float4 *>(hv)[d4];
+                        vf[0] = n.x; vf[1] = n.y; vf[2] = n.z; vf[3] = n.w;
+                    }
+#pragma unroll
+                    for (int gg = 0; gg < G; ++gg)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[gg][e] = fmaf(pw[i][gg], vf[e], acc[gg][e]);
+                }
             }
         }
         if (more) load_v(c0 + ROWS);
