@@ -390,6 +390,139 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnKernelArgs a, int n)
         }
 }
 
+// Prefill on the matrix cores (head_dim 128): one block per (tile of 64
+// consecutive tokens, query head), 16 tokens per wave. Key/value rows walk
+// through LDS 32 positions at a time (loaded one tile ahead, as f32); each
+// wave forms S = Q K^T for its 16 queries with v_mfma_f32_16x16x4f32 (f32
+// products, f32 sums), applies the causal mask and the online softmax along
+// its 16-lane rows, passes P through LDS into the A-operand layout and adds
+// P V into 16 x 128 f32 accumulators. Layout of 16x16x4 (checked on the GPU):
+// lane l holds A[l%16][l/16] and B[l/16][l%16], and D[4(l/16)+e][l%16].
+constexpr int kMQT = 64, kMKT = 32;
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dpp_get<0xB1>(v, -INFINITY));
+    v = fmaxf(v, dpp_get<0x4E>(v, -INFINITY));
+    v = fmaxf(v, dpp_get<0x124>(v, -INFINITY));
+    v = fmaxf(v, dpp_get<0x128>(v, -INFINITY));
+    return v;
+}
+
+template <typename KV>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n) {
+    constexpr int HD = 128, KS = HD + 4, VS = HD + 16, PS = kMKT + 4;  // LDS row strides (floats)
+    __shared__ float ks[kMKT * KS];
+    __shared__ float vs[kMKT * VS];
+    __shared__ float ps[4][16 * PS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lk = lane >> 4;
+    const int h = blockIdx.y, g = h / a.group;
+    const int t0 = blockIdx.x * kMQT;
+    const int nq = n - t0 < kMQT ? n - t0 : kMQT;
+    const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
+    // Q in the A-operand layout: qa[k] = Q[query li of the wave][4k + lk].
+    const int tq = t0 + wave * 16 + li;
+    float qa[HD / 4];
+    {
+        const float *qp = a.q + ((long long)(tq < n ? tq : 0) * a.n_heads + h) * HD + lk;
+#pragma unroll
+        for (int k = 0; k < HD / 4; ++k) qa[k] = tq < n ? qp[4 * k] : 0.f;
+    }
+    const KV *kb = reinterpret_cast<const KV *>(a.k) + (long long)g * a.head_stride;
+    const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
+    const long long last = pos + t0 + nq - 1;                       // the block's last query position
+    const long long wlast = pos + t0 + wave * 16 + 15;              // this wave's last query position
+    floatx4 o[HD / 16];
+    float m[4], l[4];
+#pragma unroll
+    for (int d = 0; d < HD / 16; ++d) o[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+    }
+    constexpr int PER = kMKT * HD / 4 / 256;  // float4 of K (and of V) per thread per tile
+    float4 kr4[PER], vr4[PER];
+    auto fetch = [&](long long c0) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
+            const long long p = c0 + row;
+            kr4[u] = vr4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p <= last) {
+                kr4[u] = load4(kb + p * a.pos_stride + c4 * 4);
+                vr4[u] = load4(vb + p * a.pos_stride + c4 * 4);
+            }
+        }
+    };
+    fetch(0);
+    for (long long c0 = 0; c0 <= last; c0 += kMKT) {
+        __syncthreads();  // the previous tile is consumed
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
+            *reinterpret_cast<float4 *>(ks + row * KS + c4 * 4) = kr4[u];
+            *reinterpret_cast<float4 *>(vs + row * VS + c4 * 4) = vr4[u];
+        }
+        __syncthreads();
+        if (c0 + kMKT <= last) fetch(c0 + kMKT);
+        if (c0 > wlast) continue;  // every query of this wave precedes the tile
+        // S for keys c0 + [0, 16) and c0 + [16, 32).
+        floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < HD / 4; ++k) {
+            const float b0 = ks[li * KS + 4 * k + lk], b1 = ks[(16 + li) * KS + 4 * k + lk];
+            s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[k], b0, s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[k], b1, s1, 0, 0, 0);
+        }
+        // Causal mask and online softmax of rows 4 lk + r (this lane: keys li, 16 + li).
+        float al[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int qi = wave * 16 + 4 * lk + r;  // query within the block
+            const long long qp = pos + t0 + qi;
+            const bool in = qi < nq;
+            const float v0 = in && c0 + li <= qp ? a.scale * s0[r] : -INFINITY;
+            const float v1 = in && c0 + 16 + li <= qp ? a.scale * s1[r] : -INFINITY;
+            const float mn = fmaxf(m[r], row_max16(fmaxf(v0, v1)));
+            const float p0 = v0 == -INFINITY ? 0.f : expf(v0 - mn);
+            const float p1 = v1 == -INFINITY ? 0.f : expf(v1 - mn);
+            al[r] = m[r] == -INFINITY ? 0.f : expf(m[r] - mn);
+            l[r] = l[r] * al[r] + row_sum_dpp(p0 + p1);
+            m[r] = mn;
+            ps[wave][(4 * lk + r) * PS + li] = p0;
+            ps[wave][(4 * lk + r) * PS + 16 + li] = p1;
+        }
+#pragma unroll
+        for (int d = 0; d < HD / 16; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[d][r] *= al[r];
+        // P back in the A-operand layout (same wave: LDS stays in order).
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float pa[kMKT / 4];
+#pragma unroll
+        for (int kk = 0; kk < kMKT / 4; ++kk) pa[kk] = ps[wave][li * PS + 4 * kk + lk];
+#pragma unroll
+        for (int kk = 0; kk < kMKT / 4; ++kk)
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d)
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[kk], vs[(4 * kk + lk) * VS + d * 16 + li], o[d], 0,
+                                                            0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int qi = wave * 16 + 4 * lk + r;
+        if (qi < nq) {
+            float *op = a.out + ((long long)(t0 + qi) * a.n_heads + h) * HD + li;
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d) op[d * 16] = o[d][r] / l[r];
+        }
+    }
+}
+
 template <int HD>
 static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
     dim3 grid((unsigned)(n * (size_t)k.n_kv_heads * (size_t)k.nsplit));
@@ -405,11 +538,11 @@ static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim) {
     if (n == 0) return hipSuccess;
     if (head_dim == 128 && n >= kAttnTileMin) {
-        dim3 grid((unsigned)((n + kQT - 1) / kQT), (unsigned)k.n_heads);
+        dim3 grid((unsigned)((n + kMQT - 1) / kMQT), (unsigned)k.n_heads);
         if (k.kv_bf16)
-            attn_tile_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
+            attn_mfma_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
         else
-            attn_tile_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
+            attn_mfma_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
         return hipGetLastError();
     }
     switch (head_dim) {

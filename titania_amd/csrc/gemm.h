@@ -27,12 +27,19 @@ struct GemmOut {
     float *out;
 };
 
-// Bytes of scratch launch_gemm_multi needs for n tokens of `cols` columns.
-size_t gemm_scratch_bytes(size_t n, size_t cols);
+// Most ways a single-matrix GEMM splits its K range (into partial tiles that a
+// second kernel sums in a fixed order).
+constexpr int kGemmMaxSplitK = 4;
+
+// Bytes of scratch launch_gemm_multi needs for n tokens of `cols` columns and
+// single-matrix outputs of up to `rows` rows (room for the split-K partials).
+size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows);
 
 // Up to three matrices that share the input x [n][cols], in two launches (the
-// activation split into `scratch`, then one GEMM over all their rows).
+// activation split into `scratch`, then one GEMM over all their rows); a
+// single matrix of few row tiles may split K, with partials in the rest of
+// `scratch` (scratch_bytes long) and a third launch that sums them.
 hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t cols, const GemmOut *outs, int n_outs,
-                             void *scratch);
+                             void *scratch, size_t scratch_bytes);
 
 }  // namespace th

@@ -97,17 +97,24 @@ __device__ __forceinline__ bf16x8 frag(const uint4 *tile, int row, int lc) {
     return __builtin_bit_cast(bf16x8, tile[row * CH + (lc ^ swz(row))]);
 }
 
+// With ksplit > 1 (one matrix), block z of the grid's third dimension takes
+// K steps [z nk / ksplit, (z + 1) nk / ksplit) and stores its partial tile in
+// part[z][t][r]; launch_gemm_multi then sums the partials in z order.
 __global__ __launch_bounds__(NTHR, 2) void gemm_kernel(Segs sg, const uint16_t *__restrict__ hi,
-                                                        const uint16_t *__restrict__ lo, int n, int cols) {
+                                                        const uint16_t *__restrict__ lo, int n, int cols,
+                                                        float *__restrict__ part, int ksplit) {
     __shared__ Stage ring[kStages];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = blockIdx.y * BM;
     int rl;
     const int sgi = seg_of(sg, blockIdx.x * BN, rl);
-    const uint16_t *w = sg.w[sgi] + (size_t)rl * cols;
     const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
     const int fr = lane & 15, fq = lane >> 4;  // fragment row, quarter of the K slice
-    const int nk = cols / BK;
+    const int nk_all = cols / BK, z = blockIdx.z;
+    const int kb = (int)((long long)z * nk_all / ksplit), nk = (int)((long long)(z + 1) * nk_all / ksplit) - kb;
+    const uint16_t *w = sg.w[sgi] + (size_t)rl * cols + (size_t)kb * BK;
+    hi += (size_t)kb * BK;
+    lo += (size_t)kb * BK;
 
     f32x4 acc[2][2];
 #pragma unroll
@@ -150,8 +157,8 @@ __global__ __launch_bounds__(NTHR, 2) void gemm_kernel(Segs sg, const uint16_t *
         }
     }
     // D[4 (l / 16) + i][l % 16]: token rows, weight-row columns.
-    float *out = sg.out[sgi];
     const int rows = sg.rows[sgi];
+    float *out = ksplit > 1 ? part + (size_t)z * n * rows : sg.out[sgi];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -180,6 +187,22 @@ __global__ void split_kernel(const float4 *__restrict__ x, uint2 *__restrict__ h
     }
 }
 
+// out[i] = sum over z < ksplit of part[z * m + i] (z in order), 4 a thread.
+__global__ void splitk_sum_kernel(const float4 *__restrict__ part, float4 *__restrict__ out, size_t m4, int ksplit) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < m4; i += stride) {
+        float4 acc = part[i];
+        for (int z = 1; z < ksplit; ++z) {
+            const float4 v = part[(size_t)z * m4 + i];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        out[i] = acc;
+    }
+}
+
 }  // namespace
 
 bool gemm_supported(size_t rows, size_t cols) {
@@ -187,10 +210,12 @@ bool gemm_supported(size_t rows, size_t cols) {
            rows * cols < ((size_t)1 << 40);
 }
 
-size_t gemm_scratch_bytes(size_t n, size_t cols) { return n * cols * 2 * sizeof(uint16_t); }
+size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows) {
+    return n * cols * 2 * sizeof(uint16_t) + (size_t)kGemmMaxSplitK * n * rows * sizeof(float);
+}
 
 hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t cols, const GemmOut *outs, int n_outs,
-                             void *scratch) {
+                             void *scratch, size_t scratch_bytes) {
     if (n == 0) return hipSuccess;
     if (n_outs < 1 || n_outs > 3 || !scratch || (n + BM - 1) / BM > 65535 || n > ((size_t)1 << 24))
         return hipErrorInvalidValue;
@@ -212,8 +237,23 @@ hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t col
                                         reinterpret_cast<uint2 *>(lo), n4);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    dim3 grid((unsigned)(total / BN), (unsigned)((n + BM - 1) / BM));
-    gemm_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols);
+    // A single matrix with few output tiles (o, down: 1024 rows) splits K so
+    // that the launch still fills the chip, when the scratch has room for
+    // the partial tiles.
+    const size_t tiles = (total / BN) * ((n + BM - 1) / BM), nk = cols / BK;
+    int ksplit = 1;
+    float *part = reinterpret_cast<float *>(hi + 2 * n * cols);
+    if (n_outs == 1)
+        while (ksplit < kGemmMaxSplitK && tiles * ksplit < 512 && (size_t)ksplit * 2 * 4 <= nk &&
+               n * cols * 4 + (size_t)ksplit * 2 * n * total * sizeof(float) <= scratch_bytes)
+            ksplit *= 2;
+    dim3 grid((unsigned)(total / BN), (unsigned)((n + BM - 1) / BM), (unsigned)ksplit);
+    gemm_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+    e = hipGetLastError();
+    if (e != hipSuccess || ksplit == 1) return e;
+    const size_t m4 = n * total / 4;
+    splitk_sum_kernel<<<(unsigned)std::min<size_t>((m4 + 255) / 256, 4096), 256, 0, s>>>(
+        reinterpret_cast<const float4 *>(part), reinterpret_cast<float4 *>(outs[0].out), m4, ksplit);
     return hipGetLastError();
 }
 
@@ -223,10 +263,11 @@ hipError_t launch_gemm(hipStream_t s, float *out, const uint16_t *w, size_t rows
     if (!gemm_supported(rows, cols)) return hipErrorInvalidValue;
     // The split activations live in stream-ordered scratch for this call.
     void *scratch = nullptr;
-    hipError_t e = hipMallocAsync(&scratch, gemm_scratch_bytes(n, cols), s);
+    const size_t bytes = gemm_scratch_bytes(n, cols, rows);
+    hipError_t e = hipMallocAsync(&scratch, bytes, s);
     if (e != hipSuccess) return e;
     const GemmOut o{w, rows, out};
-    e = launch_gemm_multi(s, x, n, cols, &o, 1, scratch);
+    e = launch_gemm_multi(s, x, n, cols, &o, 1, scratch, bytes);
     const hipError_t f = hipFreeAsync(scratch, s);
     return e != hipSuccess ? e : f;
 }

@@ -71,6 +71,7 @@ struct th_state {
           *fgate = nullptr, *fup = nullptr, *fy = nullptr;
     void *fsplit = nullptr;   // bf16 hi/lo halves of a GEMM input (fb tokens x fsplit_cols)
     size_t fsplit_cols = 0;
+    size_t fsplit_bytes = 0;
     void *kv = nullptr;  // all caches, one allocation
     size_t kv_elem = 4;
     float *attn_part = nullptr;  // attention partials for the fused path
@@ -321,7 +322,8 @@ int ensure_fused_state(th_state *s) {
     for (auto &b : bufs) TH_HIP(hipMalloc(b.p, s->fb * b.n * sizeof(float)));
     if (s->fb >= th::kGemmMinTokens) {
         s->fsplit_cols = std::max(std::max(H, qd), I);
-        TH_HIP(hipMalloc(&s->fsplit, th::gemm_scratch_bytes(s->fb, s->fsplit_cols)));
+        s->fsplit_bytes = th::gemm_scratch_bytes(s->fb, s->fsplit_cols, H);
+        TH_HIP(hipMalloc(&s->fsplit, s->fsplit_bytes));
     }
     s->kv_elem = s->kv_dtype == TH_KV_BF16 ? 2 : 4;
     size_t kv_bytes = (size_t)c.num_hidden_layers * 2 * kvd * s->max_len * s->kv_elem;
@@ -482,7 +484,7 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         TH_HIP(th::launch_add_rmsnorm(st, s->fx, i ? s->fy : nullptr, s->fxb, n, L.attn_norm->ptr, H, eps));
         if (use_gemm(H) && th::gemm_supported(qd, H) && th::gemm_supported(nkv * hd, H)) {
             const th::GemmOut o[3] = {{L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
-            TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 3, s->fsplit));
+            TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 3, s->fsplit, s->fsplit_bytes));
         } else {
             TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
             TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
@@ -530,14 +532,14 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
 
         if (use_gemm(qd) && th::gemm_supported(H, qd)) {
             const th::GemmOut o{L.o->ptr, H, s->fy};
-            TH_HIP(th::launch_gemm_multi(st, s->fatt, n, qd, &o, 1, s->fsplit));
+            TH_HIP(th::launch_gemm_multi(st, s->fatt, n, qd, &o, 1, s->fsplit, s->fsplit_bytes));
         } else {
             TH_HIP(th::launch_matmul(st, s->fy, L.o->ptr, H, qd, s->fatt, n));
         }
         TH_HIP(th::launch_add_rmsnorm(st, s->fx, s->fy, s->fxb, n, L.mlp_norm->ptr, H, eps));
         if (use_gemm(H) && th::gemm_supported(I, H)) {
             const th::GemmOut o[2] = {{L.gate->ptr, I, s->fgate}, {L.up->ptr, I, s->fup}};
-            TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 2, s->fsplit));
+            TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 2, s->fsplit, s->fsplit_bytes));
         } else {
             TH_HIP(th::launch_matmul(st, s->fgate, L.gate->ptr, I, H, s->fxb, n));
             TH_HIP(th::launch_matmul(st, s->fup, L.up->ptr, I, H, s->fxb, n));
@@ -545,7 +547,7 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         TH_HIP(th::launch_silu_mul(st, s->fgate, s->fup, n * I));
         if (use_gemm(I) && th::gemm_supported(H, I)) {
             const th::GemmOut o{L.down->ptr, H, s->fy};
-            TH_HIP(th::launch_gemm_multi(st, s->fgate, n, I, &o, 1, s->fsplit));
+            TH_HIP(th::launch_gemm_multi(st, s->fgate, n, I, &o, 1, s->fsplit, s->fsplit_bytes));
         } else {
             TH_HIP(th::launch_matmul(st, s->fy, L.down->ptr, H, I, s->fgate, n));
         }

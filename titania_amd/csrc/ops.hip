@@ -78,6 +78,10 @@ hipError_t launch_silu_mul(hipStream_t s, float *gate, const float *up, size_t l
 // model/cpu.rs:85-94, optionally preceded by the residual add of
 // model/model.rs:132/141: one wave per dim-long row. If y is given, x += y is
 // stored back into x; the normalized row goes to xb (which may be x).
+// NV > 0: dim == 256 * NV, each lane holds NV float4 of the row and issues all
+// their loads before using any (one memory round trip per row); NV == 0: any
+// dim, element by element.
+template <int NV>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ y,
                                                           float *xb, size_t rows, const uint16_t *__restrict__ w,
                                                           size_t dim, float eps) {
@@ -88,6 +92,39 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x,
     float *outr = xb + row * dim;
     const float *yr = y ? y + row * dim : nullptr;
     float ss = 0.f;
+    if (NV > 0) {
+        float4 v[NV > 0 ? NV : 1], u[NV > 0 ? NV : 1];
+        uint2 g[NV > 0 ? NV : 1];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int i = lane + 64 * k;
+            v[k] = reinterpret_cast<const float4 *>(xr)[i];
+            if (yr) u[k] = reinterpret_cast<const float4 *>(yr)[i];
+            g[k] = reinterpret_cast<const uint2 *>(w)[i];
+        }
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            if (yr) {
+                v[k].x = v[k].x + u[k].x;
+                v[k].y = v[k].y + u[k].y;
+                v[k].z = v[k].z + u[k].z;
+                v[k].w = v[k].w + u[k].w;
+                reinterpret_cast<float4 *>(xr)[lane + 64 * k] = v[k];
+            }
+            ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+        }
+        const float scale = 1.0f / sqrtf(wave_sum_dpp(ss) / (float)dim + eps);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float4 o;
+            o.x = v[k].x * (scale * bf16_lo(g[k].x));
+            o.y = v[k].y * (scale * bf16_hi(g[k].x));
+            o.z = v[k].z * (scale * bf16_lo(g[k].y));
+            o.w = v[k].w * (scale * bf16_hi(g[k].y));
+            reinterpret_cast<float4 *>(outr)[lane + 64 * k] = o;
+        }
+        return;
+    }
     for (size_t i = lane; i < dim; i += 64) {
         float v = xr[i];
         if (yr) {
@@ -104,7 +141,18 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x,
 hipError_t launch_add_rmsnorm(hipStream_t s, float *x, const float *y, float *xb, size_t rows, const uint16_t *w,
                               size_t dim, float eps) {
     if (rows == 0) return hipSuccess;
-    add_rmsnorm_kernel<<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s>>>(x, y, xb, rows, w, dim, eps);
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    // Row views as float4 need 16-byte alignment; the device's buffers are.
+    const bool vec = dim % 256 == 0 && ((uintptr_t)x | (uintptr_t)xb | (uintptr_t)y | (uintptr_t)w) % 16 == 0;
+    switch (vec ? dim / 256 : 0) {
+    case 1: add_rmsnorm_kernel<1><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
+    case 2: add_rmsnorm_kernel<2><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
+    case 4: add_rmsnorm_kernel<4><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
+    case 8: add_rmsnorm_kernel<8><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
+    case 10: add_rmsnorm_kernel<10><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
+    case 16: add_rmsnorm_kernel<16><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
+    default: add_rmsnorm_kernel<0><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
+    }
     return hipGetLastError();
 }
 
