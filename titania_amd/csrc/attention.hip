@@ -20,6 +20,7 @@ namespace th {
 constexpr int kAttnMaxGroup = 8;   // query heads per KV head
 constexpr int kAttnSub = 256;      // positions scored per sub-chunk
 constexpr size_t kAttnTileMin = 8; // tokens from which a launch uses the query-tiled kernel
+constexpr size_t kMKTiles = 32;    // positions per key tile of that kernel
 
 template <typename KV>
 __device__ __forceinline__ void load8(const KV *p, float f[8]);
@@ -237,7 +238,13 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__
     }
 }
 
-int attention_splits(size_t n, size_t n_kv_heads, size_t max_len) {
+int attention_splits(size_t n, size_t n_kv_heads, size_t max_len, size_t head_dim) {
+    // Several tokens on the matrix cores: split a query tile's keys so that
+    // each split walks at least 4 key tiles, at most 8 splits.
+    if (head_dim == 128 && n >= kAttnTileMin) {
+        const size_t tiles = (max_len + kMKTiles - 1) / kMKTiles;
+        return (int)std::min<size_t>(std::max<size_t>(tiles / 4, 1), 8);
+    }
     // One split while a block's share is short; otherwise about two blocks per
     // CU, each split covering at least 64 positions.
     if (max_len <= 512) return 1;
@@ -398,7 +405,7 @@ __global__ __launch_bounds__(256) void attn_tile_kernel(AttnKernelArgs a, int n)
 // its 16-lane rows, passes P through LDS into the A-operand layout and adds
 // P V into 16 x 128 f32 accumulators. Layout of 16x16x4 (checked on the GPU):
 // lane l holds A[l%16][l/16] and B[l/16][l%16], and D[4(l/16)+e][l%16].
-constexpr int kMQT = 64, kMKT = 32;
+constexpr int kMQT = 64, kMKT = (int)kMKTiles;
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float row_max16(float v) {
@@ -433,6 +440,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
     const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
     const long long last = pos + t0 + nq - 1;                       // the block's last query position
     const long long wlast = pos + t0 + wave * 16 + 15;              // this wave's last query position
+    // Key split z of a.nsplit: key tiles [kt0, kt1) of the block's range.
+    const long long ntiles = last / kMKT + 1, z = blockIdx.z;
+    const long long kt0 = z * ntiles / a.nsplit, kt1 = (z + 1) * ntiles / a.nsplit;
     floatx4 o[HD / 16];
     float m[4], l[4];
 #pragma unroll
@@ -456,8 +466,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
             }
         }
     };
-    fetch(0);
-    for (long long c0 = 0; c0 <= last; c0 += kMKT) {
+    const long long cend = kt1 * kMKT;  // positions [kt0 kMKT, cend) of this split
+    if (kt0 < kt1) fetch(kt0 * kMKT);
+    for (long long c0 = kt0 * kMKT; c0 < cend; c0 += kMKT) {
         __syncthreads();  // the previous tile is consumed
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
@@ -466,7 +477,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
             *reinterpret_cast<float4 *>(vs + row * VS + c4 * 4) = vr4[u];
         }
         __syncthreads();
-        if (c0 + kMKT <= last) fetch(c0 + kMKT);
+        if (c0 + kMKT < cend) fetch(c0 + kMKT);
         if (c0 > wlast) continue;  // every query of this wave precedes the tile
         // S for keys c0 + [0, 16) and c0 + [16, 32).
         floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -515,10 +526,23 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int qi = wave * 16 + 4 * lk + r;
-        if (qi < nq) {
-            float *op = a.out + ((long long)(t0 + qi) * a.n_heads + h) * HD + li;
+        if (qi >= nq) continue;
+        const long long th = (long long)(t0 + qi) * a.n_heads + h;
+        if (a.nsplit == 1) {
+            float *op = a.out + th * HD + li;
 #pragma unroll
             for (int d = 0; d < HD / 16; ++d) op[d * 16] = o[d][r] / l[r];
+        } else {
+            // Unnormalised sum, max and denominator for launch_attn_combine
+            // (a split with no key of this query leaves m = -inf).
+            const long long slot = th * a.nsplit + z;
+            float *op = a.part_acc + slot * HD + li;
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d) op[d * 16] = o[d][r];
+            if (li == 0) {
+                a.part_ml[slot * 2] = m[r];
+                a.part_ml[slot * 2 + 1] = l[r];
+            }
         }
     }
 }
@@ -538,12 +562,14 @@ static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim) {
     if (n == 0) return hipSuccess;
     if (head_dim == 128 && n >= kAttnTileMin) {
-        dim3 grid((unsigned)((n + kMQT - 1) / kMQT), (unsigned)k.n_heads);
+        dim3 grid((unsigned)((n + kMQT - 1) / kMQT), (unsigned)k.n_heads, (unsigned)k.nsplit);
         if (k.kv_bf16)
             attn_mfma_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
         else
             attn_mfma_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
-        return hipGetLastError();
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || k.nsplit == 1) return e;
+        return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128);
     }
     switch (head_dim) {
     case 64: return attn_launch<64>(s, k, n);

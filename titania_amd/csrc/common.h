@@ -116,8 +116,9 @@ struct AttnKernelArgs {
     float *part_acc;  // [n][n_heads][nsplit][head_dim] when nsplit > 1
     float *part_ml;   // [n][n_heads][nsplit][2]
 };
-// Splits of the sequence for n tokens whose contexts reach at most max_len.
-int attention_splits(size_t n, size_t n_kv_heads, size_t max_len);
+// Splits of the sequence for n tokens (of head_dim) whose contexts reach at
+// most max_len.
+int attention_splits(size_t n, size_t n_kv_heads, size_t max_len, size_t head_dim);
 // Scratch floats the partials of `nsplit` splits take (0 for one split).
 size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit);
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim);
