@@ -66,7 +66,7 @@ hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a);
 
 // The q/k/v GEMV (as launch_step_qkv) and single-split attention in one launch:
 // the GEMV blocks publish the rows as (value | epoch << 32) words, epoch =
-// st->epoch * 64 + layer + 1; one extra block per KV head stages its cached
+// st->epoch * 64 + layer + 1; one extra block per q head requests its cached
 // rows meanwhile, then attends from the words. For contexts one split covers.
 struct StepQkvAttnArgs {
     StepQkvArgs qkv;               // x_out as launch_step_qkv; qkv unused

@@ -381,16 +381,19 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
 }
 
 // The q/k/v rows of launch_step_qkv (two per wave) published as epoch words by
-// the first blocks, and after them one block per KV head that attends for its
-// group from those words. Blocks start in index order and the GEMV blocks
-// never wait, so the attention blocks' polls always end.
+// the first blocks, and after them one block per q head that attends from
+// those words. Blocks start in index order and the GEMV blocks never wait, so
+// the attention blocks' polls always end.
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
     constexpr int RPW = 2, RPB = RPW * kWaves;
     const int ngemv = (a.n_rows + RPB - 1) / RPB;
     const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
-        attend_regs<G, KV, true>(q.at, blockIdx.x - ngemv, 0, q.at.head_stride / 128, q.words, epoch, q.err);
+        // One block per q head: the heads of a KV group attend in parallel
+        // (each reads the group's cached rows), the group's first appends.
+        const int b = blockIdx.x - ngemv, g = b / G;
+        attend_regs<1, KV, true>(q.at, g, b, b % G == 0, 0, q.at.head_stride / 128, q.words, epoch, q.err);
         return;
     }
     extern __shared__ float xs[];
@@ -422,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
 
 template <int CPL, int G>
 hipError_t qkv_attn_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a) {
-    dim3 grid((unsigned)((a.n_rows + 7) / 8 + q.at.n_kv_heads));
+    dim3 grid((unsigned)((a.n_rows + 7) / 8 + q.at.n_heads));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
         qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(q, a);
@@ -445,7 +448,8 @@ hipError_t qkv_attn_g(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a
 template <int G, typename KV>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
 void step_attention_regs_kernel(StepAttnArgs a, long long chunk) {
-    attend_regs<G, KV, false>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, chunk, nullptr, 0, nullptr);
+    const int g = blockIdx.x / a.nsplit;
+    attend_regs<G, KV, false>(a, g, g * G, true, blockIdx.x % a.nsplit, chunk, nullptr, 0, nullptr);
 }
 
 template <int G>

@@ -175,9 +175,14 @@ template <> struct KvRegs<uint16_t> {
 // passes request their rows as soon as the previous pass has used the
 // registers. Reductions are DPP. The output goes to a.out with one split,
 // else (sum, max, denominator) partials for launch_attn_combine.
+//
+// The block's G q heads are qh0 .. qh0 + G - 1 of KV head g (qh0 = g G unless
+// a KV head's group is spread over several blocks, of which only the one with
+// `append` writes the new key and value).
 template <int G, typename KV, bool WORDS>
-__device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int split, long long chunk,
-                                            const unsigned long long *words, unsigned epoch, unsigned *err) {
+__device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh0, bool append, int split,
+                                            long long chunk, const unsigned long long *words, unsigned epoch,
+                                            unsigned *err) {
     using R = KvRegs<KV>;
     constexpr int HD = 128, HALF = HD / 2, ROWS = R::kRows;
     constexpr int NK = ROWS / 16;  // keys per lane in the score pass
@@ -225,7 +230,7 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int sp
             gb[hh] = bf16_to_f32(gain[lane + HALF]);
         }
         if (!WORDS && h <= G) {
-            const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
+            const float *x = h < G ? a.qkv + (size_t)(qh0 + h) * HD : a.qkv + qd + (size_t)g * HD;
             av[hh] = x[lane];
             bv[hh] = x[lane + HALF];
         }
@@ -242,7 +247,7 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int sp
                 const int h = wave + hh * kWaves;
                 if (h <= G) {
                     const unsigned long long *x =
-                        h < G ? words + (size_t)(g * G + h) * HD : words + qd + (size_t)g * HD;
+                        h < G ? words + (size_t)(qh0 + h) * HD : words + qd + (size_t)g * HD;
                     const unsigned long long wa =
                         __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     const unsigned long long wb =
@@ -380,7 +385,7 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int sp
     }
     // The split holding pos appends the new key and value (model.rs:119-120);
     // no block of this launch reads that position from the caches.
-    if (pos >= s0 && pos < s0 + chunk && tid < HD) {
+    if (append && pos >= s0 && pos < s0 + chunk && tid < HD) {
         store_kv(const_cast<KV *>(kc) + pos * HD + tid, hk[tid]);
         store_kv(const_cast<KV *>(vc) + pos * HD + tid, hv[tid]);
     }
@@ -396,7 +401,7 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int sp
     for (int idx = tid; idx < G * HD; idx += kThreads) {
         const int gg = idx / HD, d = idx % HD;
         const float sm = ((red[gg][0][d] + red[gg][1][d]) + red[gg][2][d]) + red[gg][3][d];
-        const long long h = (long long)g * G + gg;
+        const long long h = (long long)qh0 + gg;
         if (a.nsplit == 1) {
             a.out[h * HD + d] = sm / st_l[gg];
         } else {
