@@ -14,6 +14,7 @@
 // device memory, which lets one captured decode step replay at every position.
 #include "common.h"
 #include "device_util.h"
+#include "gemm.h"
 
 namespace th {
 
@@ -191,7 +192,8 @@ constexpr int kCombineThreads = 256, kMaxSplits = 256;
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__restrict__ out,
                                                                       const float *__restrict__ part_acc,
                                                                       const float *__restrict__ part_ml, int nsplit,
-                                                                      int hd) {
+                                                                      int hd, uint16_t *__restrict__ hi,
+                                                                      uint16_t *__restrict__ lo) {
     __shared__ float w[kMaxSplits];
     __shared__ float red[kCombineThreads / 64];
     __shared__ float acc_red[kCombineThreads];
@@ -232,7 +234,10 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__
         if (grp == 0 && d < hd) {
             float sum = 0.f;
             for (int gi = 0; gi < groups; ++gi) sum += acc_red[gi * hd + tid % hd];
-            out[th * hd + d] = sum / l;
+            if (hi)
+                split_bf16(sum / l, hi[th * hd + d], lo[th * hd + d]);
+            else
+                out[th * hd + d] = sum / l;
         }
         __syncthreads();
     }
@@ -261,9 +266,10 @@ size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit) 
 }
 
 hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,
-                               int nsplit, int hd) {
-    if (nsplit > kMaxSplits) return hipErrorInvalidValue;
-    attn_combine_kernel<<<dim3((unsigned)heads), dim3(kCombineThreads), 0, s>>>(out, part_acc, part_ml, nsplit, hd);
+                               int nsplit, int hd, uint16_t *hi, uint16_t *lo) {
+    if (nsplit > kMaxSplits || (!hi != !lo)) return hipErrorInvalidValue;
+    attn_combine_kernel<<<dim3((unsigned)heads), dim3(kCombineThreads), 0, s>>>(out, part_acc, part_ml, nsplit, hd,
+                                                                                hi, lo);
     return hipGetLastError();
 }
 
@@ -528,7 +534,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
         const int qi = wave * 16 + 4 * lk + r;
         if (qi >= nq) continue;
         const long long th = (long long)(t0 + qi) * a.n_heads + h;
-        if (a.nsplit == 1) {
+        if (a.nsplit == 1 && a.out_hi) {
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d)
+                split_bf16(o[d][r] / l[r], a.out_hi[th * HD + li + d * 16], a.out_lo[th * HD + li + d * 16]);
+        } else if (a.nsplit == 1) {
             float *op = a.out + th * HD + li;
 #pragma unroll
             for (int d = 0; d < HD / 16; ++d) op[d * 16] = o[d][r] / l[r];
@@ -555,8 +565,10 @@ static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
     else
         attn_split_kernel<HD, float><<<grid, 256, 0, s>>>(k);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || k.nsplit == 1) return e;
-    return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, HD);
+    if (e == hipSuccess && k.nsplit > 1)
+        e = launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, HD);
+    if (e != hipSuccess || !k.out_hi) return e;
+    return launch_gemm_split(s, k.out, n, (size_t)k.n_heads * HD, k.out_hi, k.out_lo);
 }
 
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim) {
@@ -569,7 +581,8 @@ hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, si
             attn_mfma_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || k.nsplit == 1) return e;
-        return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128);
+        return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128, k.out_hi,
+                                   k.out_lo);
     }
     switch (head_dim) {
     case 64: return attn_launch<64>(s, k, n);

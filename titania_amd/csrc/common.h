@@ -84,10 +84,19 @@ hipError_t launch_embed(hipStream_t s, float *out, const uint16_t *table, size_t
 hipError_t launch_copy(hipStream_t s, float *dst, const float *src, size_t len);
 hipError_t launch_add(hipStream_t s, float *x, const float *y, size_t len);
 hipError_t launch_silu_mul(hipStream_t s, float *gate, const float *up, size_t len);
+// silu(gate) * up as split_bf16 terms hi/lo (len a multiple of 4).
+hipError_t launch_silu_mul_split(hipStream_t s, const float *gate, const float *up, size_t len, uint16_t *hi,
+                                 uint16_t *lo);
 hipError_t launch_rmsnorm(hipStream_t s, float *x, size_t rows, const uint16_t *w, size_t dim, float eps);
 // xb = rmsnorm(x (+)= y): if y, x += y first; xb may equal x.
 hipError_t launch_add_rmsnorm(hipStream_t s, float *x, const float *y, float *xb, size_t rows,
                               const uint16_t *w, size_t dim, float eps);
+// The same with the residual summed from ny partials y[z * y_stride] (z in
+// order; ny = 0: none), the normalized rows to xb (f32) and/or to hi/lo as
+// split_bf16 terms (either may be null, not both).
+hipError_t launch_add_rmsnorm_parts(hipStream_t s, float *x, const float *y, int ny, size_t y_stride, float *xb,
+                                    uint16_t *hi, uint16_t *lo, size_t rows, const uint16_t *w, size_t dim,
+                                    float eps);
 hipError_t launch_rope(hipStream_t s, float *x, size_t n, const float *table, size_t pos, size_t n_heads,
                        size_t head_dim);
 // Two-pass argmax: partials need argmax_partials(n) u64 of scratch.
@@ -115,6 +124,9 @@ struct AttnKernelArgs {
     float scale;
     float *part_acc;  // [n][n_heads][nsplit][head_dim] when nsplit > 1
     float *part_ml;   // [n][n_heads][nsplit][2]
+    // When set, the output goes here as split_bf16 terms [n][n_heads * head_dim]
+    // (the o projection's GEMM input); `out` may then be scratch.
+    uint16_t *out_hi, *out_lo;
 };
 // Splits of the sequence for n tokens (of head_dim) whose contexts reach at
 // most max_len.
@@ -122,8 +134,9 @@ int attention_splits(size_t n, size_t n_kv_heads, size_t max_len, size_t head_di
 // Scratch floats the partials of `nsplit` splits take (0 for one split).
 size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit);
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim);
-// Merges attention partials of `heads` (token, head) pairs into out.
+// Merges attention partials of `heads` (token, head) pairs into out (f32) or,
+// when hi is set, into hi/lo as split_bf16 terms.
 hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,
-                               int nsplit, int hd);
+                               int nsplit, int hd, uint16_t *hi = nullptr, uint16_t *lo = nullptr);
 
 }  // namespace th

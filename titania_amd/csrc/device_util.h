@@ -29,6 +29,30 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// An f32 as two bf16 terms, x ~ hi + lo with hi = bf16(x), lo = bf16(x - hi)
+// (round to nearest even, the hardware conversion): 16 significant bits
+// together. The matrix-core GEMM takes its activations in this form.
+typedef __bf16 th_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float th_f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) {
+    const __bf16 h = (__bf16)x;
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, (__bf16)(x - (float)h));
+}
+
+__device__ __forceinline__ void split_bf16x4(const float4 &v, uint2 &hi, uint2 &lo) {
+    const th_bf16x2 h01 = __builtin_convertvector((th_f32x2){v.x, v.y}, th_bf16x2);
+    const th_bf16x2 h23 = __builtin_convertvector((th_f32x2){v.z, v.w}, th_bf16x2);
+    const uint32_t u01 = __builtin_bit_cast(uint32_t, h01), u23 = __builtin_bit_cast(uint32_t, h23);
+    const th_bf16x2 l01 = __builtin_convertvector(
+        (th_f32x2){v.x - __uint_as_float(u01 << 16), v.y - __uint_as_float(u01 & 0xffff0000u)}, th_bf16x2);
+    const th_bf16x2 l23 = __builtin_convertvector(
+        (th_f32x2){v.z - __uint_as_float(u23 << 16), v.w - __uint_as_float(u23 & 0xffff0000u)}, th_bf16x2);
+    hi = make_uint2(u01, u23);
+    lo = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -31,6 +31,19 @@ struct GemmOut {
 // second kernel sums in a fixed order).
 constexpr int kGemmMaxSplitK = 4;
 
+// split_bf16 of x [n][cols] into hi[n * cols], lo[n * cols].
+hipError_t launch_gemm_split(hipStream_t s, const float *x, size_t n, size_t cols, uint16_t *hi, uint16_t *lo);
+
+// Ways the GEMM of n tokens, `rows` output rows (all matrices) and `cols`
+// columns splits K for n_outs matrices (1: no split).
+int gemm_ksplit(size_t n, size_t rows, size_t cols, int n_outs);
+
+// The GEMM on split activations hi/lo [n][cols]: with ksplit > 1 (one
+// matrix) the partial products go to part[ksplit][n][rows] instead of the
+// output, to be summed by the consumer in split order.
+hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
+                          const GemmOut *outs, int n_outs, float *part, int ksplit);
+
 // Bytes of scratch launch_gemm_multi needs for n tokens of `cols` columns and
 // single-matrix outputs of up to `rows` rows (room for the split-K partials).
 size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows);

@@ -20,12 +20,12 @@
 // v; gate and up): their rows are concatenated.
 #include "gemm.h"
 
+#include "device_util.h"
+
 namespace th {
 namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
 constexpr int BM = 64, BN = 64, BK = 64;  // tokens, weight rows, columns per step
@@ -170,21 +170,10 @@ __global__ __launch_bounds__(NTHR, 2) void gemm_kernel(Segs sg, const uint16_t *
             }
 }
 
-// hi = bf16(x), lo = bf16(x - hi) for 4 elements a thread (round to nearest even).
+// split_bf16 of 4 elements a thread.
 __global__ void split_kernel(const float4 *__restrict__ x, uint2 *__restrict__ hi, uint2 *__restrict__ lo, size_t n4) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        const float4 v = x[i];
-        const bf16x2 h01 = __builtin_convertvector((f32x2){v.x, v.y}, bf16x2);
-        const bf16x2 h23 = __builtin_convertvector((f32x2){v.z, v.w}, bf16x2);
-        const uint32_t u01 = __builtin_bit_cast(uint32_t, h01), u23 = __builtin_bit_cast(uint32_t, h23);
-        const bf16x2 l01 = __builtin_convertvector(
-            (f32x2){v.x - __uint_as_float(u01 << 16), v.y - __uint_as_float(u01 & 0xffff0000u)}, bf16x2);
-        const bf16x2 l23 = __builtin_convertvector(
-            (f32x2){v.z - __uint_as_float(u23 << 16), v.w - __uint_as_float(u23 & 0xffff0000u)}, bf16x2);
-        hi[i] = make_uint2(u01, u23);
-        lo[i] = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
-    }
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) split_bf16x4(x[i], hi[i], lo[i]);
 }
 
 // out[i] = sum over z < ksplit of part[z * m + i] (z in order), 4 a thread.
@@ -214,10 +203,32 @@ size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows) {
     return n * cols * 2 * sizeof(uint16_t) + (size_t)kGemmMaxSplitK * n * rows * sizeof(float);
 }
 
-hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t cols, const GemmOut *outs, int n_outs,
-                             void *scratch, size_t scratch_bytes) {
+hipError_t launch_gemm_split(hipStream_t s, const float *x, size_t n, size_t cols, uint16_t *hi, uint16_t *lo) {
     if (n == 0) return hipSuccess;
-    if (n_outs < 1 || n_outs > 3 || !scratch || (n + BM - 1) / BM > 65535 || n > ((size_t)1 << 24))
+    if (cols % 4 || !x || !hi || !lo) return hipErrorInvalidValue;
+    const size_t n4 = n * cols / 4;
+    const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
+    split_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(hi),
+                                        reinterpret_cast<uint2 *>(lo), n4);
+    return hipGetLastError();
+}
+
+// A single matrix with few output tiles (o, down: 1024 rows) splits K so that
+// the launch still fills the chip, keeping at least 4 K steps per split.
+int gemm_ksplit(size_t n, size_t rows, size_t cols, int n_outs) {
+    if (n_outs != 1) return 1;
+    const size_t tiles = (rows / BN) * ((n + BM - 1) / BM), nk = cols / BK;
+    int ksplit = 1;
+    while (ksplit < kGemmMaxSplitK && tiles * ksplit < 512 && (size_t)ksplit * 2 * 4 <= nk) ksplit *= 2;
+    return ksplit;
+}
+
+hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
+                          const GemmOut *outs, int n_outs, float *part, int ksplit) {
+    if (n == 0) return hipSuccess;
+    if (n_outs < 1 || n_outs > 3 || !hi || !lo || (n + BM - 1) / BM > 65535 || n > ((size_t)1 << 24) ||
+        ksplit < 1 || ksplit > kGemmMaxSplitK || (ksplit > 1 && (n_outs != 1 || !part)) ||
+        (size_t)ksplit > cols / BK)
         return hipErrorInvalidValue;
     Segs sg{};
     size_t total = 0;
@@ -230,26 +241,25 @@ hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t col
     }
     sg.n = n_outs;
     if (total / BN > 65535) return hipErrorInvalidValue;
-    uint16_t *hi = static_cast<uint16_t *>(scratch), *lo = hi + n * cols;
-    const size_t n4 = n * cols / 4;
-    const unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
-    split_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(hi),
-                                        reinterpret_cast<uint2 *>(lo), n4);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    // A single matrix with few output tiles (o, down: 1024 rows) splits K so
-    // that the launch still fills the chip, when the scratch has room for
-    // the partial tiles.
-    const size_t tiles = (total / BN) * ((n + BM - 1) / BM), nk = cols / BK;
-    int ksplit = 1;
-    float *part = reinterpret_cast<float *>(hi + 2 * n * cols);
-    if (n_outs == 1)
-        while (ksplit < kGemmMaxSplitK && tiles * ksplit < 512 && (size_t)ksplit * 2 * 4 <= nk &&
-               n * cols * 4 + (size_t)ksplit * 2 * n * total * sizeof(float) <= scratch_bytes)
-            ksplit *= 2;
     dim3 grid((unsigned)(total / BN), (unsigned)((n + BM - 1) / BM), (unsigned)ksplit);
     gemm_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
-    e = hipGetLastError();
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t cols, const GemmOut *outs, int n_outs,
+                             void *scratch, size_t scratch_bytes) {
+    if (n == 0) return hipSuccess;
+    if (n_outs < 1 || n_outs > 3 || !scratch || n * cols * 2 * sizeof(uint16_t) > scratch_bytes)
+        return hipErrorInvalidValue;
+    size_t total = 0;
+    for (int i = 0; i < n_outs; ++i) total += outs[i].rows;
+    uint16_t *hi = static_cast<uint16_t *>(scratch), *lo = hi + n * cols;
+    float *part = reinterpret_cast<float *>(hi + 2 * n * cols);
+    // The partial tiles take the rest of the scratch; fewer splits when it is short.
+    int ksplit = gemm_ksplit(n, total, cols, n_outs);
+    while (ksplit > 1 && n * cols * 4 + (size_t)ksplit * n * total * sizeof(float) > scratch_bytes) ksplit /= 2;
+    hipError_t e = launch_gemm_split(s, x, n, cols, hi, lo);
+    if (e == hipSuccess) e = launch_gemm_hl(s, hi, lo, n, cols, outs, n_outs, part, ksplit);
     if (e != hipSuccess || ksplit == 1) return e;
     const size_t m4 = n * total / 4;
     splitk_sum_kernel<<<(unsigned)std::min<size_t>((m4 + 255) / 256, 4096), 256, 0, s>>>(

@@ -477,18 +477,49 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
     // split once per input into fsplit).
     auto use_gemm = [&](size_t cols) { return n >= th::kGemmMinTokens && s->fsplit && cols <= s->fsplit_cols; };
 
+    // When every projection goes through the MFMA GEMM, the kernels that
+    // produce a GEMM input (the norms, attention, silu_mul) write it as bf16
+    // hi/lo terms directly, and the residual add after the o and down GEMMs
+    // sums their split-K partials itself.
+    const bool hl = use_gemm(std::max(std::max(H, qd), I)) && th::gemm_supported(qd, H) &&
+                    th::gemm_supported(nkv * hd, H) && th::gemm_supported(H, qd) && th::gemm_supported(I, H) &&
+                    th::gemm_supported(H, I);
+    uint16_t *hi = static_cast<uint16_t *>(s->fsplit), *lo = hi ? hi + s->fb * s->fsplit_cols : nullptr;
+    float *part = hi ? reinterpret_cast<float *>(hi + 2 * s->fb * s->fsplit_cols) : nullptr;
+    const int ks_o = th::gemm_ksplit(n, H, qd, 1), ks_down = th::gemm_ksplit(n, H, I, 1);
+    // The residual still to be added to fx: ny partials of stride y_stride.
+    const float *res = nullptr;
+    int nres = 0;
+    size_t res_stride = 0;
+    auto single_gemm = [&](const uint16_t *w, size_t cols, int ks) -> int {
+        const th::GemmOut o{w, H, s->fy};
+        TH_HIP(th::launch_gemm_hl(st, hi, lo, n, cols, &o, 1, part, ks));
+        res = ks > 1 ? part : s->fy;
+        nres = ks;
+        res_stride = n * H;
+        return TH_OK;
+    };
+
     TH_HIP(th::launch_embed(st, s->fx, m->embed->ptr, H, tokens, n));
     for (size_t i = 0; i < m->layers.size(); ++i) {
         const Layer &L = m->layers[i];
         // Residual add of the previous layer's MLP output, then the attention norm.
-        TH_HIP(th::launch_add_rmsnorm(st, s->fx, i ? s->fy : nullptr, s->fxb, n, L.attn_norm->ptr, H, eps));
-        if (use_gemm(H) && th::gemm_supported(qd, H) && th::gemm_supported(nkv * hd, H)) {
+        if (hl) {
+            TH_HIP(th::launch_add_rmsnorm_parts(st, s->fx, res, nres, res_stride, nullptr, hi, lo, n,
+                                                L.attn_norm->ptr, H, eps));
             const th::GemmOut o[3] = {{L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
-            TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 3, s->fsplit, s->fsplit_bytes));
+            TH_HIP(th::launch_gemm_hl(st, hi, lo, n, H, o, 3, nullptr, 1));
         } else {
-            TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
-            TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
-            TH_HIP(th::launch_matmul(st, s->fv, L.v->ptr, nkv * hd, H, s->fxb, n));
+            TH_HIP(th::launch_add_rmsnorm(st, s->fx, i ? s->fy : nullptr, s->fxb, n, L.attn_norm->ptr, H, eps));
+            if (use_gemm(H) && th::gemm_supported(qd, H) && th::gemm_supported(nkv * hd, H)) {
+                const th::GemmOut o[3] = {
+                    {L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
+                TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 3, s->fsplit, s->fsplit_bytes));
+            } else {
+                TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
+                TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
+                TH_HIP(th::launch_matmul(st, s->fv, L.v->ptr, nkv * hd, H, s->fxb, n));
+            }
         }
         th::QkvPostArgs qa{};
         qa.q = s->fq;
@@ -528,8 +559,22 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         aa.scale = 1.0f / sqrtf((float)hd);
         aa.part_acc = s->attn_part;
         aa.part_ml = s->attn_part ? s->attn_part + n * nh * (size_t)nsplit * hd : nullptr;
+        if (hl) {
+            aa.out_hi = hi;
+            aa.out_lo = lo;
+        }
         TH_HIP(th::launch_attention(st, aa, n, hd));
 
+        if (hl) {
+            TRY(single_gemm(L.o->ptr, qd, ks_o));
+            TH_HIP(th::launch_add_rmsnorm_parts(st, s->fx, res, nres, res_stride, nullptr, hi, lo, n,
+                                                L.mlp_norm->ptr, H, eps));
+            const th::GemmOut o[2] = {{L.gate->ptr, I, s->fgate}, {L.up->ptr, I, s->fup}};
+            TH_HIP(th::launch_gemm_hl(st, hi, lo, n, H, o, 2, nullptr, 1));
+            TH_HIP(th::launch_silu_mul_split(st, s->fgate, s->fup, n * I, hi, lo));
+            TRY(single_gemm(L.down->ptr, I, ks_down));
+            continue;
+        }
         if (use_gemm(qd) && th::gemm_supported(H, qd)) {
             const th::GemmOut o{L.o->ptr, H, s->fy};
             TH_HIP(th::launch_gemm_multi(st, s->fatt, n, qd, &o, 1, s->fsplit, s->fsplit_bytes));
@@ -551,10 +596,14 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         } else {
             TH_HIP(th::launch_matmul(st, s->fy, L.down->ptr, H, I, s->fgate, n));
         }
+        res = s->fy;
+        nres = 1;
+        res_stride = 0;
     }
     // Only the last token's logits are wanted (model.rs:143-147).
     float *xl = s->fx + (n - 1) * H;
-    TH_HIP(th::launch_add_rmsnorm(st, xl, s->fy + (n - 1) * H, s->fxb, 1, m->norm->ptr, H, eps));
+    TH_HIP(th::launch_add_rmsnorm_parts(st, xl, res ? res + (n - 1) * H : nullptr, nres, res_stride, s->fxb, nullptr,
+                                        nullptr, 1, m->norm->ptr, H, eps));
     TH_HIP(th::launch_matmul(st, s->logits->ptr, m->out_proj()->ptr, (size_t)c.vocab_size, H, s->fxb, 1));
     return TH_OK;
 }

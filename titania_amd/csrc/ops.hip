@@ -75,22 +75,60 @@ hipError_t launch_silu_mul(hipStream_t s, float *gate, const float *up, size_t l
     return hipGetLastError();
 }
 
+// The same product as split_bf16 terms (the down projection's GEMM input), 4
+// elements a thread.
+__global__ void silu_mul_split_kernel(const float4 *__restrict__ g, const float4 *__restrict__ u,
+                                      uint2 *__restrict__ hi, uint2 *__restrict__ lo, size_t len4) {
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len4; i += stride) {
+        const float4 a = g[i], b = u[i];
+        split_bf16x4(make_float4(silu(a.x) * b.x, silu(a.y) * b.y, silu(a.z) * b.z, silu(a.w) * b.w), hi[i], lo[i]);
+    }
+}
+
+hipError_t launch_silu_mul_split(hipStream_t s, const float *gate, const float *up, size_t len, uint16_t *hi,
+                                 uint16_t *lo) {
+    if (len == 0) return hipSuccess;
+    if (len % 4 || ((uintptr_t)gate | (uintptr_t)up) % 16 || ((uintptr_t)hi | (uintptr_t)lo) % 8)
+        return hipErrorInvalidValue;
+    const size_t len4 = len / 4;
+    unsigned blocks = (unsigned)std::min<size_t>((len4 + 255) / 256, 4096);
+    silu_mul_split_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<const float4 *>(gate),
+                                                 reinterpret_cast<const float4 *>(up), reinterpret_cast<uint2 *>(hi),
+                                                 reinterpret_cast<uint2 *>(lo), len4);
+    return hipGetLastError();
+}
+
 // model/cpu.rs:85-94, optionally preceded by the residual add of
-// model/model.rs:132/141: one wave per dim-long row. If y is given, x += y is
-// stored back into x; the normalized row goes to xb (which may be x).
+// model/model.rs:132/141: one wave per dim-long row. The residual, if any, is
+// the sum of ny partial products y[z * y_stride] taken in z order (a GEMM's
+// split-K partials, or ny = 1 for a plain vector); x += residual is stored
+// back into x. The normalized row goes to xb (f32, which may be x) and/or, as
+// split_bf16 terms, to hi/lo for the next matrix-core GEMM.
 // NV > 0: dim == 256 * NV, each lane holds NV float4 of the row and issues all
 // their loads before using any (one memory round trip per row); NV == 0: any
 // dim, element by element.
+struct NormArgs {
+    float *x;
+    const float *y;
+    int ny;
+    size_t y_stride;
+    float *xb;
+    uint16_t *hi, *lo;
+    size_t rows;
+    const uint16_t *w;
+    size_t dim;
+    float eps;
+};
+
 template <int NV>
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ y,
-                                                          float *xb, size_t rows, const uint16_t *__restrict__ w,
-                                                          size_t dim, float eps) {
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
     const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    float *xr = x + row * dim;
-    float *outr = xb + row * dim;
-    const float *yr = y ? y + row * dim : nullptr;
+    if (row >= a.rows) return;
+    const size_t dim = a.dim;
+    float *xr = a.x + row * dim;
+    const float *yr = a.ny ? a.y + row * dim : nullptr;
     float ss = 0.f;
     if (NV > 0) {
         float4 v[NV > 0 ? NV : 1], u[NV > 0 ? NV : 1];
@@ -100,7 +138,20 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x,
             const int i = lane + 64 * k;
             v[k] = reinterpret_cast<const float4 *>(xr)[i];
             if (yr) u[k] = reinterpret_cast<const float4 *>(yr)[i];
-            g[k] = reinterpret_cast<const uint2 *>(w)[i];
+            g[k] = reinterpret_cast<const uint2 *>(a.w)[i];
+        }
+        for (int z = 1; z < a.ny; ++z) {
+            const float4 *yz = reinterpret_cast<const float4 *>(yr + (size_t)z * a.y_stride);
+            float4 t[NV > 0 ? NV : 1];
+#pragma unroll
+            for (int k = 0; k < NV; ++k) t[k] = yz[lane + 64 * k];
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                u[k].x += t[k].x;
+                u[k].y += t[k].y;
+                u[k].z += t[k].z;
+                u[k].w += t[k].w;
+            }
         }
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
@@ -113,7 +164,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x,
             }
             ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
         }
-        const float scale = 1.0f / sqrtf(wave_sum_dpp(ss) / (float)dim + eps);
+        const float scale = 1.0f / sqrtf(wave_sum_dpp(ss) / (float)dim + a.eps);
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             float4 o;
@@ -121,39 +172,58 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ x,
             o.y = v[k].y * (scale * bf16_hi(g[k].x));
             o.z = v[k].z * (scale * bf16_lo(g[k].y));
             o.w = v[k].w * (scale * bf16_hi(g[k].y));
-            reinterpret_cast<float4 *>(outr)[lane + 64 * k] = o;
+            const size_t i = row * dim / 4 + lane + 64 * k;
+            if (a.xb) reinterpret_cast<float4 *>(a.xb)[i] = o;
+            if (a.hi) split_bf16x4(o, reinterpret_cast<uint2 *>(a.hi)[i], reinterpret_cast<uint2 *>(a.lo)[i]);
         }
         return;
     }
     for (size_t i = lane; i < dim; i += 64) {
         float v = xr[i];
         if (yr) {
-            v = v + yr[i];
+            float u = yr[i];
+            for (int z = 1; z < a.ny; ++z) u += yr[(size_t)z * a.y_stride + i];
+            v = v + u;
             xr[i] = v;
         }
         ss += v * v;
     }
     ss = wave_sum(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
-    for (size_t i = lane; i < dim; i += 64) outr[i] = xr[i] * (scale * bf16_to_f32(w[i]));
+    const float scale = 1.0f / sqrtf(ss / (float)dim + a.eps);
+    for (size_t i = lane; i < dim; i += 64) {
+        const float o = xr[i] * (scale * bf16_to_f32(a.w[i]));
+        if (a.xb) a.xb[row * dim + i] = o;
+        if (a.hi) split_bf16(o, a.hi[row * dim + i], a.lo[row * dim + i]);
+    }
+}
+
+hipError_t launch_add_rmsnorm_parts(hipStream_t s, float *x, const float *y, int ny, size_t y_stride, float *xb,
+                                    uint16_t *hi, uint16_t *lo, size_t rows, const uint16_t *w, size_t dim,
+                                    float eps) {
+    if (rows == 0) return hipSuccess;
+    if (ny < 0 || (ny > 0 && !y) || (!xb && !hi) || (!hi != !lo)) return hipErrorInvalidValue;
+    const NormArgs a{x, ny ? y : nullptr, ny, y_stride, xb, hi, lo, rows, w, dim, eps};
+    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    // Row views as float4 (and hi/lo as uint2) need 16-byte (8-byte) alignment;
+    // the device's buffers have it.
+    const bool vec = dim % 256 == 0 && y_stride % 4 == 0 &&
+                     ((uintptr_t)x | (uintptr_t)xb | (uintptr_t)a.y | (uintptr_t)w) % 16 == 0 &&
+                     ((uintptr_t)hi | (uintptr_t)lo) % 8 == 0;
+    switch (vec ? dim / 256 : 0) {
+    case 1: add_rmsnorm_kernel<1><<<grid, block, 0, s>>>(a); break;
+    case 2: add_rmsnorm_kernel<2><<<grid, block, 0, s>>>(a); break;
+    case 4: add_rmsnorm_kernel<4><<<grid, block, 0, s>>>(a); break;
+    case 8: add_rmsnorm_kernel<8><<<grid, block, 0, s>>>(a); break;
+    case 10: add_rmsnorm_kernel<10><<<grid, block, 0, s>>>(a); break;
+    case 16: add_rmsnorm_kernel<16><<<grid, block, 0, s>>>(a); break;
+    default: add_rmsnorm_kernel<0><<<grid, block, 0, s>>>(a); break;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_add_rmsnorm(hipStream_t s, float *x, const float *y, float *xb, size_t rows, const uint16_t *w,
                               size_t dim, float eps) {
-    if (rows == 0) return hipSuccess;
-    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    // Row views as float4 need 16-byte alignment; the device's buffers are.
-    const bool vec = dim % 256 == 0 && ((uintptr_t)x | (uintptr_t)xb | (uintptr_t)y | (uintptr_t)w) % 16 == 0;
-    switch (vec ? dim / 256 : 0) {
-    case 1: add_rmsnorm_kernel<1><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
-    case 2: add_rmsnorm_kernel<2><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
-    case 4: add_rmsnorm_kernel<4><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
-    case 8: add_rmsnorm_kernel<8><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
-    case 10: add_rmsnorm_kernel<10><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
-    case 16: add_rmsnorm_kernel<16><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
-    default: add_rmsnorm_kernel<0><<<grid, block, 0, s>>>(x, y, xb, rows, w, dim, eps); break;
-    }
-    return hipGetLastError();
+    return launch_add_rmsnorm_parts(s, x, y, y ? 1 : 0, 0, xb, nullptr, nullptr, rows, w, dim, eps);
 }
 
 hipError_t launch_rmsnorm(hipStream_t s, float *x, size_t rows, const uint16_t *w, size_t dim, float eps) {
