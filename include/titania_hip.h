@@ -194,6 +194,21 @@ TH_API int th_decode(th_model *model, th_state *state, size_t pos, size_t steps,
 TH_API int th_decode_sample(th_model *model, th_state *state, size_t pos, size_t steps, float temperature,
                             size_t top_k, float top_p, uint64_t *rng, uint32_t *out_tokens);
 
+/* The reply loop of model/chat.rs:147-178 (`Chat::generate` once its prompt
+ * has been fed), kept on the device: from the logits the last th_forward left,
+ * pick (temperature 0) or draw (as th_decode_sample) a token; if it is one of
+ * the n_stop (1..8) stop tokens, stop; else feed it at the next position (pos,
+ * pos + 1, ...) and go on, for at most max_tokens tokens. Writes the tokens to
+ * out_tokens (room for max_tokens) and their count to *n_out. When the last is
+ * a stop token it was not fed, and the conversation has grown by *n_out - 1
+ * tokens; otherwise by *n_out. The host looks for a stop every 8 steps (the
+ * steps after it repeat the last fed token and change nothing). rng may be
+ * NULL at temperature 0. No counterpart in the trait: the reference's Chat
+ * drives Model::forward and Sampler::sample one token at a time. */
+TH_API int th_generate(th_model *model, th_state *state, size_t pos, size_t max_tokens, const uint32_t *stop,
+                       size_t n_stop, float temperature, size_t top_k, float top_p, uint64_t *rng,
+                       uint32_t *out_tokens, size_t *n_out);
+
 /* Phase trace of the last th_decode on the persistent path, when the state was
  * created with TITANIA_TRACE=<steps> in the environment: word 0 is the kernel's
  * start tick, then for each traced step and each phase (5 per layer: attention

@@ -266,6 +266,44 @@ class RefModel:
         return toks
 
 
+class RefChat:
+    """model/chat.rs:24-196 at the token level: the conversation stays in the
+    caches and each call runs the model over its new tokens only (`feed`,
+    chat.rs:189-196); a reply samples, stops at a stop token without feeding
+    it, and otherwise feeds each token (chat.rs:132-187). `sampler` None is
+    the temperature-0 pick (sampler.rs:27-33). max_tokens bounds a reply (the
+    reference's loop has no bound)."""
+
+    def __init__(self, model: RefModel, max_len: int, sampler: Sampler | None = None):
+        self.model = model
+        self.state = model.state(max_len)
+        self.sampler = sampler
+        self.len = 0
+        self.logits = None
+
+    def feed(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        if self.len + t.size > self.state.max_len:
+            raise ValueError("the conversation no longer fits in the context window")
+        if t.size:
+            self.logits = self.model.forward(self.state, t, self.len)
+        self.len += t.size
+        return self.logits
+
+    def generate(self, prompt, stop, end, max_tokens: int) -> np.ndarray:
+        stops = {int(x) for x in np.asarray(stop).reshape(-1)}
+        logits = self.feed(prompt)
+        out = []
+        while len(out) < max_tokens:
+            tok = self.sampler.sample(logits) if self.sampler is not None else argmax(logits)
+            out.append(tok)
+            if tok in stops:
+                break
+            logits = self.feed([tok])
+        self.feed(end)
+        return np.array(out, dtype=np.uint32)
+
+
 class RefState:
     def __init__(self, model: RefModel, max_len: int):
         self.model = model

@@ -243,6 +243,48 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__
     }
 }
 
+// The same merge with one wave per (token, head), for many pairs of few
+// splits (prefill): lane s holds split s's statistics, each lane HD / 64
+// dimensions of the accumulators, walked over the splits in order.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_wave_kernel(float *__restrict__ out,
+                                                                const float *__restrict__ part_acc,
+                                                                const float *__restrict__ part_ml, int nsplit,
+                                                                long long heads, uint16_t *__restrict__ hi,
+                                                                uint16_t *__restrict__ lo) {
+    constexpr int D = HD / 64;
+    const long long th = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (th >= heads) return;
+    float ms = -INFINITY, ls = 0.f;
+    if (lane < nsplit) {
+        const float2 v = reinterpret_cast<const float2 *>(part_ml + th * nsplit * 2)[lane];
+        ms = v.x;
+        ls = v.y;
+    }
+    const float m = wave_max_dpp(ms);
+    const float ws = ms != -INFINITY ? expf(ms - m) : 0.f;
+    const float l = wave_sum_dpp(ls * ws);
+    const float *pa = part_acc + th * nsplit * HD + lane * D;
+    float acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) acc[d] = 0.f;
+#pragma unroll 4
+    for (int sp = 0; sp < nsplit; ++sp) {
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ws), sp));
+#pragma unroll
+        for (int d = 0; d < D; ++d) acc[d] += pa[(size_t)sp * HD + d] * w;
+    }
+    const long long o = th * HD + lane * D;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (hi)
+            split_bf16(acc[d] / l, hi[o + d], lo[o + d]);
+        else
+            out[o + d] = acc[d] / l;
+    }
+}
+
 int attention_splits(size_t n, size_t n_kv_heads, size_t max_len, size_t head_dim) {
     // Several tokens on the matrix cores: split a query tile's keys so that
     // each split walks at least 4 key tiles, at most 8 splits.
@@ -268,6 +310,15 @@ size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit) 
 hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,
                                int nsplit, int hd, uint16_t *hi, uint16_t *lo) {
     if (nsplit > kMaxSplits || (!hi != !lo)) return hipErrorInvalidValue;
+    if (heads >= 1024 && nsplit <= 64 && (hd == 64 || hd == 128 || hd == 256)) {
+        const dim3 grid((unsigned)((heads + 3) / 4));
+        switch (hd) {
+        case 64: attn_combine_wave_kernel<64><<<grid, 256, 0, s>>>(out, part_acc, part_ml, nsplit, heads, hi, lo); break;
+        case 128: attn_combine_wave_kernel<128><<<grid, 256, 0, s>>>(out, part_acc, part_ml, nsplit, heads, hi, lo); break;
+        default: attn_combine_wave_kernel<256><<<grid, 256, 0, s>>>(out, part_acc, part_ml, nsplit, heads, hi, lo); break;
+        }
+        return hipGetLastError();
+    }
     attn_combine_kernel<<<dim3((unsigned)heads), dim3(kCombineThreads), 0, s>>>(out, part_acc, part_ml, nsplit, hd,
                                                                                 hi, lo);
     return hipGetLastError();

@@ -31,6 +31,8 @@ hipError_t launch_qk_norm_rope_append(hipStream_t s, const QkvPostArgs &a);
 
 // State of the on-device greedy loop, in device memory so that one captured
 // decode step can replay at every position.
+constexpr int kStepMaxStops = 8;  // stop tokens a decode call may end at
+
 struct StepState {
     long long pos;         // position of the token to feed next
     long long step;        // tokens fed so far in this decode call
@@ -38,6 +40,9 @@ struct StepState {
     uint32_t epoch;        // decode steps ever advanced on this state (tags exchange words)
     uint32_t *tokens_out;  // picks, indexed by step
     float *logits_out;     // logits after each fed token, or null
+    int n_stop;            // entries of stop[] in use
+    int stopped;           // index in tokens_out of the stop token picked, plus one (0: none yet)
+    uint32_t stop[kStepMaxStops];
 };
 
 // The embedding row the pick writes for the next step (model/cpu.rs:38-47),
@@ -48,16 +53,32 @@ struct PickEmbed {
     float *out = nullptr;
 };
 
-// Records the step's pick: with `advance` (a token has been fed) the position,
-// step and epoch move on first; then st->token and st->tokens_out[st->step].
-__device__ __forceinline__ void step_record(StepState *st, int advance, uint32_t tok) {
+// Records the step's pick and returns the token the next step feeds. With
+// `advance` (a token has been fed) the position, step and epoch move on
+// first; then st->token and st->tokens_out[st->step]. A pick in stop[] is
+// recorded after the others but not fed (model/chat.rs:149-153): the position
+// stays on the last fed token, which later steps of the call feed again at
+// that position, rewriting the same cache row and logits, and their picks are
+// dropped. The epoch advances with every step all the same, so that the
+// exchange words of each step carry a tag of their own.
+__device__ __forceinline__ uint32_t step_record(StepState *st, int advance, uint32_t tok) {
+    if (advance) st->epoch += 1;
+    if (st->stopped) return st->token;
+    bool stop = false;
+    for (int i = 0; i < st->n_stop; ++i) stop = stop || tok == st->stop[i];
+    if (stop) {
+        const long long at = st->step + (advance ? 1 : 0);
+        if (st->tokens_out) st->tokens_out[at] = tok;
+        st->stopped = (int)at + 1;
+        return st->token;
+    }
     if (advance) {
         st->pos += 1;
         st->step += 1;
-        st->epoch += 1;
     }
     st->token = tok;
     if (st->tokens_out) st->tokens_out[st->step] = tok;
+    return tok;
 }
 
 // emb.out = the embedding row of `tok` (model/cpu.rs:38-47), by the block.

@@ -126,9 +126,7 @@ __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__
     if (threadIdx.x == 0) {
         uint64_t b = 0;
         for (int w = 0; w < 16; ++w) b = max_u64(b, red[w]);
-        uint32_t tok = argmax_index(b);
-        step_record(st, advance, tok);
-        picked = tok;
+        picked = step_record(st, advance, argmax_index(b));
     }
     if (!emb.table) return;
     __syncthreads();

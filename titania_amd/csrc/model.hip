@@ -670,6 +670,20 @@ int capture_step(th_state *s) {
     return TH_OK;
 }
 
+// The captured decode step, captured again unless it already copies out the
+// logits as `keep` asks and draws or picks as `sampling` asks.
+int capture_or_keep(th_state *s, bool keep, bool sampling) {
+    if (s->graph_exec && (s->graph_keep != keep || s->sampling != sampling)) {
+        TH_HIP(hipGraphExecDestroy(s->graph_exec));
+        TH_HIP(hipGraphDestroy(s->graph));
+        s->graph_exec = nullptr;
+        s->graph = nullptr;
+    }
+    s->graph_keep = keep;
+    s->sampling = sampling;
+    return capture_step(s);
+}
+
 // All `steps` decode steps in one launch of the persistent kernel; the first
 // pick (from the logits the last forward left) runs just before it.
 int decode_persistent(th_state *s, size_t steps) {
@@ -917,11 +931,22 @@ int th_decode_trace(th_state *s, uint64_t *out, size_t cap, size_t *n) {
 
 namespace {
 
+// Decode steps a call with stop tokens enqueues between looks at whether one
+// has been picked (the steps after it repeat the last one and are wasted).
+constexpr size_t kStopCheckSteps = 8;
+
 // th_decode, and th_decode_sample when `sp` (the sampler's parameters and
-// generator state, updated on return) is not null.
+// generator state, updated on return) is not null. With stop tokens the call
+// ends at the first pick among them (recorded, not fed); *n_out then counts
+// the tokens written to out_tokens, the stop token included.
 int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tokens, float *out_logits,
-           th::SampleState *sp) {
+           th::SampleState *sp, const uint32_t *stops = nullptr, size_t n_stop = 0, size_t *n_out = nullptr,
+           bool *hit_stop = nullptr) {
+    if (hit_stop) *hit_stop = false;
     TH_REQUIRE(m && s && s->m == m && out_tokens, "th_decode: null argument or a state of another model");
+    TH_REQUIRE(n_stop <= (size_t)th::kStepMaxStops && (n_stop == 0 || stops), "at most %d stop tokens",
+               th::kStepMaxStops);
+    if (n_out) *n_out = 0;
     TH_REQUIRE(s->path == TH_PATH_FUSED, "decode continues a fused-path forward; run th_forward first");
     TH_REQUIRE(pos + steps <= s->max_len, "tokens past the end of the cache");
     if (steps == 0) return TH_OK;
@@ -957,6 +982,8 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
     init.tokens_out = s->tokens_dev;
     init.logits_out = out_logits ? s->logits_dev : nullptr;
     init.epoch = s->step_epoch;
+    init.n_stop = (int)n_stop;
+    for (size_t i = 0; i < n_stop; ++i) init.stop[i] = stops[i];
     TH_HIP(hipMemcpyAsync(s->step, &init, sizeof init, hipMemcpyHostToDevice, st));
     if (sampling) TH_HIP(hipMemcpyAsync(s->s_sample, sp, sizeof *sp, hipMemcpyHostToDevice, st));
     TH_HIP(hipStreamSynchronize(st));  // `init` is a stack temporary
@@ -969,8 +996,29 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
                                             step_embed(s))
                         : th::launch_pick(st, s->logits->ptr, vocab, s->argmax_part, s->step, 0, step_embed(s));
     };
-    if (s->xcd && !sampling) {
+    // Whether a stop token has been picked (its index in tokens_out + 1).
+    int stopped = 0;
+    auto look = [&]() -> int {
+        TH_HIP(hipMemcpyAsync(&stopped, &s->step->stopped, sizeof stopped, hipMemcpyDeviceToHost, st));
+        TH_HIP(hipStreamSynchronize(st));
+        return TH_OK;
+    };
+    size_t launched = 0;  // steps enqueued (each advances the epoch once)
+    if (n_stop) {
+        // The loop of model/chat.rs:147-178 on the device: the captured step,
+        // a few steps at a time, until a stop token or `steps` tokens.
+        TRY(capture_or_keep(s, out_logits != nullptr, sampling));
+        TH_HIP(first_pick());
+        TRY(look());
+        while (!stopped && launched < steps) {
+            const size_t n = std::min(kStopCheckSteps, steps - launched);
+            for (size_t i = 0; i < n; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
+            launched += n;
+            TRY(look());
+        }
+    } else if (s->xcd && !sampling) {
         TRY(decode_xcd(s, steps));
+        launched = steps;
     } else if (s->persistent && !sampling) {
         TRY(decode_persistent(s, steps));
     } else if (mode && strcmp(mode, "eager") == 0 && s->step_fused) {
@@ -980,25 +1028,26 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
         s->sampling = sampling;
         TH_HIP(first_pick());
         for (size_t i = 0; i < steps; ++i) TRY(enqueue_step(s));
+        launched = steps;
     } else {
-        // The captured step copies out the logits only if this call wants
-        // them, and draws or picks as this call does.
-        if (s->graph_exec && (s->graph_keep != (out_logits != nullptr) || s->sampling != sampling)) {
-            TH_HIP(hipGraphExecDestroy(s->graph_exec));
-            TH_HIP(hipGraphDestroy(s->graph));
-            s->graph_exec = nullptr;
-            s->graph = nullptr;
-        }
-        s->graph_keep = out_logits != nullptr;
-        s->sampling = sampling;
-        TRY(capture_step(s));
+        TRY(capture_or_keep(s, out_logits != nullptr, sampling));
         TH_HIP(first_pick());
         for (size_t i = 0; i < steps; ++i) TH_HIP(hipGraphLaunch(s->graph_exec, st));
+        launched = steps;
     }
-    s->step_epoch += (uint32_t)steps;
-    TH_HIP(hipMemcpyAsync(out_tokens, s->tokens_dev, steps * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    if (out_logits)
-        TH_HIP(hipMemcpyAsync(out_logits, s->logits_dev, steps * vocab * sizeof(float), hipMemcpyDeviceToHost, st));
+    s->step_epoch += (uint32_t)launched;
+    // A stop token picked after the last fed token is past the call's tokens:
+    // the next call picks it again.
+    if ((size_t)stopped > steps) stopped = 0;
+    if (hit_stop) *hit_stop = stopped != 0;
+    // Tokens out: all `steps`, or up to the stop token; each but the stop
+    // token was fed, and its logits kept when asked.
+    const size_t n_tok = stopped ? (size_t)stopped : steps;
+    const size_t n_fed = stopped ? (size_t)stopped - 1 : steps;
+    if (n_out) *n_out = n_tok;
+    TH_HIP(hipMemcpyAsync(out_tokens, s->tokens_dev, n_tok * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    if (out_logits && n_fed)
+        TH_HIP(hipMemcpyAsync(out_logits, s->logits_dev, n_fed * vocab * sizeof(float), hipMemcpyDeviceToHost, st));
     unsigned poll_failures = 0;
     if (s->s_err) TH_HIP(hipMemcpyAsync(&poll_failures, s->s_err, sizeof poll_failures, hipMemcpyDeviceToHost, st));
     if (sampling) TH_HIP(hipMemcpyAsync(sp, s->s_sample, sizeof *sp, hipMemcpyDeviceToHost, st));
@@ -1033,6 +1082,31 @@ int th_decode_sample(th_model *m, th_state *s, size_t pos, size_t steps, float t
     // token, which the next call draws again): hand back the state after the
     // steps-th draw, as the reference's sampler would have it.
     *rng = steps ? ss.rng_prev : ss.rng;
+    return TH_OK;
+}
+
+int th_generate(th_model *m, th_state *s, size_t pos, size_t max_tokens, const uint32_t *stop, size_t n_stop,
+                float temperature, size_t top_k, float top_p, uint64_t *rng, uint32_t *out_tokens, size_t *n_out) {
+    TH_REQUIRE(m && n_out, "th_generate: null argument");
+    *n_out = 0;
+    TH_REQUIRE(n_stop >= 1 && n_stop <= (size_t)th::kStepMaxStops && stop, "th_generate: 1 to %d stop tokens",
+               th::kStepMaxStops);
+    for (size_t i = 0; i < n_stop; ++i)
+        TH_REQUIRE(stop[i] < (uint32_t)m->c.vocab_size, "stop token %u is past the vocabulary", stop[i]);
+    bool hit = false;
+    if (temperature == 0.0f) return decode(m, s, pos, max_tokens, out_tokens, nullptr, nullptr, stop, n_stop, n_out, &hit);
+    TH_REQUIRE(rng, "th_generate: null generator state");
+    const size_t vocab = (size_t)m->c.vocab_size;
+    const size_t k = std::min(std::max<size_t>(top_k, 1), vocab);
+    TH_REQUIRE(k <= (size_t)th::kSampleMaxTopK, "top_k %zu: the device samples from at most %d candidates", k,
+               th::kSampleMaxTopK);
+    TH_REQUIRE(vocab <= th::kSampleMaxVocab, "sampling over %zu values: at most %zu", vocab, th::kSampleMaxVocab);
+    TH_REQUIRE(top_p > 0.0f, "top_p must be greater than 0");
+    th::SampleState ss{*rng, *rng, temperature, top_p, (int)k, 0};
+    TRY(decode(m, s, pos, max_tokens, out_tokens, nullptr, &ss, stop, n_stop, n_out, &hit));
+    // Ended at a stop token: every draw was used (no draw after it). Else the
+    // device drew once past the last token, as in th_decode_sample.
+    *rng = hit || !max_tokens ? ss.rng : ss.rng_prev;
     return TH_OK;
 }
 

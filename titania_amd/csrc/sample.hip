@@ -90,10 +90,12 @@ __global__ __launch_bounds__(kSortThreads) void sample_kernel(const float *__res
                 n += 1;
             }
         }
+        // Steps after a stop token draw nothing (their picks are dropped).
+        const bool draw = !(st && st->stopped);
         uint64_t x = ss->rng;
-        ss->rng_prev = x;
+        if (draw) ss->rng_prev = x;
         float r = rng_next_f32(x) * cumulative;
-        ss->rng = x;
+        if (draw) ss->rng = x;
         uint32_t tok = argmax_index(keys[n - 1]);
         for (int i = 0; i < n; ++i) {
             r -= probs[i];
@@ -102,7 +104,7 @@ __global__ __launch_bounds__(kSortThreads) void sample_kernel(const float *__res
                 break;
             }
         }
-        if (st) step_record(st, advance, tok);
+        if (st) tok = step_record(st, advance, tok);
         else ss->token = tok;
         picked = tok;
     }

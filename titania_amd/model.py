@@ -99,6 +99,25 @@ class Model:
         return (toks, logits) if keep_logits else toks
 
 
+    def decode_until(self, state: "State", pos: int, max_tokens: int, stop, sampler=None) -> np.ndarray:
+        """th_generate: from position `pos`, picks (or draws, with `sampler`)
+        and feeds tokens until one in `stop` (1 to 8 ids) is picked, at most
+        `max_tokens` in all. Returns the tokens; a stop token, if reached, is
+        the last and was not fed."""
+        stops = np.ascontiguousarray(stop, dtype=np.uint32).reshape(-1)
+        toks = np.empty(max(int(max_tokens), 0), dtype=np.uint32)
+        n = C.c_size_t()
+        rng = C.c_uint64(sampler.rng if sampler is not None else 0)
+        t = float(sampler.temperature) if sampler is not None else 0.0
+        k = max(sampler.top_k, 0) if sampler is not None else 0
+        p = float(sampler.top_p) if sampler is not None else 1.0
+        check(lib().th_generate(self.handle, state.handle, int(pos), toks.size, stops.ctypes.data, stops.size, t, k, p,
+                                C.byref(rng) if sampler is not None else None, toks.ctypes.data, C.byref(n)))
+        if sampler is not None:
+            sampler.rng = rng.value
+        return toks[: n.value].copy()
+
+
 class State:
     """Caches and buffers for sequences of up to max_len tokens (model.rs:176-211)."""
 
