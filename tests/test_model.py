@@ -277,6 +277,18 @@ def _long_context_check(model, cfg, n_prompt, steps, kv, tol, seed):
     ops.close()
 
 
+@pytest.mark.parametrize("n_prompt,steps,kv", [(250, 12, TH_KV_F32), (120, 16, TH_KV_F32), (900, 6, TH_KV_F32),
+                                               (1500, 8, TH_KV_F32), (1020, 20, TH_KV_BF16), (3000, 6, TH_KV_BF16)])
+def test_qwen06_decode_chunked(qwen06, n_prompt, steps, kv):
+    """Qwen3-0.6B contexts that the fused q/k/v + attention launch covers with
+    several attention blocks per q head (one per 64 f32 / 128 bf16 cached
+    positions, merged by the head's first): steps crossing chunk boundaries,
+    up to 24 chunks (merged eight at a time). bf16 caches differ from the f32 reference path by their
+    rounding, hence the looser bar there."""
+    m, _ = qwen06
+    _long_context_check(m, QWEN3_0_6B, n_prompt, steps, kv, 1e-3 if kv == TH_KV_F32 else 3e-2, seed=n_prompt)
+
+
 @pytest.mark.slow
 def test_qwen06_decode_4k_context(qwen06):
     """Qwen3-0.6B at a 4096-token context, f32 caches (the reference's type)."""

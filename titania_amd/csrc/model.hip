@@ -353,8 +353,11 @@ int ensure_fused_state(th_state *s) {
         for (auto &b : sb) TH_HIP(hipMalloc(b.p, b.n * sizeof(float)));
         TH_HIP(hipMalloc(&s->s_part, (size_t)th::step_logits_partials((int)c.vocab_size) * sizeof(uint64_t)));
         // Zeroed: epoch 0 precedes every epoch a step uses.
-        TH_HIP(hipMalloc(&s->s_words, (qd + 2 * kvd) * sizeof(unsigned long long)));
-        TH_HIP(hipMemset(s->s_words, 0, (qd + 2 * kvd) * sizeof(unsigned long long)));
+        const int chunks = std::max(
+            th::step_qkv_attn_chunks(s->max_len, s->kv_dtype == TH_KV_BF16, (int)c.num_attention_heads), 1);
+        const size_t words = th::step_qkv_attn_words((int)qd, (int)kvd, (int)c.num_attention_heads, chunks);
+        TH_HIP(hipMalloc(&s->s_words, words * sizeof(unsigned long long)));
+        TH_HIP(hipMemset(s->s_words, 0, words * sizeof(unsigned long long)));
         TH_HIP(hipMalloc(&s->s_err, sizeof(unsigned)));
         TH_HIP(hipMemset(s->s_err, 0, sizeof(unsigned)));
 
@@ -384,11 +387,12 @@ int enqueue_step(th_state *s) {
     const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads;
     const int qd = nh * hd, kvd = nkv * hd, V = (int)c.vocab_size;
     const float eps = c.rms_norm_eps;
+    const int chunks = th::step_qkv_attn_chunks(s->max_len, s->kv_dtype == TH_KV_BF16, (int)nh);
     const int nsplit = th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
     // One launch for q/k/v and attention while one split covers the context.
-    const bool fuse_attn = nsplit == 1 && th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64;
+    const bool fuse_attn = chunks > 0 && th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64;
     // sx_b holds the token's embedding row: the previous pick wrote it.
     const float *y_prev = nullptr;
     for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -417,7 +421,7 @@ int enqueue_step(th_state *s) {
         a.pos = &s->step->pos;
         a.n_heads = nh;
         a.n_kv_heads = nkv;
-        a.nsplit = nsplit;
+        a.nsplit = fuse_attn ? 1 : nsplit;
         a.kv_bf16 = s->kv_dtype == TH_KV_BF16;
         a.eps = eps;
         a.out = s->s_att;
@@ -431,6 +435,7 @@ int enqueue_step(th_state *s) {
             f.err = s->s_err;
             f.st = s->step;
             f.layer = (int)l;
+            f.chunks = chunks;
             TH_HIP(th::launch_step_qkv_attn(st, f));
         } else {
             TH_HIP(th::launch_step_qkv(st, q));

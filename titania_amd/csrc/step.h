@@ -64,18 +64,35 @@ struct StepAttnArgs {
 int step_attention_splits(size_t max_len, int kv_bf16);
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a);
 
-// The q/k/v GEMV (as launch_step_qkv) and single-split attention in one launch:
-// the GEMV blocks publish the rows as (value | epoch << 32) words, epoch =
-// st->epoch * 64 + layer + 1; one extra block per q head requests its cached
-// rows meanwhile, then attends from the words. For contexts one split covers.
+// The q/k/v GEMV (as launch_step_qkv) and the attention in one launch: the
+// GEMV blocks publish the rows as (value | epoch << 32) words, epoch =
+// st->epoch * 64 + layer + 1; `chunks` extra blocks per q head, one per pass
+// of cached rows, request their rows meanwhile, then attend from the words;
+// the first chunk's block merges the others' partials (exchanged as words).
 struct StepQkvAttnArgs {
     StepQkvArgs qkv;               // x_out as launch_step_qkv; qkv unused
     StepAttnArgs at;               // qkv and partials unused, nsplit 1
-    unsigned long long *words;     // [q_rows + 2 kv_rows]
+    // [q_rows + 2 kv_rows] q/k/v words, then [n_heads][chunks][head_dim + 2]
+    // chunk partials (sum, max, denominator)
+    unsigned long long *words;
     unsigned *err;                 // counts attention blocks whose poll gave up
     const StepState *st;
     int layer;
+    int chunks;                    // attention blocks per q head (step_qkv_attn_chunks)
 };
+
+// Most attention blocks per q head, and per launch, in launch_step_qkv_attn.
+constexpr int kStepQkvAttnMaxChunks = 32;
+constexpr int kStepQkvAttnMaxBlocks = 512;
+
+// Attention blocks per q head that launch_step_qkv_attn uses for caches of
+// max_len positions (one per register pass of rows: 64 f32 or 128 bf16
+// positions), or 0 when that is more than kStepQkvAttnMaxChunks or the
+// launch's attention blocks more than kStepQkvAttnMaxBlocks.
+int step_qkv_attn_chunks(size_t max_len, int kv_bf16, int n_heads);
+
+// Exchange words launch_step_qkv_attn needs.
+size_t step_qkv_attn_words(int q_rows, int kv_rows, int n_heads, int chunks);
 
 // The attention blocks of launch_step_qkv_attn read cached rows in passes of
 // up to this many positions without clamping to the context: the caches'

@@ -390,10 +390,13 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
     const int ngemv = (a.n_rows + RPB - 1) / RPB;
     const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
-        // One block per q head: the heads of a KV group attend in parallel
-        // (each reads the group's cached rows), the group's first appends.
-        const int b = blockIdx.x - ngemv, g = b / G;
-        attend_regs<1, KV, true>(q.at, g, b, b % G == 0, 0, q.at.head_stride / 128, q.words, epoch, q.err);
+        // `chunks` blocks per q head, one per pass of cached rows: the heads
+        // of a KV group attend in parallel (each reads the group's rows), the
+        // group's first head appends; each head's first chunk merges.
+        const int b = blockIdx.x - ngemv, h = b / q.chunks, c = b % q.chunks, g = h / G;
+        unsigned long long *xw = q.words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
+        attend_regs<1, KV, true>(q.at, g, h, h % G == 0, c, KvRegs<KV>::kRows, q.words, epoch, q.err, xw,
+                                 q.chunks);
         return;
     }
     extern __shared__ float xs[];
@@ -425,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
 
 template <int CPL, int G>
 hipError_t qkv_attn_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a) {
-    dim3 grid((unsigned)((a.n_rows + 7) / 8 + q.at.n_heads));
+    dim3 grid((unsigned)((a.n_rows + 7) / 8 + q.at.n_heads * q.chunks));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
         qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(q, a);
@@ -566,9 +569,24 @@ bool step_qkv_attn_supported(int hidden, int n_heads, int n_kv_heads) {
     return hidden % 512 == 0 && (g == 2 || g == 4) && (cpl == 1 || cpl == 2 || cpl == 5);
 }
 
+int step_qkv_attn_chunks(size_t max_len, int kv_bf16, int n_heads) {
+    const size_t rows = kv_bf16 ? KvRegs<uint16_t>::kRows : KvRegs<float>::kRows;
+    const size_t chunks = (max_len + rows - 1) / rows;
+    return chunks >= 1 && chunks <= (size_t)kStepQkvAttnMaxChunks &&
+                   chunks * (size_t)n_heads <= (size_t)kStepQkvAttnMaxBlocks
+               ? (int)chunks
+               : 0;
+}
+
+size_t step_qkv_attn_words(int q_rows, int kv_rows, int n_heads, int chunks) {
+    return (size_t)q_rows + 2 * (size_t)kv_rows + (size_t)n_heads * chunks * (128 + 2);
+}
+
 hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
     const StepQkvArgs &k = q.qkv;
-    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit != 1)
+    const long long max_len = q.at.head_stride / 128;
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit != 1 || q.chunks < 1 ||
+        q.chunks != step_qkv_attn_chunks((size_t)max_len, q.at.kv_bf16, q.at.n_heads))
         return hipErrorInvalidValue;
     GemvArgs a{};
     a.rows.base[0] = k.wq;

@@ -179,10 +179,16 @@ template <> struct KvRegs<uint16_t> {
 // The block's G q heads are qh0 .. qh0 + G - 1 of KV head g (qh0 = g G unless
 // a KV head's group is spread over several blocks, of which only the one with
 // `append` writes the new key and value).
+//
+// With `xw` (chunked launches, G = 1): the block covers one chunk of the
+// context; chunks past the context return at once. When several chunks hold
+// positions, each but the first publishes its (sum, max, denominator) as
+// epoch words at xw + (qh0 * n_chunks + split) * (head_dim + 2), and the
+// first polls them and merges all, in chunk order, into a.out.
 template <int G, typename KV, bool WORDS>
 __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh0, bool append, int split,
                                             long long chunk, const unsigned long long *words, unsigned epoch,
-                                            unsigned *err) {
+                                            unsigned *err, unsigned long long *xw = nullptr, int n_chunks = 1) {
     using R = KvRegs<KV>;
     constexpr int HD = 128, HALF = HD / 2, ROWS = R::kRows;
     constexpr int NK = ROWS / 16;  // keys per lane in the score pass
@@ -238,6 +244,7 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
     if (!WORDS && tid < HD) vnew = a.qkv[qd + kvd + (size_t)g * HD + tid];
     const long long pos = *a.pos;
     const long long len = pos + 1;
+    if (xw && s0 >= len) return;  // a chunk past the context (uniform over the block)
     const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
     if (WORDS) {
         for (int it = 0;; ++it) {
@@ -398,10 +405,64 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
             if (lane < 32) red[gg][wave][d4 * 4 + i] = acc[gg][i];
         }
     __syncthreads();
+    const int n_live = (int)((len + chunk - 1) / chunk);  // chunks holding positions
     for (int idx = tid; idx < G * HD; idx += kThreads) {
         const int gg = idx / HD, d = idx % HD;
         const float sm = ((red[gg][0][d] + red[gg][1][d]) + red[gg][2][d]) + red[gg][3][d];
         const long long h = (long long)qh0 + gg;
+        if (xw && n_live > 1) {
+            unsigned long long *hw = xw + (size_t)h * n_chunks * (HD + 2);
+            auto tag = [&](float v) { return ((unsigned long long)epoch << 32) | __float_as_uint(v); };
+            if (split > 0) {
+                unsigned long long *cw = hw + (size_t)split * (HD + 2);
+                __hip_atomic_store(cw + d, tag(sm), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0) {
+                    __hip_atomic_store(cw + HD, tag(st_m[gg]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(cw + HD + 1, tag(st_l[gg]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                continue;
+            }
+            // Merge chunks 1.. into this one's (sum, max, denominator), in
+            // order, polling eight chunks' words at a time.
+            constexpr int PG = 8;
+            float num = sm, m = st_m[gg], den = st_l[gg];
+            for (int c0 = 1; c0 < n_live; c0 += PG) {
+                unsigned long long wa[PG], wm[PG], wl[PG];
+                for (int it = 0;; ++it) {
+                    bool ok = true;
+#pragma unroll
+                    for (int i = 0; i < PG; ++i) {
+                        if (c0 + i >= n_live) break;
+                        const unsigned long long *cw = hw + (size_t)(c0 + i) * (HD + 2);
+                        wa[i] = __hip_atomic_load(cw + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        wm[i] = __hip_atomic_load(cw + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        wl[i] = __hip_atomic_load(cw + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+#pragma unroll
+                    for (int i = 0; i < PG; ++i) {
+                        if (c0 + i >= n_live) break;
+                        ok = ok && (unsigned)(wa[i] >> 32) == epoch && (unsigned)(wm[i] >> 32) == epoch &&
+                             (unsigned)(wl[i] >> 32) == epoch;
+                    }
+                    if (ok) break;
+                    if (it >= (1 << 21)) {
+                        if (d == 0) atomicAdd(err, 1u);
+                        break;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < PG; ++i) {
+                    if (c0 + i >= n_live) break;
+                    const float mc = __uint_as_float((unsigned)wm[i]), mx = fmaxf(m, mc);
+                    const float s_old = expf(m - mx), s_new = expf(mc - mx);
+                    num = num * s_old + __uint_as_float((unsigned)wa[i]) * s_new;
+                    den = den * s_old + __uint_as_float((unsigned)wl[i]) * s_new;
+                    m = mx;
+                }
+            }
+            a.out[h * HD + d] = num / den;
+            continue;
+        }
         if (a.nsplit == 1) {
             a.out[h * HD + d] = sm / st_l[gg];
         } else {
