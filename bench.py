@@ -210,6 +210,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=32, help="timed decode steps")
     ap.add_argument("--warmup", type=int, default=32, help="untimed decode steps before the timed ones")
     ap.add_argument("--prompt", type=int, default=16)
+    ap.add_argument("--max-len", type=int, default=0,
+                    help="positions the state's caches hold (0: prompt + steps, the default workload)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kv", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--model", choices=["qwen3-0.6b", "qwen3-4b"], default="qwen3-0.6b")
@@ -253,7 +255,7 @@ def main() -> int:
     dev = Hip(0)
     model = Model(dev, cfg, weights)
     K, W = args.steps, args.warmup
-    state = State(model, args.prompt + max(K, W, 1), kv)
+    state = State(model, max(args.max_len, args.prompt + max(K, W, 1)), kv)
 
     # Warmup: prefill, W decode steps (captures the decode graph).
     model.forward(state, prompt, 0, TH_PATH_FUSED, want_logits=False)
@@ -303,7 +305,7 @@ def main() -> int:
         "data": "synthetic (seeded N(0,0.02) bf16 weights, gains 1, uniform-random prompt)",
         "config": {
             "workload": f"{args.model} greedy decode, {args.prompt}-token prompt, {K} steps, batch 1, "
-                        f"{args.kv} KV cache",
+                        f"{args.kv} KV cache" + (f" of {args.max_len} positions" if args.max_len else ""),
             "model": args.model,
             "global_batch": 1,
             "seq_len": args.prompt + K,

@@ -200,7 +200,7 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
     __shared__ float scores[G][ROWS];
     __shared__ float st_m[G], st_l[G], st_a[G];
     __shared__ float red[G][kWaves][HD];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane & 15, kq = wave * 4 + (lane >> 4);  // score pass: dims 8*sub.., key kq of 16
     const int d4 = tid & 31, pv = tid >> 5;                   // value pass: dims 4*d4.., key pv of 8
     const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
@@ -218,34 +218,62 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
 #pragma unroll
         for (int i = 0; i < NV; ++i) vr[i] = R::load_v(vc + (c0 + i * 8) * HD + pv * HD, d4);
     };
-    if (s0 < max_len) {
-        load_k(s0);
-        load_v(s0);
+    // The position through the scalar cache (the kernel only reads it): a
+    // chunk past the context leaves before requesting any rows, and the small
+    // loads that depend on the position need no vector wait first.
+    const long long pos = *(const __attribute__((address_space(4))) long long *)a.pos;
+    const long long len = pos + 1;
+    if (xw && s0 >= len) return;  // a chunk past the context (uniform over the block)
+    // A range starting past max_len (it has no positions) reads the last rows
+    // again, within the caches' tail: the loads need no branch.
+    const long long k0 = s0 < max_len ? s0 : max_len - 1;
+    if (WORDS) {
+        // The q/k/v words come long after the rows: request the rows first.
+        load_k(k0);
+        load_v(k0);
     }
+    const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
     // RMSNorm gains of this wave's heads (q heads 0..G-1, then k), and, from
-    // a.qkv, the raw rows: all requested before the position is known.
-    float ga[HPW], gb[HPW], av[HPW], bv[HPW], vnew = 0.f;
+    // a.qkv, the raw rows: loaded with no branch (rows clamped to valid ones)
+    // and used only once the cached rows are requested, so that no wait for
+    // them comes before that.
+    uint32_t gra[HPW], grb[HPW];
+    float ar[HPW], br[HPW], vraw = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+        const int h = min(wave + hh * kWaves, G);
+        const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
+        const uint16_t *gp = gain ? gain : reinterpret_cast<const uint16_t *>(a.rope);
+        gra[hh] = gp[lane];
+        grb[hh] = gp[lane + HALF];
+        ar[hh] = br[hh] = 0.f;
+        if (!WORDS) {
+            const float *x = h < G ? a.qkv + (size_t)(qh0 + h) * HD : a.qkv + qd + (size_t)g * HD;
+            ar[hh] = x[lane];
+            br[hh] = x[lane + HALF];
+        }
+    }
+    if (!WORDS) {
+        vraw = a.qkv[qd + kvd + (size_t)g * HD + (tid & (HD - 1))];
+        // Here q/k/v are already in memory: the small loads go first, so that
+        // waiting for them (loads complete in issue order for the wait
+        // counter) does not wait for the rows, which stream in meanwhile.
+        __builtin_amdgcn_sched_barrier(0);
+        load_k(k0);
+        load_v(k0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    float ga[HPW], gb[HPW], av[HPW], bv[HPW];
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
         const int h = wave + hh * kWaves;
-        ga[hh] = gb[hh] = 1.f;
-        av[hh] = bv[hh] = 0.f;
-        const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
-        if (h <= G && gain) {
-            ga[hh] = bf16_to_f32(gain[lane]);
-            gb[hh] = bf16_to_f32(gain[lane + HALF]);
-        }
-        if (!WORDS && h <= G) {
-            const float *x = h < G ? a.qkv + (size_t)(qh0 + h) * HD : a.qkv + qd + (size_t)g * HD;
-            av[hh] = x[lane];
-            bv[hh] = x[lane + HALF];
-        }
+        const bool gained = h <= G && (h < G ? a.q_norm : a.k_norm) != nullptr;
+        ga[hh] = gained ? bf16_to_f32((uint16_t)gra[hh]) : 1.f;
+        gb[hh] = gained ? bf16_to_f32((uint16_t)grb[hh]) : 1.f;
+        av[hh] = h <= G ? ar[hh] : 0.f;
+        bv[hh] = h <= G ? br[hh] : 0.f;
     }
-    if (!WORDS && tid < HD) vnew = a.qkv[qd + kvd + (size_t)g * HD + tid];
-    const long long pos = *a.pos;
-    const long long len = pos + 1;
-    if (xw && s0 >= len) return;  // a chunk past the context (uniform over the block)
-    const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
+    float vnew = tid < HD ? vraw : 0.f;
     if (WORDS) {
         for (int it = 0;; ++it) {
             int ok = 1;
