@@ -395,8 +395,7 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
         // group's first head appends; each head's first chunk merges.
         const int b = blockIdx.x - ngemv, h = b / q.chunks, c = b % q.chunks, g = h / G;
         unsigned long long *xw = q.words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
-        attend_regs<1, KV, true>(q.at, g, h, h % G == 0, c, KvRegs<KV>::kRows, q.words, epoch, q.err, xw,
-                                 q.chunks);
+        attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
         return;
     }
     extern __shared__ float xs[];

@@ -163,6 +163,69 @@ template <> struct KvRegs<uint16_t> {
     }
 };
 
+// The end of a chunked launch for dimension d of q head h, given this chunk's
+// (sum, max, denominator): with one chunk holding positions, the output;
+// else chunks 1.. publish theirs as epoch words at
+// xw + (h * n_chunks + split) * (128 + 2) and chunk 0 polls them (eight
+// chunks at a time) and merges all in chunk order into a.out.
+__device__ __forceinline__ void chunk_finish(const StepAttnArgs &a, long long h, int d, float sm, float sm_m,
+                                             float sm_l, unsigned long long *xw, int n_chunks, int split,
+                                             int n_live, unsigned epoch, unsigned *err) {
+    constexpr int HD = 128;
+    if (n_live == 1) {
+        a.out[h * HD + d] = sm / sm_l;
+        return;
+    }
+    unsigned long long *hw = xw + (size_t)h * n_chunks * (HD + 2);
+    auto tag = [&](float v) { return ((unsigned long long)epoch << 32) | __float_as_uint(v); };
+    if (split > 0) {
+        unsigned long long *cw = hw + (size_t)split * (HD + 2);
+        __hip_atomic_store(cw + d, tag(sm), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+            __hip_atomic_store(cw + HD, tag(sm_m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(cw + HD + 1, tag(sm_l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    constexpr int PG = 8;
+    float num = sm, m = sm_m, den = sm_l;
+    for (int c0 = 1; c0 < n_live; c0 += PG) {
+        unsigned long long wa[PG], wm[PG], wl[PG];
+        for (int it = 0;; ++it) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < PG; ++i) {
+                if (c0 + i >= n_live) break;
+                const unsigned long long *cw = hw + (size_t)(c0 + i) * (HD + 2);
+                wa[i] = __hip_atomic_load(cw + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wm[i] = __hip_atomic_load(cw + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wl[i] = __hip_atomic_load(cw + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int i = 0; i < PG; ++i) {
+                if (c0 + i >= n_live) break;
+                ok = ok && (unsigned)(wa[i] >> 32) == epoch && (unsigned)(wm[i] >> 32) == epoch &&
+                     (unsigned)(wl[i] >> 32) == epoch;
+            }
+            if (ok) break;
+            if (it >= (1 << 21)) {
+                if (d == 0) atomicAdd(err, 1u);
+                break;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PG; ++i) {
+            if (c0 + i >= n_live) break;
+            const float mc = __uint_as_float((unsigned)wm[i]), mx = fmaxf(m, mc);
+            const float s_old = expf(m - mx), s_new = expf(mc - mx);
+            num = num * s_old + __uint_as_float((unsigned)wa[i]) * s_new;
+            den = den * s_old + __uint_as_float((unsigned)wl[i]) * s_new;
+            m = mx;
+        }
+    }
+    a.out[h * HD + d] = num / den;
+}
+
 // Attention of one KV head by one block over the positions [s0, s0 + chunk)
 // of the context, s0 = split * chunk: the whole context (split 0, chunk
 // max_len) or one split of it. The raw q/k/v come from a.qkv, or (WORDS) from
@@ -439,56 +502,7 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
         const float sm = ((red[gg][0][d] + red[gg][1][d]) + red[gg][2][d]) + red[gg][3][d];
         const long long h = (long long)qh0 + gg;
         if (xw && n_live > 1) {
-            unsigned long long *hw = xw + (size_t)h * n_chunks * (HD + 2);
-            auto tag = [&](float v) { return ((unsigned long long)epoch << 32) | __float_as_uint(v); };
-            if (split > 0) {
-                unsigned long long *cw = hw + (size_t)split * (HD + 2);
-                __hip_atomic_store(cw + d, tag(sm), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (d == 0) {
-                    __hip_atomic_store(cw + HD, tag(st_m[gg]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(cw + HD + 1, tag(st_l[gg]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                continue;
-            }
-            // Merge chunks 1.. into this one's (sum, max, denominator), in
-            // order, polling eight chunks' words at a time.
-            constexpr int PG = 8;
-            float num = sm, m = st_m[gg], den = st_l[gg];
-            for (int c0 = 1; c0 < n_live; c0 += PG) {
-                unsigned long long wa[PG], wm[PG], wl[PG];
-                for (int it = 0;; ++it) {
-                    bool ok = true;
-#pragma unroll
-                    for (int i = 0; i < PG; ++i) {
-                        if (c0 + i >= n_live) break;
-                        const unsigned long long *cw = hw + (size_t)(c0 + i) * (HD + 2);
-                        wa[i] = __hip_atomic_load(cw + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        wm[i] = __hip_atomic_load(cw + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        wl[i] = __hip_atomic_load(cw + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-#pragma unroll
-                    for (int i = 0; i < PG; ++i) {
-                        if (c0 + i >= n_live) break;
-                        ok = ok && (unsigned)(wa[i] >> 32) == epoch && (unsigned)(wm[i] >> 32) == epoch &&
-                             (unsigned)(wl[i] >> 32) == epoch;
-                    }
-                    if (ok) break;
-                    if (it >= (1 << 21)) {
-                        if (d == 0) atomicAdd(err, 1u);
-                        break;
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < PG; ++i) {
-                    if (c0 + i >= n_live) break;
-                    const float mc = __uint_as_float((unsigned)wm[i]), mx = fmaxf(m, mc);
-                    const float s_old = expf(m - mx), s_new = expf(mc - mx);
-                    num = num * s_old + __uint_as_float((unsigned)wa[i]) * s_new;
-                    den = den * s_old + __uint_as_float((unsigned)wl[i]) * s_new;
-                    m = mx;
-                }
-            }
-            a.out[h * HD + d] = num / den;
+            chunk_finish(a, h, d, sm, st_m[gg], st_l[gg], xw, n_chunks, split, n_live, epoch, err);
             continue;
         }
         if (a.nsplit == 1) {
@@ -501,6 +515,185 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
                 a.part_ml[slot * 2 + 1] = st_l[gg];
             }
         }
+    }
+}
+
+// Value pairs (dims 2 lane, 2 lane + 1 of a row) as the four-wave attention
+// holds them.
+template <typename KV> struct VPair;
+template <> struct VPair<float> {
+    using T = float2;
+    __device__ static T load(const float *row, int lane) { return reinterpret_cast<const float2 *>(row)[lane]; }
+    __device__ static float2 get(const T &v) { return v; }
+};
+template <> struct VPair<uint16_t> {
+    using T = uint32_t;
+    __device__ static T load(const uint16_t *row, int lane) { return reinterpret_cast<const uint32_t *>(row)[lane]; }
+    __device__ static float2 get(const T &v) { return make_float2(bf16_lo(v), bf16_hi(v)); }
+};
+
+// Attention of one q head h (of KV head g) over one chunk of the cache, rows
+// [split * kRows, + kRows) (64 f32 / 128 bf16 positions), by the block's four
+// waves with two block barriers. Waves 0, 1 and 2 poll the q, k and v words
+// (q and k are normalized and rotated in registers) into LDS; then wave w
+// takes a quarter of the rows: its lanes score them in groups of
+// 64 / rows-per-wave lanes (each load instruction reads consecutive 16-byte
+// chunks of every row), the wave takes the max and sum of its rows with DPP
+// reductions and accumulates P.V for two dimensions a lane, each row's weight
+// broadcast from the lane that holds it. The four (sum, max, denominator)
+// partials merge in wave order and chunk_finish ends the chunk. The cached
+// rows, the norm gains and the RoPE row are requested at the start, before
+// the words arrive; rows past max_len come from the caches' tail and, like
+// every row past the context, are masked.
+template <typename KV>
+__device__ __forceinline__ void attend_wave4(const StepAttnArgs &a, int g, int h, bool append, int split,
+                                             const unsigned long long *words, unsigned epoch, unsigned *err,
+                                             unsigned long long *xw, int n_chunks) {
+    constexpr int HD = 128, HALF = HD / 2;
+    constexpr int ROWS = KvRegs<KV>::kRows;
+    constexpr int RW = ROWS / kWaves;         // rows per wave: 16 f32 / 32 bf16
+    constexpr int LPR = 64 / RW;              // lanes per row in the scores: 4 / 2
+    constexpr int DPL = HD / LPR;             // dims per lane in the scores: 32 / 64
+    constexpr int EPV = 16 / (int)sizeof(KV); // elements per 16-byte load
+    constexpr int NKL = DPL / EPV;            // 16-byte K loads per lane: 8
+    static_assert(LPR == 2 || LPR == 4, "row groups within a DPP quad");
+    __shared__ float hq[HD], hk[HD], hv[HD];
+    __shared__ float pacc[kWaves][HD], pm[kWaves], pl[kWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
+    const long long max_len = a.head_stride / HD;
+    const long long s0 = (long long)split * ROWS;
+    const long long pos = *(const __attribute__((address_space(4))) long long *)a.pos;
+    const long long len = pos + 1;
+    if (s0 >= len) return;  // a chunk past the context (uniform over the block)
+    const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
+    const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
+    const long long r0 = s0 + wave * RW;                  // this wave's first row
+    const long long rb = r0 < max_len ? r0 : max_len - 1;  // where its loads start
+    const int sr = lane / LPR, sj = lane % LPR;           // score row of the lane, slice of it
+    // K: 16-byte chunk i * LPR + sj of the row, i < NKL (each load instruction
+    // reads LPR consecutive chunks of every row); V: dims 2 lane, 2 lane + 1.
+    uint4 kr[NKL];
+    typename VPair<KV>::T vr[RW];
+    {
+        const uint4 *kp = reinterpret_cast<const uint4 *>(kc + (rb + sr) * HD);
+#pragma unroll
+        for (int i = 0; i < NKL; ++i) kr[i] = kp[i * LPR + sj];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) vr[r] = VPair<KV>::load(vc + (rb + r) * HD, lane);
+    }
+    const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
+    const float gq0 = a.q_norm ? bf16_to_f32(a.q_norm[lane]) : 1.f;
+    const float gq1 = a.q_norm ? bf16_to_f32(a.q_norm[lane + HALF]) : 1.f;
+    const float gk0 = a.k_norm ? bf16_to_f32(a.k_norm[lane]) : 1.f;
+    const float gk1 = a.k_norm ? bf16_to_f32(a.k_norm[lane + HALF]) : 1.f;
+    // The raw q (head h), k and v (KV head g) rows from the epoch words, one
+    // row a wave (waves 0, 1, 2), normalized and rotated in registers.
+    if (wave < 3) {
+        const unsigned long long *src = wave == 0   ? words + (size_t)h * HD
+                                        : wave == 1 ? words + qd + (size_t)g * HD
+                                                    : words + qd + kvd + (size_t)g * HD;
+        unsigned long long wa, wb;
+        for (int it = 0;; ++it) {
+            wa = __hip_atomic_load(src + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wb = __hip_atomic_load(src + lane + HALF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool ok = (unsigned)(wa >> 32) == epoch && (unsigned)(wb >> 32) == epoch;
+            if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+            if (it >= (1 << 21)) {
+                if (lane == 0) atomicAdd(err, 1u);
+                break;
+            }
+        }
+        float x0 = __uint_as_float((unsigned)wa), x1 = __uint_as_float((unsigned)wb);
+        float *dst = wave == 0 ? hq : wave == 1 ? hk : hv;
+        if (wave < 2) {
+            // RMSNorm (model.rs:111-116) + RoPE (model.rs:117-118).
+            if (wave == 0 ? a.q_norm != nullptr : a.k_norm != nullptr) {
+                const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
+                const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
+                x0 = x0 * (sc * (wave == 0 ? gq0 : gk0));
+                x1 = x1 * (sc * (wave == 0 ? gq1 : gk1));
+            }
+            dst[lane] = x0 * cs.x - x1 * cs.y;
+            dst[lane + HALF] = x1 * cs.x + x0 * cs.y;
+        } else {
+            dst[lane] = x0;
+            dst[lane + HALF] = x1;
+        }
+    }
+    __syncthreads();
+    // Scores: row r0 + sr, dims [sj * DPL, + DPL); the row at pos is the new key.
+    const long long row = r0 + sr;
+    const bool fresh = row == pos;
+    float sc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NKL; ++i) {
+        float kf[EPV];
+        if (EPV == 8) {
+            unpack8(kr[i], kf);
+        } else {
+            kf[0] = __uint_as_float(kr[i].x);
+            kf[1] = __uint_as_float(kr[i].y);
+            kf[2] = __uint_as_float(kr[i].z);
+            kf[3] = __uint_as_float(kr[i].w);
+        }
+        const int c = (i * LPR + sj) * EPV;  // first dim of the chunk
+        if (fresh) {
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) kf[e] = hk[c + e];
+        }
+        const float *qs = hq + c;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) sc = fmaf(qs[e], kf[e], sc);
+    }
+    sc += dpp_get<0xB1>(sc, 0.f);                // quad_perm [1,0,3,2]
+    if (LPR == 4) sc += dpp_get<0x4E>(sc, 0.f);  // quad_perm [2,3,0,1]
+    const bool valid = row < len;
+    const float s = valid ? sc * (1.0f / sqrtf((float)HD)) : -INFINITY;
+    // Softmax statistics of the wave's rows.
+    const float m = wave_max_dpp(s);
+    const float p = valid ? expf(s - m) : 0.f;  // m is finite when any row is valid
+    const float l = wave_sum_dpp(sj == 0 ? p : 0.f);
+    // P.V: dims 2 lane, 2 lane + 1; the row at pos is the new value. Rows
+    // past the context hold stale bits (NaN among them): skipped, not weighted
+    // by 0.
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        if (r0 + r >= len) break;  // uniform over the wave
+        const float pr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r * LPR));
+        float2 v = VPair<KV>::get(vr[r]);
+        if (r0 + r == pos) v = make_float2(hv[2 * lane], hv[2 * lane + 1]);
+        acc0 = fmaf(pr, v.x, acc0);
+        acc1 = fmaf(pr, v.y, acc1);
+    }
+    pacc[wave][2 * lane] = acc0;
+    pacc[wave][2 * lane + 1] = acc1;
+    if (lane == 0) {
+        pm[wave] = m;
+        pl[wave] = l;
+    }
+    // The group's first head appends the new key and value (model.rs:119-120);
+    // no block of this launch reads that position from the caches.
+    if (append && wave == 0 && pos >= s0 && pos < s0 + ROWS) {
+        store_kv(const_cast<KV *>(kc) + pos * HD + lane, hk[lane]);
+        store_kv(const_cast<KV *>(kc) + pos * HD + lane + HALF, hk[lane + HALF]);
+        store_kv(const_cast<KV *>(vc) + pos * HD + lane, hv[lane]);
+        store_kv(const_cast<KV *>(vc) + pos * HD + lane + HALF, hv[lane + HALF]);
+    }
+    __syncthreads();
+    if (tid < HD) {
+        // Merge the waves in order (a wave with no row in the context adds nothing).
+        const float mx = fmaxf(fmaxf(pm[0], pm[1]), fmaxf(pm[2], pm[3]));
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float e = pm[w] == -INFINITY ? 0.f : expf(pm[w] - mx);
+            num = fmaf(pacc[w][tid], e, num);
+            den = fmaf(pl[w], e, den);
+        }
+        const int n_live = (int)((len + ROWS - 1) / ROWS);
+        chunk_finish(a, h, tid, num, mx, den, xw, n_chunks, split, n_live, epoch, err);
     }
 }
 
