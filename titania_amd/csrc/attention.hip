@@ -20,7 +20,7 @@ namespace th {
 
 constexpr int kAttnMaxGroup = 8;   // query heads per KV head
 constexpr int kAttnSub = 256;      // positions scored per sub-chunk
-constexpr size_t kAttnTileMin = 8; // tokens from which a launch uses the query-tiled kernel
+constexpr size_t kAttnTileMin = 8; // tokens from which a launch uses the matrix-core kernel
 constexpr size_t kMKTiles = 32;    // positions per key tile of that kernel
 
 template <typename KV>
@@ -324,144 +324,26 @@ hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc,
     return hipGetLastError();
 }
 
-// Prefill (several tokens, head_dim 128): one block per (tile of QT
-// consecutive tokens, query head). The block stages the tile's queries once and
-// walks the KV head's positions in tiles of KT rows staged in LDS, so each key
-// and value row is read once per query tile rather than once per token. Thread
-// t scores key t % 32 against queries 4 (t / 32) .. +3, the 32 lanes of a
-// half-wave that share those queries reduce the row statistics with shuffles
-// (online softmax, the causal mask per query), and the same thread then
-// accumulates dims 4 (t % 32) .. +3 of those queries' outputs. All arithmetic
-// is f32.
-constexpr int kQT = 32, kKT = 32;
-
 __device__ __forceinline__ float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ float4 load4(const uint16_t *p) {
     const uint2 w = *reinterpret_cast<const uint2 *>(p);
     return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
 }
 
-template <typename KV>
-__global__ __launch_bounds__(256) void attn_tile_kernel(AttnKernelArgs a, int n) {
-    constexpr int HD = 128, QS = HD + 4;  // padded row stride of the Q and K tiles
-    __shared__ float qs[kQT * QS];
-    __shared__ float ks[kKT * QS];
-    __shared__ float vs[kKT * HD];
-    __shared__ float ps[kQT * kKT];
-    const int tid = threadIdx.x;
-    const int h = blockIdx.y, g = h / a.group;
-    const int t0 = blockIdx.x * kQT;
-    const int nq = n - t0 < kQT ? n - t0 : kQT;
-    const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
-    for (int i = tid; i < kQT * HD / 4; i += 256) {
-        const int row = i / (HD / 4), c4 = i % (HD / 4);
-        const float4 v = row < nq ? load4(a.q + ((long long)(t0 + row) * a.n_heads + h) * HD + c4 * 4)
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4 *>(qs + row * QS + c4 * 4) = v;
-    }
-    const KV *kb = reinterpret_cast<const KV *>(a.k) + (long long)g * a.head_stride;
-    const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
-    const int j = tid & 31, qi0 = (tid >> 5) * 4, d0 = (tid & 31) * 4;
-    float m[4], l[4], acc[4][4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        m[q] = -INFINITY;
-        l[q] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[q][e] = 0.f;
-    }
-    const long long last = pos + t0 + nq - 1;  // the last position a query of the tile attends
-    // Key/value rows travel through registers one tile ahead: the loads of
-    // tile c0 + KT are in flight while tile c0 is scored.
-    constexpr int PER = kKT * HD / 4 / 256;  // float4 of K (and of V) per thread per tile
-    float4 kr4[PER], vr4[PER];
-    auto fetch = [&](long long c0) {
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
-            const long long p = c0 + row;
-            kr4[u] = vr4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (p <= last) {
-                kr4[u] = load4(kb + p * a.pos_stride + c4 * 4);
-                vr4[u] = load4(vb + p * a.pos_stride + c4 * 4);
-            }
-        }
-    };
-    fetch(0);
-    for (long long c0 = 0; c0 <= last; c0 += kKT) {
-        __syncthreads();  // the previous tile's rows are consumed (and the queries stored)
-#pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
-            *reinterpret_cast<float4 *>(ks + row * QS + c4 * 4) = kr4[u];
-            *reinterpret_cast<float4 *>(vs + row * HD + c4 * 4) = vr4[u];
-        }
-        __syncthreads();
-        if (c0 + kKT <= last) fetch(c0 + kKT);
-        float sc[4] = {0.f, 0.f, 0.f, 0.f};
-        const float *kr = ks + j * QS;
-#pragma unroll 8
-        for (int c = 0; c < HD; c += 4) {
-            const float4 kk = *reinterpret_cast<const float4 *>(kr + c);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float4 qv = *reinterpret_cast<const float4 *>(qs + (qi0 + q) * QS + c);
-                sc[q] = fmaf(qv.x, kk.x, sc[q]);
-                sc[q] = fmaf(qv.y, kk.y, sc[q]);
-                sc[q] = fmaf(qv.z, kk.z, sc[q]);
-                sc[q] = fmaf(qv.w, kk.w, sc[q]);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const long long qp = pos + t0 + qi0 + q;  // the query's position
-            const bool valid = qi0 + q < nq && c0 + j <= qp;
-            const float sv = valid ? a.scale * sc[q] : -INFINITY;
-            float mx = sv;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
-            const float mn = fmaxf(m[q], mx);
-            const float pv = sv == -INFINITY ? 0.f : expf(sv - mn);
-            float sum = pv;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
-            const float al = m[q] == -INFINITY ? 0.f : expf(m[q] - mn);
-            l[q] = l[q] * al + sum;
-            m[q] = mn;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[q][e] *= al;
-            ps[(qi0 + q) * kKT + j] = pv;
-        }
-        __syncthreads();
-#pragma unroll 4
-        for (int jj = 0; jj < kKT; ++jj) {
-            const float4 v4 = *reinterpret_cast<const float4 *>(vs + jj * HD + d0);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float pj = ps[(qi0 + q) * kKT + jj];
-                acc[q][0] = fmaf(pj, v4.x, acc[q][0]);
-                acc[q][1] = fmaf(pj, v4.y, acc[q][1]);
-                acc[q][2] = fmaf(pj, v4.z, acc[q][2]);
-                acc[q][3] = fmaf(pj, v4.w, acc[q][3]);
-            }
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        if (qi0 + q < nq) {
-            float4 o = make_float4(acc[q][0] / l[q], acc[q][1] / l[q], acc[q][2] / l[q], acc[q][3] / l[q]);
-            *reinterpret_cast<float4 *>(a.out + ((long long)(t0 + qi0 + q) * a.n_heads + h) * HD + d0) = o;
-        }
-}
-
-// Prefill on the matrix cores (head_dim 128): one block per (tile of 64
-// consecutive tokens, query head), 16 tokens per wave. Key/value rows walk
-// through LDS 32 positions at a time (loaded one tile ahead, as f32); each
-// wave forms S = Q K^T for its 16 queries with v_mfma_f32_16x16x4f32 (f32
-// products, f32 sums), applies the causal mask and the online softmax along
-// its 16-lane rows, passes P through LDS into the A-operand layout and adds
-// P V into 16 x 128 f32 accumulators. Layout of 16x16x4 (checked on the GPU):
-// lane l holds A[l%16][l/16] and B[l/16][l%16], and D[4(l/16)+e][l%16].
+// Prefill on the matrix cores (head_dim 128): a flash attention with one
+// block per (tile of 64 consecutive tokens, query head, key split), 16 tokens
+// per wave. Key/value rows walk through LDS 32 positions at a time (loaded
+// into registers one tile ahead). Each wave forms S = Q K^T for its 16
+// queries, applies the causal mask and the online softmax along its 16-lane
+// rows, passes P through LDS into the A-operand layout and adds P V into
+// 16 x 128 f32 accumulators. The products run on v_mfma_f32_16x16x32_bf16:
+// every f32 operand is split into bf16 terms x = hi + lo (split_bf16; q and
+// the probabilities always, an f32 cache's keys and values too; a bf16 cache
+// is exact in hi) and a product is the sum of the hi*hi, hi*lo and lo*hi
+// terms (relative error ~2^-16), accumulated in f32. Keys are staged in LDS
+// as bf16 rows, values transposed (dimension x key) so that a lane's eight
+// keys of one dimension are one 16-byte read. Layout of 16x16x32: lane l
+// holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16] and D[4(l/16)+e][l%16].
 constexpr int kMQT = 64, kMKT = (int)kMKTiles;
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -473,32 +355,55 @@ __device__ __forceinline__ float row_max16(float v) {
     return v;
 }
 
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+
+__device__ __forceinline__ void split8(const float *f, uint4 &hi, uint4 &lo) {
+    uint2 h0, l0, h1, l1;
+    split_bf16x4(make_float4(f[0], f[1], f[2], f[3]), h0, l0);
+    split_bf16x4(make_float4(f[4], f[5], f[6], f[7]), h1, l1);
+    hi = make_uint4(h0.x, h0.y, h1.x, h1.y);
+    lo = make_uint4(l0.x, l0.y, l1.x, l1.y);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf8(const uint4 &v) { return __builtin_bit_cast(bf16x8_t, v); }
+
 template <typename KV>
-__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n) {
-    constexpr int HD = 128, KS = HD + 4, VS = HD + 16, PS = kMKT + 4;  // LDS row strides (floats)
-    __shared__ float ks[kMKT * KS];
-    __shared__ float vs[kMKT * VS];
-    __shared__ float ps[4][16 * PS];
+__global__ __launch_bounds__(256) void attn_bf16_kernel(AttnKernelArgs a, int n) {
+    constexpr bool F32 = sizeof(KV) == 4;
+    constexpr int HD = 128, KT = kMKT;                       // dims, keys per tile
+    constexpr int KSB = HD + 8, VTS = KT + 8, PS = KT + 4;   // LDS row strides (bf16, bf16, f32)
+    __shared__ uint4 ksh[KT * KSB / 8], ksl[F32 ? KT * KSB / 8 : 1];
+    __shared__ uint4 vth[HD * VTS / 8], vtl[F32 ? HD * VTS / 8 : 1];
+    __shared__ __align__(16) float ps[4][16 * PS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lk = lane >> 4;
     const int h = blockIdx.y, g = h / a.group;
     const int t0 = blockIdx.x * kMQT;
     const int nq = n - t0 < kMQT ? n - t0 : kMQT;
     const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
-    // Q in the A-operand layout: qa[k] = Q[query li of the wave][4k + lk].
+    // Q of query li of the wave, dims 32 c + 8 lk + [0, 8), as bf16 hi / lo.
     const int tq = t0 + wave * 16 + li;
-    float qa[HD / 4];
+    uint4 qh[HD / 32], ql[HD / 32];
     {
-        const float *qp = a.q + ((long long)(tq < n ? tq : 0) * a.n_heads + h) * HD + lk;
+        const float *qp = a.q + ((long long)(tq < n ? tq : 0) * a.n_heads + h) * HD + 8 * lk;
 #pragma unroll
-        for (int k = 0; k < HD / 4; ++k) qa[k] = tq < n ? qp[4 * k] : 0.f;
+        for (int c = 0; c < HD / 32; ++c) {
+            float f[8];
+            const float4 x0 = *reinterpret_cast<const float4 *>(qp + 32 * c);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qp + 32 * c + 4);
+            f[0] = x0.x; f[1] = x0.y; f[2] = x0.z; f[3] = x0.w;
+            f[4] = x1.x; f[5] = x1.y; f[6] = x1.z; f[7] = x1.w;
+            if (tq >= n)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = 0.f;
+            split8(f, qh[c], ql[c]);
+        }
     }
     const KV *kb = reinterpret_cast<const KV *>(a.k) + (long long)g * a.head_stride;
     const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
-    const long long last = pos + t0 + nq - 1;                       // the block's last query position
-    const long long wlast = pos + t0 + wave * 16 + 15;              // this wave's last query position
-    // Key split z of a.nsplit: key tiles [kt0, kt1) of the block's range.
-    const long long ntiles = last / kMKT + 1, z = blockIdx.z;
+    const long long last = pos + t0 + nq - 1;           // the block's last query position
+    const long long wlast = pos + t0 + wave * 16 + 15;  // this wave's last query position
+    const long long ntiles = last / KT + 1, z = blockIdx.z;
     const long long kt0 = z * ntiles / a.nsplit, kt1 = (z + 1) * ntiles / a.nsplit;
     floatx4 o[HD / 16];
     float m[4], l[4];
@@ -509,40 +414,77 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
         m[r] = -INFINITY;
         l[r] = 0.f;
     }
-    constexpr int PER = kMKT * HD / 4 / 256;  // float4 of K (and of V) per thread per tile
-    float4 kr4[PER], vr4[PER];
+    // Staging: thread t loads key t / 8, dims 16 (t % 8) + [0, 16) of K, and
+    // keys 8 (t / 64) + [0, 8) of V at dims 2 (t % 64), + 1 (each load
+    // instruction of a wave reads consecutive bytes of a row). Positions past
+    // the block's last query read as 0.
+    const int kkey = tid / 8, kd0 = (tid % 8) * 16, vd = 2 * (tid % 64), vk0 = 8 * (tid / 64);
+    float kraw[16], vraw[8][2];
     auto fetch = [&](long long c0) {
+        const long long pk = c0 + kkey;
 #pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
-            const long long p = c0 + row;
-            kr4[u] = vr4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (p <= last) {
-                kr4[u] = load4(kb + p * a.pos_stride + c4 * 4);
-                vr4[u] = load4(vb + p * a.pos_stride + c4 * 4);
+        for (int e = 0; e < 16; e += 4) {
+            const float4 x = pk <= last ? load4(kb + pk * a.pos_stride + kd0 + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            kraw[e] = x.x; kraw[e + 1] = x.y; kraw[e + 2] = x.z; kraw[e + 3] = x.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const long long pv = c0 + vk0 + j;
+            float2 v = make_float2(0.f, 0.f);
+            if (pv <= last) {
+                if (F32) {
+                    v = *reinterpret_cast<const float2 *>(reinterpret_cast<const float *>(vb) + pv * a.pos_stride + vd);
+                } else {
+                    const uint32_t w =
+                        *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(vb) + pv * a.pos_stride + vd);
+                    v = make_float2(bf16_lo(w), bf16_hi(w));
+                }
             }
+            vraw[j][0] = v.x;
+            vraw[j][1] = v.y;
         }
     };
-    const long long cend = kt1 * kMKT;  // positions [kt0 kMKT, cend) of this split
-    if (kt0 < kt1) fetch(kt0 * kMKT);
-    for (long long c0 = kt0 * kMKT; c0 < cend; c0 += kMKT) {
+    const long long cend = kt1 * KT;
+    if (kt0 < kt1) fetch(kt0 * KT);
+    for (long long c0 = kt0 * KT; c0 < cend; c0 += KT) {
         __syncthreads();  // the previous tile is consumed
+        {
+            uint4 hi, lo;
 #pragma unroll
-        for (int u = 0; u < PER; ++u) {
-            const int i = tid + u * 256, row = i / (HD / 4), c4 = i % (HD / 4);
-            *reinterpret_cast<float4 *>(ks + row * KS + c4 * 4) = kr4[u];
-            *reinterpret_cast<float4 *>(vs + row * VS + c4 * 4) = vr4[u];
+            for (int e = 0; e < 16; e += 8) {
+                split8(kraw + e, hi, lo);
+                ksh[(kkey * KSB + kd0 + e) / 8] = hi;
+                if (F32) ksl[(kkey * KSB + kd0 + e) / 8] = lo;
+            }
+#pragma unroll
+            for (int dd = 0; dd < 2; ++dd) {
+                float f[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) f[j] = vraw[j][dd];
+                split8(f, hi, lo);
+                vth[((vd + dd) * VTS + vk0) / 8] = hi;
+                if (F32) vtl[((vd + dd) * VTS + vk0) / 8] = lo;
+            }
         }
         __syncthreads();
-        if (c0 + kMKT < cend) fetch(c0 + kMKT);
+        if (c0 + KT < cend) fetch(c0 + KT);
         if (c0 > wlast) continue;  // every query of this wave precedes the tile
         // S for keys c0 + [0, 16) and c0 + [16, 32).
         floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < HD / 4; ++k) {
-            const float b0 = ks[li * KS + 4 * k + lk], b1 = ks[(16 + li) * KS + 4 * k + lk];
-            s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[k], b0, s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[k], b1, s1, 0, 0, 0);
+        for (int c = 0; c < HD / 32; ++c) {
+            const int off = 32 * c + 8 * lk;
+            const bf16x8_t qhc = as_bf8(qh[c]), qlc = as_bf8(ql[c]);
+            const bf16x8_t k0 = as_bf8(ksh[(li * KSB + off) / 8]), k1 = as_bf8(ksh[((16 + li) * KSB + off) / 8]);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhc, k0, s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhc, k1, s1, 0, 0, 0);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qlc, k0, s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qlc, k1, s1, 0, 0, 0);
+            if (F32) {
+                const bf16x8_t k0l = as_bf8(ksl[(li * KSB + off) / 8]), k1l = as_bf8(ksl[((16 + li) * KSB + off) / 8]);
+                s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhc, k0l, s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhc, k1l, s1, 0, 0, 0);
+            }
         }
         // Causal mask and online softmax of rows 4 lk + r (this lane: keys li, 16 + li).
         float al[4];
@@ -566,19 +508,27 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
         for (int d = 0; d < HD / 16; ++d)
 #pragma unroll
             for (int r = 0; r < 4; ++r) o[d][r] *= al[r];
-        // P back in the A-operand layout (same wave: LDS stays in order).
+        // P in the A-operand layout: query li, keys 8 lk + [0, 8) (same wave:
+        // LDS stays in order).
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float pa[kMKT / 4];
+        uint4 ph, pl;
+        {
+            const float4 x0 = *reinterpret_cast<const float4 *>(&ps[wave][li * PS + 8 * lk]);
+            const float4 x1 = *reinterpret_cast<const float4 *>(&ps[wave][li * PS + 8 * lk + 4]);
+            const float f[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            split8(f, ph, pl);
+        }
+        const bf16x8_t pha = as_bf8(ph), pla = as_bf8(pl);
 #pragma unroll
-        for (int kk = 0; kk < kMKT / 4; ++kk) pa[kk] = ps[wave][li * PS + 4 * kk + lk];
-#pragma unroll
-        for (int kk = 0; kk < kMKT / 4; ++kk)
-#pragma unroll
-            for (int d = 0; d < HD / 16; ++d)
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[kk], vs[(4 * kk + lk) * VS + d * 16 + li], o[d], 0,
-                                                            0, 0);
+        for (int d = 0; d < HD / 16; ++d) {
+            const int vo = ((d * 16 + li) * VTS + 8 * lk) / 8;
+            const bf16x8_t vh = as_bf8(vth[vo]);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pha, vh, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pla, vh, o[d], 0, 0, 0);
+            if (F32) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pha, as_bf8(vtl[vo]), o[d], 0, 0, 0);
+        }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -594,8 +544,6 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(AttnKernelArgs a, int n)
 #pragma unroll
             for (int d = 0; d < HD / 16; ++d) op[d * 16] = o[d][r] / l[r];
         } else {
-            // Unnormalised sum, max and denominator for launch_attn_combine
-            // (a split with no key of this query leaves m = -inf).
             const long long slot = th * a.nsplit + z;
             float *op = a.part_acc + slot * HD + li;
 #pragma unroll
@@ -627,9 +575,9 @@ hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, si
     if (head_dim == 128 && n >= kAttnTileMin) {
         dim3 grid((unsigned)((n + kMQT - 1) / kMQT), (unsigned)k.n_heads, (unsigned)k.nsplit);
         if (k.kv_bf16)
-            attn_mfma_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
+            attn_bf16_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
         else
-            attn_mfma_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
+            attn_bf16_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || k.nsplit == 1) return e;
         return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128, k.out_hi,
