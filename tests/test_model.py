@@ -70,6 +70,24 @@ def test_tiny_decode(tiny, kv):
     st.close()
 
 
+@pytest.mark.parametrize("kv", [TH_KV_F32, TH_KV_BF16])
+def test_tiny_decode_large_cache(tiny, kv):
+    """A state far larger than its context (1024 positions, 9 + 20 used): the
+    attention chunks past the context leave at once and the result is the
+    oracle's, as with a state of just the right size."""
+    m, r = tiny
+    c = QWEN3_TINY
+    prompt = synth.prompt(9, c.vocab_size, seed=6)
+    st = State(m, 1024, kv)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    toks, logits = m.decode(st, len(prompt), 20, keep_logits=True)
+    rtoks, gaps, last = r.generate(r.state(1024), prompt, 20)
+    tol = 1e-4 if kv == TH_KV_F32 else LOGIT_TOL
+    assert np.max(np.abs(logits[-1] - last)) <= tol
+    assert list(toks) == list(rtoks) or np.min(gaps) < tol
+    st.close()
+
+
 def test_paths_refuse_to_mix(tiny):
     m, _ = tiny
     st = State(m, 32)
@@ -334,25 +352,27 @@ def test_qwen4b_bf16_cache_drift(qwen4b):
 
 # ---- sampled decode (model/chat.rs:149-178 with model/sampler.rs) ----
 
-@pytest.mark.parametrize("t,k,p", [(0.7, 20, 0.8), (1.5, 256, 1.0), (0.9, 40, 0.9)])
-def test_tiny_decode_sampled(tiny, t, k, p):
+@pytest.mark.parametrize("t,k,p,n_prompt", [(0.7, 20, 0.8, 12), (1.5, 256, 1.0, 12), (0.9, 40, 0.9, 12),
+                                           (0.8, 30, 0.95, 170)])
+def test_tiny_decode_sampled(tiny, t, k, p, n_prompt):
     """Draws on the device across a decode, against the oracle's chat-style
     loop; a second call continues the generator where the first left it, and
     a greedy decode on the same state afterwards is unaffected. f32 caches:
-    bf16 caches move the logits by up to ~2e-2, enough to move draws."""
+    bf16 caches move the logits by up to ~2e-2, enough to move draws. The
+    170-token prompt puts the decode in several 64-position attention chunks."""
     kv = TH_KV_F32
     m, r = tiny
     c = QWEN3_TINY
-    prompt = synth.prompt(12, c.vocab_size, seed=5)
-    st = State(m, 12 + 40 + 8, kv)
+    prompt = synth.prompt(n_prompt, c.vocab_size, seed=5)
+    st = State(m, n_prompt + 40 + 8, kv)
     m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
     dev = Sampler(t, k, p, 1234)
-    got = list(m.decode(st, 12, 24, sampler=dev)) + list(m.decode(st, 36, 16, sampler=dev))
+    got = list(m.decode(st, n_prompt, 24, sampler=dev)) + list(m.decode(st, n_prompt + 24, 16, sampler=dev))
     cpu = ref.Sampler(t, k, p, 1234)
-    exp = list(r.generate_sampled(r.state(12 + 40 + 8), prompt, 40, cpu))
+    exp = list(r.generate_sampled(r.state(n_prompt + 40 + 8), prompt, 40, cpu))
     assert got == exp
     assert dev.rng == cpu.state
-    more = m.decode(st, 52, 4)
+    more = m.decode(st, n_prompt + 40, 4)
     assert len(more) == 4
     st.close()
 
