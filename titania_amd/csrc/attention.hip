@@ -218,22 +218,24 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__
     if (lane == 0) red[wave] = l;
     __syncthreads();
     l = ((red[0] + red[1]) + red[2]) + red[3];
-    // groups of splits per dimension: thread t takes dimension t % hd of the
-    // splits s = t / hd, + groups, ...
-    const int groups = hd < kCombineThreads ? kCombineThreads / hd : 1;
-    for (int d0 = 0; d0 < hd; d0 += kCombineThreads) {
-        const int d = d0 + tid % hd, grp = tid / hd;
+    // This block's dimensions [dlo, dlo + dw) (gridDim.y blocks share a
+    // head), in groups of splits: thread t takes dimension dlo + t % dw of
+    // the splits s = t / dw, + groups, ...
+    const int dw = hd / (int)gridDim.y, dlo = (int)blockIdx.y * dw;
+    const int groups = dw < kCombineThreads ? kCombineThreads / dw : 1;
+    for (int d0 = 0; d0 < dw; d0 += kCombineThreads) {
+        const int dd = d0 + tid % dw, grp = tid / dw, d = dlo + dd;
         float acc = 0.f;
-        if (d < hd && grp < groups) {
+        if (dd < dw && grp < groups) {
             const float *pa = part_acc + th * nsplit * hd + d;
 #pragma unroll 8
             for (int s = grp; s < nsplit; s += groups) acc += pa[(size_t)s * hd] * w[s];
         }
         acc_red[tid] = acc;
         __syncthreads();
-        if (grp == 0 && d < hd) {
+        if (grp == 0 && dd < dw) {
             float sum = 0.f;
-            for (int gi = 0; gi < groups; ++gi) sum += acc_red[gi * hd + tid % hd];
+            for (int gi = 0; gi < groups; ++gi) sum += acc_red[gi * dw + tid % dw];
             if (hi)
                 split_bf16(sum / l, hi[th * hd + d], lo[th * hd + d]);
             else
@@ -319,8 +321,12 @@ hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc,
         }
         return hipGetLastError();
     }
-    attn_combine_kernel<<<dim3((unsigned)heads), dim3(kCombineThreads), 0, s>>>(out, part_acc, part_ml, nsplit, hd,
-                                                                                hi, lo);
+    // Few (token, head) pairs (decode): their dimensions spread over several
+    // blocks each, at least 16 a block, so that the launch fills the chip.
+    unsigned ysplit = 1;
+    while (heads * ysplit < 256 && hd % (int)(ysplit * 2) == 0 && hd / (int)(ysplit * 2) >= 16) ysplit *= 2;
+    attn_combine_kernel<<<dim3((unsigned)heads, ysplit), dim3(kCombineThreads), 0, s>>>(out, part_acc, part_ml,
+                                                                                         nsplit, hd, hi, lo);
     return hipGetLastError();
 }
 
