@@ -8,12 +8,14 @@
 // (two v_mfma_f32_16x16x32_bf16 per fragment pair, f32 accumulation). A plain
 // bf16 rounding of x would leave ~1e-3 relative error in every output.
 //
-// Tiling: a 256-thread block computes 64 tokens x 64 weight rows; each of its
-// four waves a 32 x 32 quarter (2 x 2 MFMA tiles of 16 x 16). K advances 64 at
-// a time through a ring of kStages LDS stages (hi, lo and weight tiles, 24 KB
-// each, so two blocks fit a CU) that the block fills with direct global->LDS
-// loads (global_load_lds, 16 bytes a lane) kStages - 1 steps ahead of the step
-// being multiplied. Rows of every tile are XOR-swizzled in 16-byte chunks so
+// Tiling: a 256-thread block computes 64 tokens x 64 weight rows (the small
+// tile; each of its four waves a 32 x 32 quarter, 2 x 2 MFMA tiles of 16 x 16)
+// or, in launches of many tiles, 128 x 128 (the large tile, 4 x 4 MFMA tiles a
+// wave). K advances 64 at a time through a ring of 3 LDS stages (hi, lo and
+// weight tiles: 24 KB a stage for the small tile, so two blocks fit a CU;
+// 48 KB for the large tile, one block a CU) that the block fills with direct
+// global->LDS loads (global_load_lds, 16 bytes a lane) two steps ahead of the
+// step being multiplied. Rows of every tile are XOR-swizzled in 16-byte chunks so
 // that the 16 rows a fragment read touches land on distinct banks: the lane
 // that writes physical chunk p of row r fetches logical chunk p ^ swizzle(r).
 // One launch may cover several weight matrices that share the input (q, k and
@@ -28,17 +30,25 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
-constexpr int BM = 64, BN = 64, BK = 64;  // tokens, weight rows, columns per step
 constexpr int NTHR = 256;
-constexpr int kStages = 3;
+constexpr int BK = 64;                    // columns per K step
 constexpr int CH = BK / 8;                // 16-byte chunks per tile row (bf16)
-constexpr int TILE = BM * CH;             // 512 chunks per tile
-constexpr int DMA_PER_WAVE = 3 * TILE / NTHR;  // 6 instructions per wave per step
 
-struct alignas(16) Stage {
-    uint4 hi[TILE], lo[TILE];  // [BM][CH] activation halves
-    uint4 w[TILE];             // [BN][CH] weights
+// A block tile of BM tokens x BN weight rows, its four waves each a
+// BM/2 x BN/2 quarter, K staged through `STAGES` LDS stages.
+template <int BM_, int BN_, int STAGES_>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, kStages = STAGES_;
+    static constexpr int TA = BM * CH, TB = BN * CH;     // 16-byte chunks per tile
+    static constexpr int FM = BM / 32, FN = BN / 32;     // 16 x 16 fragments per wave
+    static constexpr int DMA_PER_WAVE = (2 * TA + TB) / NTHR;
+    struct alignas(16) Stage {
+        uint4 hi[TA], lo[TA];  // [BM][CH] activation halves
+        uint4 w[TB];           // [BN][CH] weights
+    };
 };
+using Small = Tile<64, 64, 3>;    // 24 KB a stage: two blocks a CU
+using Large = Tile<128, 128, 3>;  // 48 KB a stage: one block a CU
 
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & (CH - 1); }
 
@@ -53,6 +63,21 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
+// The block barrier of the K loop. __syncthreads() would also wait for every
+// load still in flight (its workgroup fence covers the LDS writes of
+// global_load_lds, even with the fence narrowed to LDS), the later stages'
+// too, leaving one step of the ring in flight instead of two. Each wave has
+// already waited for its own loads of the step about to be read (vmcnt counts
+// a global_load_lds until its LDS write is done) and has consumed its reads
+// of the stage about to be refilled (its MFMAs used them), so the hardware
+// barrier alone orders both; the signal fences keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void stage_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Up to three weight matrices of `cols` columns, rows concatenated.
 struct Segs {
     const uint16_t *w[3];
@@ -61,29 +86,17 @@ struct Segs {
     int n;
 };
 
-// The row tile r0 (a multiple of BN) of the concatenation: its matrix and local row.
-__device__ __forceinline__ int seg_of(const Segs &s, int r0, int &local) {
-    if (r0 < s.rows[0]) {
-        local = r0;
-        return 0;
-    }
-    if (r0 < s.rows[0] + s.rows[1]) {
-        local = r0 - s.rows[0];
-        return 1;
-    }
-    local = r0 - s.rows[0] - s.rows[1];
-    return 2;
-}
-
 // Queues the loads of K step k0 into stage st: each wave fills whole 1 KB
-// spans (64 lanes x 16 B) of the stage, two of each tile. Token rows past n
-// read row n - 1 (their results are never stored).
-__device__ __forceinline__ void issue_step(Stage &st, const uint16_t *hi, const uint16_t *lo, const uint16_t *w,
-                                           int t0, int n, int cols, int k0) {
+// spans (64 lanes x 16 B) of the stage. Token rows past n read row n - 1
+// (their results are never stored).
+template <class T>
+__device__ __forceinline__ void issue_step(typename T::Stage &st, const uint16_t *hi, const uint16_t *lo,
+                                           const uint16_t *w, int t0, int n, int cols, int k0) {
+    static_assert(T::TA == T::TB, "square tiles: one span of each tile per iteration");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < TILE / NTHR; ++i) {
-        const int span = wave * (TILE / NTHR) + i;
+    for (int i = 0; i < T::TA / NTHR; ++i) {
+        const int span = wave * (T::TA / NTHR) + i;
         const int p = span * 64 + lane, row = p / CH, pc = p % CH;
         const int t = min(t0 + row, n - 1);
         const size_t off = (size_t)t * cols + k0 + (pc ^ swz(row)) * 8;
@@ -97,77 +110,107 @@ __device__ __forceinline__ bf16x8 frag(const uint4 *tile, int row, int lc) {
     return __builtin_bit_cast(bf16x8, tile[row * CH + (lc ^ swz(row))]);
 }
 
+// The matrix that the row tile r0 of the concatenation falls in: its weights
+// from its local row, output, row count and local row. Selected without
+// indexing the argument arrays by a run-time value, which would copy them to
+// scratch memory.
+struct SegTile {
+    const uint16_t *w;
+    float *out;
+    int rows, local;
+};
+
+__device__ __forceinline__ SegTile seg_tile(const Segs &s, int r0) {
+    const int n0 = s.rows[0], n1 = s.rows[1];
+    if (r0 < n0) return SegTile{s.w[0], s.out[0], n0, r0};
+    if (r0 < n0 + n1) return SegTile{s.w[1], s.out[1], n1, r0 - n0};
+    return SegTile{s.w[2], s.out[2], s.rows[2], r0 - n0 - n1};
+}
+
 // With ksplit > 1 (one matrix), block z of the grid's third dimension takes
 // K steps [z nk / ksplit, (z + 1) nk / ksplit) and stores its partial tile in
-// part[z][t][r]; launch_gemm_multi then sums the partials in z order.
-__global__ __launch_bounds__(NTHR, 2) void gemm_kernel(Segs sg, const uint16_t *__restrict__ hi,
-                                                        const uint16_t *__restrict__ lo, int n, int cols,
-                                                        float *__restrict__ part, int ksplit) {
-    __shared__ Stage ring[kStages];
+// part[z][t][r]; the consumer sums the partials in z order.
+template <class T>
+__device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict__ hi,
+                                          const uint16_t *__restrict__ lo, int n, int cols,
+                                          float *__restrict__ part, int ksplit) {
+    constexpr int FM = T::FM, FN = T::FN, kStages = T::kStages;
+    __shared__ typename T::Stage ring[kStages];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * BM;
-    int rl;
-    const int sgi = seg_of(sg, blockIdx.x * BN, rl);
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int t0 = blockIdx.y * T::BM;
+    const int rl = sg.local;
+    const int wm = (wave >> 1) * (T::BM / 2), wn = (wave & 1) * (T::BN / 2);
     const int fr = lane & 15, fq = lane >> 4;  // fragment row, quarter of the K slice
     const int nk_all = cols / BK, z = blockIdx.z;
     const int kb = (int)((long long)z * nk_all / ksplit), nk = (int)((long long)(z + 1) * nk_all / ksplit) - kb;
-    const uint16_t *w = sg.w[sgi] + (size_t)rl * cols + (size_t)kb * BK;
+    const uint16_t *w = sg.w + (size_t)rl * cols + (size_t)kb * BK;
     hi += (size_t)kb * BK;
     lo += (size_t)kb * BK;
 
-    f32x4 acc[2][2];
+    f32x4 acc[FM][FN];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < FM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s)
-        if (s < nk) issue_step(ring[s], hi, lo, w, t0, n, cols, s * BK);
+        if (s < nk) issue_step<T>(ring[s], hi, lo, w, t0, n, cols, s * BK);
 
     for (int k = 0; k < nk; ++k) {
         // This wave's loads of step k are done once at most the later steps'
         // loads are outstanding; the barrier makes every wave's visible and
         // frees the stage step k - 1 used.
-        if (k + kStages - 2 < nk) wait_vm<(kStages - 2) * DMA_PER_WAVE>();
+        if (k + kStages - 2 < nk) wait_vm<(kStages - 2) * T::DMA_PER_WAVE>();
         else wait_vm<0>();
-        __syncthreads();
+        stage_barrier();
         if (k + kStages - 1 < nk)
-            issue_step(ring[(k + kStages - 1) % kStages], hi, lo, w, t0, n, cols, (k + kStages - 1) * BK);
-        const Stage &st = ring[k % kStages];
+            issue_step<T>(ring[(k + kStages - 1) % kStages], hi, lo, w, t0, n, cols, (k + kStages - 1) * BK);
+        const typename T::Stage &st = ring[k % kStages];
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ++ks) {
             const int lc = ks * 4 + fq;
-            bf16x8 ah[2], al[2], b[2];
+            bf16x8 ah[FM], al[FM], b[FN];
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
+            for (int m = 0; m < FM; ++m) {
                 ah[m] = frag(st.hi, wm + m * 16 + fr, lc);
                 al[m] = frag(st.lo, wm + m * 16 + fr, lc);
             }
 #pragma unroll
-            for (int q = 0; q < 2; ++q) b[q] = frag(st.w, wn + q * 16 + fr, lc);
+            for (int q = 0; q < FN; ++q) b[q] = frag(st.w, wn + q * 16 + fr, lc);
 #pragma unroll
-            for (int m = 0; m < 2; ++m)
+            for (int m = 0; m < FM; ++m)
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
+                for (int q = 0; q < FN; ++q) {
                     acc[m][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[m], b[q], acc[m][q], 0, 0, 0);
                     acc[m][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[m], b[q], acc[m][q], 0, 0, 0);
                 }
         }
     }
     // D[4 (l / 16) + i][l % 16]: token rows, weight-row columns.
-    const int rows = sg.rows[sgi];
-    float *out = ksplit > 1 ? part + (size_t)z * n * rows : sg.out[sgi];
+    const int rows = sg.rows;
+    float *out = ksplit > 1 ? part + (size_t)z * n * rows : sg.out;
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < FM; ++m)
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+        for (int q = 0; q < FN; ++q)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = t0 + wm + m * 16 + fq * 4 + i;
                 if (t < n) out[(size_t)t * rows + rl + wn + q * 16 + fr] = acc[m][q][i];
             }
+}
+
+__global__ __launch_bounds__(NTHR, 2) void gemm_kernel(Segs sg, const uint16_t *__restrict__ hi,
+                                                        const uint16_t *__restrict__ lo, int n, int cols,
+                                                        float *__restrict__ part, int ksplit) {
+    gemm_tile<Small>(seg_tile(sg, blockIdx.x * Small::BN), hi, lo, n, cols, part, ksplit);
+}
+
+__global__ __launch_bounds__(NTHR, 1) void gemm_large_kernel(Segs sg, const uint16_t *__restrict__ hi,
+                                                              const uint16_t *__restrict__ lo, int n, int cols,
+                                                              float *__restrict__ part, int ksplit) {
+    gemm_tile<Large>(seg_tile(sg, blockIdx.x * Large::BN), hi, lo, n, cols, part, ksplit);
 }
 
 // split_bf16 of 4 elements a thread.
@@ -195,9 +238,31 @@ __global__ void splitk_sum_kernel(const float4 *__restrict__ part, float4 *__res
 }  // namespace
 
 bool gemm_supported(size_t rows, size_t cols) {
-    return rows % BN == 0 && cols % BK == 0 && rows < ((size_t)1 << 24) && cols < ((size_t)1 << 20) &&
+    return rows % Small::BN == 0 && cols % BK == 0 && rows < ((size_t)1 << 24) && cols < ((size_t)1 << 20) &&
            rows * cols < ((size_t)1 << 40);
 }
+
+namespace {
+
+// A launch takes the large tile when it has at least three large tiles a CU
+// (and every matrix's rows are whole large tiles). Fewer leave the last round
+// of one-block-a-CU tiles partly empty, and the small tile, two blocks a CU
+// over four times the grid, finishes first (measured on the Qwen3 prefill
+// shapes: 2048 tokens x 19456 x 2560 607 against 703 us, 512 tokens x 19456 x
+// 2560 203 against 180 us).
+constexpr size_t kLargeMinTiles = 768;
+
+bool use_large(size_t n, const GemmOut *outs, int n_outs, int ksplit) {
+    if (ksplit != 1) return false;
+    size_t total = 0;
+    for (int i = 0; i < n_outs; ++i) {
+        if (outs[i].rows % Large::BN) return false;
+        total += outs[i].rows;
+    }
+    return (total / Large::BN) * ((n + Large::BM - 1) / Large::BM) >= kLargeMinTiles;
+}
+
+}  // namespace
 
 size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows) {
     return n * cols * 2 * sizeof(uint16_t) + (size_t)kGemmMaxSplitK * n * rows * sizeof(float);
@@ -217,7 +282,7 @@ hipError_t launch_gemm_split(hipStream_t s, const float *x, size_t n, size_t col
 // the launch still fills the chip, keeping at least 4 K steps per split.
 int gemm_ksplit(size_t n, size_t rows, size_t cols, int n_outs) {
     if (n_outs != 1) return 1;
-    const size_t tiles = (rows / BN) * ((n + BM - 1) / BM), nk = cols / BK;
+    const size_t tiles = (rows / Small::BN) * ((n + Small::BM - 1) / Small::BM), nk = cols / BK;
     int ksplit = 1;
     while (ksplit < kGemmMaxSplitK && tiles * ksplit < 512 && (size_t)ksplit * 2 * 4 <= nk) ksplit *= 2;
     return ksplit;
@@ -226,8 +291,8 @@ int gemm_ksplit(size_t n, size_t rows, size_t cols, int n_outs) {
 hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
                           const GemmOut *outs, int n_outs, float *part, int ksplit) {
     if (n == 0) return hipSuccess;
-    if (n_outs < 1 || n_outs > 3 || !hi || !lo || (n + BM - 1) / BM > 65535 || n > ((size_t)1 << 24) ||
-        ksplit < 1 || ksplit > kGemmMaxSplitK || (ksplit > 1 && (n_outs != 1 || !part)) ||
+    if (n_outs < 1 || n_outs > 3 || !hi || !lo || (n + Small::BM - 1) / Small::BM > 65535 ||
+        n > ((size_t)1 << 24) || ksplit < 1 || ksplit > kGemmMaxSplitK || (ksplit > 1 && (n_outs != 1 || !part)) ||
         (size_t)ksplit > cols / BK)
         return hipErrorInvalidValue;
     Segs sg{};
@@ -240,9 +305,14 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
         total += outs[i].rows;
     }
     sg.n = n_outs;
-    if (total / BN > 65535) return hipErrorInvalidValue;
-    dim3 grid((unsigned)(total / BN), (unsigned)((n + BM - 1) / BM), (unsigned)ksplit);
-    gemm_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+    if (total / Small::BN > 65535) return hipErrorInvalidValue;
+    if (use_large(n, outs, n_outs, ksplit)) {
+        dim3 grid((unsigned)(total / Large::BN), (unsigned)((n + Large::BM - 1) / Large::BM), 1);
+        gemm_large_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, 1);
+    } else {
+        dim3 grid((unsigned)(total / Small::BN), (unsigned)((n + Small::BM - 1) / Small::BM), (unsigned)ksplit);
+        gemm_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+    }
     return hipGetLastError();
 }
 

@@ -27,7 +27,7 @@
 namespace {
 
 constexpr size_t kBatch = 64;          // model/model.rs:8 BATCH (the ops path)
-constexpr size_t kFusedBatch = 512;    // tokens per chunk on the fused path
+constexpr size_t kFusedBatch = 2048;   // tokens per chunk on the fused path
 constexpr size_t kWeightsPerLayer = 11;
 
 struct Layer {
