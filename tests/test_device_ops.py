@@ -276,10 +276,13 @@ def test_prefill_attention(hip):
     assert_close(hip.read(out), expected, rel=1e-4, abs_=1e-5, what="prefill attention")
 
 
-@pytest.mark.parametrize("n,pos,H,KVH", [(33, 0, 16, 8), (512, 0, 16, 8), (64, 300, 32, 8), (8, 5, 4, 1)])
+@pytest.mark.parametrize("n,pos,H,KVH", [(33, 0, 16, 8), (512, 0, 16, 8), (64, 300, 32, 8), (8, 5, 4, 1),
+                                         (77, 40, 8, 8), (50, 90, 16, 2), (300, 700, 32, 8), (20, 0, 12, 4)])
 def test_prefill_attention_tiles(hip, n, pos, H, KVH):
-    """The query-tiled prefill kernel: a ragged tile, a 512-token prompt, a
-    4-query-head group after a long prefix, the smallest tiled launch."""
+    """The query-tiled prefill kernels: a ragged tile, a 512-token prompt, a
+    4-query-head group after a long prefix, the smallest tiled launch, groups
+    of 1 and 8 query heads, a long prefix split over several blocks, and a
+    group of 3 (not a divisor of 8: the one-head-a-block kernel)."""
     hd = 128
     L = pos + n
     kv = bf16_to_f32(normal_bf16(L * KVH * hd, n, "tk"))

@@ -562,6 +562,302 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(AttnKernelArgs a, int n)
     }
 }
 
+// Prefill attention with the keys and values of a KV group shared by its G
+// query heads: one block per (tile of 128 / G tokens, KV head, key split),
+// 128 (token, head) rows a block, NW waves of 128 / NW rows, each as sets of
+// 16 rows. Keys walk through LDS 64 at a time. Each wave forms S^T = K Q^T
+// (keys down, rows across) on v_mfma_f32_16x16x32_bf16, so that the D layout
+// leaves a lane sixteen keys of one row: the causal mask, the online softmax
+// (base 2, the scale folded with log2 e) and its row reductions (two shuffles
+// across the lane groups) run on the lane's own row, and the probabilities
+// are already the B operand of O^T = V^T P^T, whose D layout again gives a
+// lane four dimensions of its row to rescale. V^T is staged in LDS with the
+// keys of each 32-key slice in the order that layout implies: within a slice,
+// operand position 8 g + i holds key 4 g + i for i < 4 and 16 + 4 g + i - 4
+// otherwise. Operands are split into bf16 hi + lo terms as in
+// attn_bf16_kernel (q and p always; an f32 cache's keys and values too).
+constexpr int kGqaRows = 128, kGqaKeys = 64;
+
+template <typename KV>
+struct GqaShape;
+template <>
+struct GqaShape<uint16_t> {
+    static constexpr int NW = 8;
+};
+template <>
+struct GqaShape<float> {
+    static constexpr int NW = 8;
+};
+
+template <typename KV>
+__global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void attn_gqa_kernel(AttnKernelArgs a, int n) {
+    constexpr bool F32 = sizeof(KV) == 4;
+    constexpr int NW = GqaShape<KV>::NW, NT = 64 * NW, SETS = kGqaRows / 16 / NW, RW = 16 * SETS;
+    constexpr int HD = 128, KT = kGqaKeys;
+    constexpr int KSB = HD + 8;  // K row stride (bf16): 16 rows of a fragment read land on 16 bank groups
+    constexpr int VTS = KT + 8;  // V^T row stride (bf16), likewise
+    constexpr int KU = KT * (HD / 8) / NT;  // K units (key, 8 dims) a thread stages
+    constexpr int VU = 64 * (KT / 8) / NT;  // V items (dimension pair, operand group) a thread stages
+    constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
+    __shared__ uint4 ksh[KT * KSB / 8], ksl[F32 ? KT * KSB / 8 : 1];
+    __shared__ uint4 vth[HD * VTS / 8], vtl[F32 ? HD * VTS / 8 : 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int G = a.group, QT = kGqaRows / G;
+    const int g = blockIdx.y;
+    const int t0 = blockIdx.x * QT;
+    const int nq = n - t0 < QT ? n - t0 : QT;
+    const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
+    // Rows of set s: block row r = RW wave + 16 s + li is head g G + r / QT,
+    // token t0 + r % QT.
+    int qloc[SETS], head[SETS];
+    uint4 qh[SETS][HD / 32], ql[SETS][HD / 32];
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+        const int r = RW * wave + 16 * s + li;
+        qloc[s] = r % QT;
+        head[s] = g * G + r / QT;
+        const float *qp = a.q + ((long long)(t0 + (qloc[s] < nq ? qloc[s] : 0)) * a.n_heads + head[s]) * HD + 8 * lg;
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c) {
+            float f[8];
+            const float4 x0 = *reinterpret_cast<const float4 *>(qp + 32 * c);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qp + 32 * c + 4);
+            f[0] = x0.x; f[1] = x0.y; f[2] = x0.z; f[3] = x0.w;
+            f[4] = x1.x; f[5] = x1.y; f[6] = x1.z; f[7] = x1.w;
+            if (qloc[s] >= nq)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = 0.f;
+            split8(f, qh[s][c], ql[s][c]);
+        }
+    }
+    const KV *kb = reinterpret_cast<const KV *>(a.k) + (long long)g * a.head_stride;
+    const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
+    const long long last = pos + t0 + nq - 1;  // the block's last query position
+    // This wave's last query position (rows past n excluded).
+    const int wq = QT >= RW ? (RW * wave) % QT + RW - 1 : QT - 1;
+    const long long wlast = pos + t0 + (wq < nq - 1 ? wq : nq - 1);
+    const long long ntiles = last / KT + 1, z = blockIdx.z;
+    const long long kt0 = z * ntiles / a.nsplit, kt1 = (z + 1) * ntiles / a.nsplit;
+    floatx4 o[SETS][HD / 16];
+    float m[SETS], l[SETS];
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+        m[s] = -INFINITY;
+        l[s] = 0.f;
+#pragma unroll
+        for (int d = 0; d < HD / 16; ++d) o[s][d] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float scale2 = a.scale * kLog2e;
+    // Staging. K unit u = tid + NT i is key u / 16, dims 8 (u % 16) + [0, 8).
+    // V item u = tid + NT i is dimensions 2 (u % 64) + {0, 1} of operand group
+    // u / 64 (slice (u / 64) / 4, group (u / 64) % 4). Positions past the
+    // block's last query read as 0. A bf16 cache stays packed in registers
+    // (its lo terms are 0); an f32 cache is held as f32 and split when stored.
+    const int vd = 2 * (tid & 63);
+    auto kkey = [&](int i) { return (tid + NT * i) >> 4; };
+    auto kch = [&](int i) { return (tid + NT * i) & 15; };
+    auto vgrp = [&](int i) { return (tid + NT * i) >> 6; };
+    auto vkey = [&](int i, int j) {  // key (within the tile) at operand position j of item i
+        const int gr = vgrp(i), sigma = gr >> 2, gp = gr & 3;
+        return 32 * sigma + (j < 4 ? 4 * gp + j : 16 + 4 * gp + j - 4);
+    };
+    uint4 kpk[F32 ? 1 : KU];
+    uint32_t vpk[F32 ? 1 : VU][8];
+    float4 kf[F32 ? KU : 1][2];
+    float2 vf[F32 ? VU : 1][8];
+    auto fetch = [&](long long c0) {
+#pragma unroll
+        for (int i = 0; i < KU; ++i) {
+            const long long pk = c0 + kkey(i);
+            const KV *src = kb + pk * a.pos_stride + 8 * kch(i);
+            if constexpr (F32) {
+                kf[i][0] = pk <= last ? *reinterpret_cast<const float4 *>(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+                kf[i][1] = pk <= last ? *reinterpret_cast<const float4 *>(src + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                kpk[i] = pk <= last ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VU; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const long long pv = c0 + vkey(i, j);
+                const KV *src = vb + pv * a.pos_stride + vd;
+                if constexpr (F32)
+                    vf[i][j] = pv <= last ? *reinterpret_cast<const float2 *>(src) : make_float2(0.f, 0.f);
+                else
+                    vpk[i][j] = pv <= last ? *reinterpret_cast<const uint32_t *>(src) : 0u;
+            }
+    };
+    const long long cend = kt1 * KT;
+    if (kt0 < kt1) fetch(kt0 * KT);
+    for (long long c0 = kt0 * KT; c0 < cend; c0 += KT) {
+        __syncthreads();  // the previous tile is consumed
+#pragma unroll
+        for (int i = 0; i < KU; ++i) {
+            const int off = (kkey(i) * KSB + 8 * kch(i)) / 8;
+            if constexpr (F32) {
+                const float f[8] = {kf[i][0].x, kf[i][0].y, kf[i][0].z, kf[i][0].w,
+                                    kf[i][1].x, kf[i][1].y, kf[i][1].z, kf[i][1].w};
+                split8(f, ksh[off], ksl[off]);
+            } else {
+                ksh[off] = kpk[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VU; ++i) {
+            const int gr = vgrp(i);
+            const int off0 = (vd * VTS + 32 * (gr >> 2) + 8 * (gr & 3)) / 8, off1 = off0 + VTS / 8;
+            if constexpr (F32) {
+                float f0[8], f1[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    f0[j] = vf[i][j].x;
+                    f1[j] = vf[i][j].y;
+                }
+                split8(f0, vth[off0], vtl[off0]);
+                split8(f1, vth[off1], vtl[off1]);
+            } else {
+                uint32_t e[4], d[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t w0 = vpk[i][2 * j], w1 = vpk[i][2 * j + 1];
+                    e[j] = (w0 & 0xFFFFu) | (w1 << 16);          // dimension vd
+                    d[j] = (w0 >> 16) | (w1 & 0xFFFF0000u);      // dimension vd + 1
+                }
+                vth[off0] = make_uint4(e[0], e[1], e[2], e[3]);
+                vth[off1] = make_uint4(d[0], d[1], d[2], d[3]);
+            }
+        }
+        __syncthreads();
+        if (c0 + KT < cend) fetch(c0 + KT);
+        if (c0 > wlast) continue;  // every query of this wave precedes the tile
+        // S^T: keys c0 + 16 j + [0, 16) down, the set's 16 rows across.
+        floatx4 st[SETS][KT / 16];
+#pragma unroll
+        for (int s = 0; s < SETS; ++s)
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j) st[s][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c)
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j) {
+                const int ko = ((16 * j + li) * KSB + 32 * c + 8 * lg) / 8;
+                const bf16x8_t kh = as_bf8(ksh[ko]);
+#pragma unroll
+                for (int s = 0; s < SETS; ++s) {
+                    st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, as_bf8(qh[s][c]), st[s][j], 0, 0, 0);
+                    st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, as_bf8(ql[s][c]), st[s][j], 0, 0, 0);
+                }
+                if constexpr (F32) {
+                    const bf16x8_t kl = as_bf8(ksl[ko]);
+#pragma unroll
+                    for (int s = 0; s < SETS; ++s)
+                        st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, as_bf8(qh[s][c]), st[s][j], 0, 0, 0);
+                }
+            }
+        // Causal mask and online softmax of the lane's row; p overwrites st.
+#pragma unroll
+        for (int s = 0; s < SETS; ++s) {
+            const long long qpos = pos + t0 + qloc[s];
+            const bool in = qloc[s] < nq;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const long long key = c0 + 16 * j + 4 * lg + e;
+                    const float v = in && key <= qpos ? st[s][j][e] * scale2 : -INFINITY;
+                    st[s][j][e] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mn = fmaxf(m[s], mx);
+            const float alpha = m[s] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[s] - mn);
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v = st[s][j][e];
+                    const float p = v == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v - mn);
+                    st[s][j][e] = p;
+                    sum += p;
+                }
+            sum += __shfl_xor(sum, 16);
+            sum += __shfl_xor(sum, 32);
+            l[s] = l[s] * alpha + sum;
+            m[s] = mn;
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[s][d][e] *= alpha;
+        }
+        // O^T += V^T P^T over the tile's two 32-key slices.
+#pragma unroll
+        for (int sg = 0; sg < KT / 32; ++sg) {
+            uint4 ph[SETS], pl[SETS];
+#pragma unroll
+            for (int s = 0; s < SETS; ++s) {
+                const float f[8] = {st[s][2 * sg][0],     st[s][2 * sg][1],     st[s][2 * sg][2],
+                                    st[s][2 * sg][3],     st[s][2 * sg + 1][0], st[s][2 * sg + 1][1],
+                                    st[s][2 * sg + 1][2], st[s][2 * sg + 1][3]};
+                split8(f, ph[s], pl[s]);
+            }
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d) {
+                const int vo = ((16 * d + li) * VTS + 32 * sg + 8 * lg) / 8;
+                const bf16x8_t vh = as_bf8(vth[vo]);
+#pragma unroll
+                for (int s = 0; s < SETS; ++s) {
+                    o[s][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, as_bf8(ph[s]), o[s][d], 0, 0, 0);
+                    o[s][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, as_bf8(pl[s]), o[s][d], 0, 0, 0);
+                }
+                if constexpr (F32) {
+                    const bf16x8_t vl = as_bf8(vtl[vo]);
+#pragma unroll
+                    for (int s = 0; s < SETS; ++s)
+                        o[s][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, as_bf8(ph[s]), o[s][d], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // o[s][d][e] is dimension 16 d + 4 lg + e of the lane's row.
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+        if (qloc[s] >= nq) continue;
+        const long long th = (long long)(t0 + qloc[s]) * a.n_heads + head[s];
+        if (a.nsplit == 1) {
+            const float inv = 1.f / l[s];
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d) {
+                const float4 v = make_float4(o[s][d][0] * inv, o[s][d][1] * inv, o[s][d][2] * inv, o[s][d][3] * inv);
+                const long long off = th * HD + 16 * d + 4 * lg;
+                if (a.out_hi) {
+                    uint2 h, w;
+                    split_bf16x4(v, h, w);
+                    *reinterpret_cast<uint2 *>(a.out_hi + off) = h;
+                    *reinterpret_cast<uint2 *>(a.out_lo + off) = w;
+                } else {
+                    *reinterpret_cast<float4 *>(a.out + off) = v;
+                }
+            }
+        } else {
+            const long long slot = th * a.nsplit + z;
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d)
+                *reinterpret_cast<float4 *>(a.part_acc + slot * HD + 16 * d + 4 * lg) =
+                    make_float4(o[s][d][0], o[s][d][1], o[s][d][2], o[s][d][3]);
+            if (lg == 0) {
+                a.part_ml[slot * 2] = m[s] * kLn2;
+                a.part_ml[slot * 2 + 1] = l[s];
+            }
+        }
+    }
+}
+
 template <int HD>
 static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
     dim3 grid((unsigned)(n * (size_t)k.n_kv_heads * (size_t)k.nsplit));
@@ -579,11 +875,20 @@ static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim) {
     if (n == 0) return hipSuccess;
     if (head_dim == 128 && n >= kAttnTileMin) {
-        dim3 grid((unsigned)((n + kMQT - 1) / kMQT), (unsigned)k.n_heads, (unsigned)k.nsplit);
-        if (k.kv_bf16)
-            attn_bf16_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
-        else
-            attn_bf16_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
+        if (k.group >= 1 && k.group <= 8 && 8 % k.group == 0 && k.n_kv_heads * k.group == k.n_heads) {
+            const int qt = kGqaRows / k.group;
+            dim3 grid((unsigned)((n + qt - 1) / qt), (unsigned)k.n_kv_heads, (unsigned)k.nsplit);
+            if (k.kv_bf16)
+                attn_gqa_kernel<uint16_t><<<grid, 64 * GqaShape<uint16_t>::NW, 0, s>>>(k, (int)n);
+            else
+                attn_gqa_kernel<float><<<grid, 64 * GqaShape<float>::NW, 0, s>>>(k, (int)n);
+        } else {
+            dim3 grid((unsigned)((n + kMQT - 1) / kMQT), (unsigned)k.n_heads, (unsigned)k.nsplit);
+            if (k.kv_bf16)
+                attn_bf16_kernel<uint16_t><<<grid, 256, 0, s>>>(k, (int)n);
+            else
+                attn_bf16_kernel<float><<<grid, 256, 0, s>>>(k, (int)n);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || k.nsplit == 1) return e;
         return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128, k.out_hi,
