@@ -261,8 +261,8 @@ def test_qwen_decode_attention(hip, ctx):
 
 
 def test_prefill_attention(hip):
-    """Causal attention of 100 tokens from position 20 (several splits)."""
-    H, KVH, hd, n, pos = 16, 8, 128, 100, 20
+    """Causal attention of 100 tokens from position 300 (keys split over two blocks)."""
+    H, KVH, hd, n, pos = 16, 8, 128, 100, 300
     L = pos + n
     kv = bf16_to_f32(normal_bf16(L * KVH * hd, 7, "pk"))
     vv = bf16_to_f32(normal_bf16(L * KVH * hd, 7, "pv"))

@@ -21,7 +21,9 @@ namespace th {
 constexpr int kAttnMaxGroup = 8;   // query heads per KV head
 constexpr int kAttnSub = 256;      // positions scored per sub-chunk
 constexpr size_t kAttnTileMin = 8; // tokens from which a launch uses the matrix-core kernel
-constexpr size_t kMKTiles = 32;    // positions per key tile of that kernel
+constexpr size_t kMKTiles = 32;    // positions per key tile of the one-head-a-block kernel
+constexpr int kMQT = 64;           // tokens per block of that kernel
+constexpr int kGqaRows = 128, kGqaKeys = 64;  // (token, head) rows a block, keys a tile: GQA kernel
 
 template <typename KV>
 __device__ __forceinline__ void load8(const KV *p, float f[8]);
@@ -287,12 +289,19 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(float *__restric
     }
 }
 
-int attention_splits(size_t n, size_t n_kv_heads, size_t max_len, size_t head_dim) {
-    // Several tokens on the matrix cores: split a query tile's keys so that
-    // each split walks at least 4 key tiles, at most 8 splits.
+int attention_splits(size_t n, size_t n_heads, size_t n_kv_heads, size_t max_len, size_t head_dim) {
+    // Several tokens on the matrix cores: split the keys until the launch has
+    // about 1024 blocks, keeping at least two 64-key tiles a split, at most 8
+    // splits (each split adds partials for the combine to read).
     if (head_dim == 128 && n >= kAttnTileMin) {
-        const size_t tiles = (max_len + kMKTiles - 1) / kMKTiles;
-        return (int)std::min<size_t>(std::max<size_t>(tiles / 4, 1), 8);
+        const size_t group = n_kv_heads ? n_heads / n_kv_heads : 0;
+        const bool gqa = group >= 1 && group <= 8 && 8 % group == 0 && group * n_kv_heads == n_heads;
+        const size_t qt = gqa ? kGqaRows / group : kMQT;
+        const size_t blocks = (n + qt - 1) / qt * (gqa ? n_kv_heads : n_heads);
+        const size_t tiles = (max_len + kGqaKeys - 1) / kGqaKeys;
+        size_t ns = 1;
+        while (ns < 8 && blocks * ns < 1024 && tiles >= 4 * ns) ns *= 2;
+        return (int)ns;
     }
     // One split while a block's share is short; otherwise about two blocks per
     // CU, each split covering at least 64 positions.
@@ -350,7 +359,7 @@ __device__ __forceinline__ float4 load4(const uint16_t *p) {
 // as bf16 rows, values transposed (dimension x key) so that a lane's eight
 // keys of one dimension are one 16-byte read. Layout of 16x16x32: lane l
 // holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16] and D[4(l/16)+e][l%16].
-constexpr int kMQT = 64, kMKT = (int)kMKTiles;
+constexpr int kMKT = (int)kMKTiles;
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float row_max16(float v) {
@@ -576,8 +585,6 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(AttnKernelArgs a, int n)
 // operand position 8 g + i holds key 4 g + i for i < 4 and 16 + 4 g + i - 4
 // otherwise. Operands are split into bf16 hi + lo terms as in
 // attn_bf16_kernel (q and p always; an f32 cache's keys and values too).
-constexpr int kGqaRows = 128, kGqaKeys = 64;
-
 template <typename KV>
 struct GqaShape;
 template <>

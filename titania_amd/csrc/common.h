@@ -130,7 +130,7 @@ struct AttnKernelArgs {
 };
 // Splits of the sequence for n tokens (of head_dim) whose contexts reach at
 // most max_len.
-int attention_splits(size_t n, size_t n_kv_heads, size_t max_len, size_t head_dim);
+int attention_splits(size_t n, size_t n_heads, size_t n_kv_heads, size_t max_len, size_t head_dim);
 // Scratch floats the partials of `nsplit` splits take (0 for one split).
 size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit);
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim);

@@ -316,7 +316,7 @@ int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_bu
     TH_REQUIRE(k_cache->len >= (pos + n) * kv_dim && v_cache->len >= (pos + n) * kv_dim,
                "the caches do not hold position %zu", pos + n - 1);
     TH_REQUIRE(out->ptr != q->ptr, "attention cannot write its queries");
-    int nsplit = th::attention_splits(n, n_kv_heads, pos + n, head_dim);
+    int nsplit = th::attention_splits(n, n_heads, n_kv_heads, pos + n, head_dim);
     size_t floats = th::attention_scratch(n, n_heads, head_dim, nsplit);
     float *scr = nullptr;
     if (floats) {

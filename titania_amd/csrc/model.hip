@@ -335,7 +335,7 @@ int ensure_fused_state(th_state *s) {
     s->attn_part_floats = th::attention_scratch(1, (size_t)c.num_attention_heads, hd,
                                                 th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16));
     for (size_t n = 1; n <= s->fb; ++n) {
-        int ns = th::attention_splits(n, (size_t)c.num_key_value_heads, s->max_len, hd);
+        int ns = th::attention_splits(n, (size_t)c.num_attention_heads, (size_t)c.num_key_value_heads, s->max_len, hd);
         s->attn_part_floats =
             std::max(s->attn_part_floats, th::attention_scratch(n, (size_t)c.num_attention_heads, hd, ns));
     }
@@ -475,7 +475,7 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
     const size_t qd = nh * hd;
     const int kv_bf16 = s->kv_dtype == TH_KV_BF16;
     const size_t max_ctx = pos_dev ? s->max_len : pos + n;
-    const int nsplit = th::attention_splits(n, nkv, max_ctx, hd);
+    const int nsplit = th::attention_splits(n, nh, nkv, max_ctx, hd);
     if (th::attention_scratch(n, nh, hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
     // Chunks of kGemmMinTokens or more go through the MFMA GEMM (activations
