@@ -10,8 +10,9 @@
 //
 // Tiling: a 256-thread block computes 64 tokens x 64 weight rows (the small
 // tile; each of its four waves a 32 x 32 quarter, 2 x 2 MFMA tiles of 16 x 16)
-// or, in launches of many tiles, 128 x 128 (the large tile, 4 x 4 MFMA tiles a
-// wave). K advances 64 at a time through a ring of 3 LDS stages (hi, lo and
+// or, in launches of many tiles, a 512-thread block 128 x 128 (the large
+// tile; eight waves of 32 tokens x 64 rows, 2 x 4 MFMA tiles, two waves a
+// SIMD). K advances 64 at a time through a ring of 3 LDS stages (hi, lo and
 // weight tiles: 24 KB a stage for the small tile, so two blocks fit a CU;
 // 48 KB for the large tile, one block a CU) that the block fills with direct
 // global->LDS loads (global_load_lds, 16 bytes a lane) two steps ahead of the
@@ -30,26 +31,28 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
-constexpr int NTHR = 256;
-constexpr int BK = 64;                    // columns per K step
-constexpr int CH = BK / 8;                // 16-byte chunks per tile row (bf16)
+constexpr int BK = 64;                    // K range multiple every launch needs
 
-// A block tile of BM tokens x BN weight rows, its four waves each a
-// BM/2 x BN/2 quarter, K staged through `STAGES` LDS stages.
-template <int BM_, int BN_, int STAGES_>
+// A block tile of BM tokens x BN weight rows, its WGM x WGN waves each a
+// BM/WGM x BN/WGN part, K staged BK columns at a time through `STAGES` LDS
+// stages.
+template <int BM_, int BN_, int BK_, int STAGES_, int WGM_ = 2, int WGN_ = 2>
 struct Tile {
-    static constexpr int BM = BM_, BN = BN_, kStages = STAGES_;
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, kStages = STAGES_;
+    static constexpr int WGM = WGM_, WGN = WGN_, NT = 64 * WGM * WGN;  // waves: WGM down x WGN across
+    static constexpr int CH = BK / 8;  // 16-byte chunks per tile row (bf16)
     static constexpr int TA = BM * CH, TB = BN * CH;     // 16-byte chunks per tile
-    static constexpr int FM = BM / 32, FN = BN / 32;     // 16 x 16 fragments per wave
-    static constexpr int DMA_PER_WAVE = (2 * TA + TB) / NTHR;
+    static constexpr int FM = BM / WGM / 16, FN = BN / WGN / 16;  // 16 x 16 fragments per wave
+    static constexpr int DMA_PER_WAVE = (2 * TA + TB) / NT;
     struct alignas(16) Stage {
         uint4 hi[TA], lo[TA];  // [BM][CH] activation halves
         uint4 w[TB];           // [BN][CH] weights
     };
 };
-using Small = Tile<64, 64, 3>;    // 24 KB a stage: two blocks a CU
-using Large = Tile<128, 128, 3>;  // 48 KB a stage: one block a CU
+using Small = Tile<64, 64, 64, 3>;    // 24 KB a stage: two blocks a CU
+using Large = Tile<128, 128, 64, 3, 4, 2>;  // 48 KB a stage: one block a CU, eight waves of 32 x 64
 
+template <int CH>
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & (CH - 1); }
 
 __device__ __forceinline__ void dma16(const void *src, uint4 *lds_wave_base) {
@@ -95,19 +98,20 @@ __device__ __forceinline__ void issue_step(typename T::Stage &st, const uint16_t
     static_assert(T::TA == T::TB, "square tiles: one span of each tile per iteration");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < T::TA / NTHR; ++i) {
-        const int span = wave * (T::TA / NTHR) + i;
-        const int p = span * 64 + lane, row = p / CH, pc = p % CH;
+    for (int i = 0; i < T::TA / T::NT; ++i) {
+        const int span = wave * (T::TA / T::NT) + i;
+        const int p = span * 64 + lane, row = p / T::CH, pc = p % T::CH;
         const int t = min(t0 + row, n - 1);
-        const size_t off = (size_t)t * cols + k0 + (pc ^ swz(row)) * 8;
+        const size_t off = (size_t)t * cols + k0 + (pc ^ swz<T::CH>(row)) * 8;
         dma16(hi + off, st.hi + span * 64);
         dma16(lo + off, st.lo + span * 64);
-        dma16(w + (size_t)row * cols + k0 + (pc ^ swz(row)) * 8, st.w + span * 64);
+        dma16(w + (size_t)row * cols + k0 + (pc ^ swz<T::CH>(row)) * 8, st.w + span * 64);
     }
 }
 
+template <int CH>
 __device__ __forceinline__ bf16x8 frag(const uint4 *tile, int row, int lc) {
-    return __builtin_bit_cast(bf16x8, tile[row * CH + (lc ^ swz(row))]);
+    return __builtin_bit_cast(bf16x8, tile[row * CH + (lc ^ swz<CH>(row))]);
 }
 
 // The matrix that the row tile r0 of the concatenation falls in: its weights
@@ -139,13 +143,13 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = blockIdx.y * T::BM;
     const int rl = sg.local;
-    const int wm = (wave >> 1) * (T::BM / 2), wn = (wave & 1) * (T::BN / 2);
+    const int wm = (wave / T::WGN) * (T::BM / T::WGM), wn = (wave % T::WGN) * (T::BN / T::WGN);
     const int fr = lane & 15, fq = lane >> 4;  // fragment row, quarter of the K slice
-    const int nk_all = cols / BK, z = blockIdx.z;
+    const int nk_all = cols / T::BK, z = blockIdx.z;
     const int kb = (int)((long long)z * nk_all / ksplit), nk = (int)((long long)(z + 1) * nk_all / ksplit) - kb;
-    const uint16_t *w = sg.w + (size_t)rl * cols + (size_t)kb * BK;
-    hi += (size_t)kb * BK;
-    lo += (size_t)kb * BK;
+    const uint16_t *w = sg.w + (size_t)rl * cols + (size_t)kb * T::BK;
+    hi += (size_t)kb * T::BK;
+    lo += (size_t)kb * T::BK;
 
     f32x4 acc[FM][FN];
 #pragma unroll
@@ -155,7 +159,7 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
 
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s)
-        if (s < nk) issue_step<T>(ring[s], hi, lo, w, t0, n, cols, s * BK);
+        if (s < nk) issue_step<T>(ring[s], hi, lo, w, t0, n, cols, s * T::BK);
 
     for (int k = 0; k < nk; ++k) {
         // This wave's loads of step k are done once at most the later steps'
@@ -165,19 +169,19 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
         else wait_vm<0>();
         stage_barrier();
         if (k + kStages - 1 < nk)
-            issue_step<T>(ring[(k + kStages - 1) % kStages], hi, lo, w, t0, n, cols, (k + kStages - 1) * BK);
+            issue_step<T>(ring[(k + kStages - 1) % kStages], hi, lo, w, t0, n, cols, (k + kStages - 1) * T::BK);
         const typename T::Stage &st = ring[k % kStages];
 #pragma unroll
-        for (int ks = 0; ks < BK / 32; ++ks) {
+        for (int ks = 0; ks < T::BK / 32; ++ks) {
             const int lc = ks * 4 + fq;
             bf16x8 ah[FM], al[FM], b[FN];
 #pragma unroll
             for (int m = 0; m < FM; ++m) {
-                ah[m] = frag(st.hi, wm + m * 16 + fr, lc);
-                al[m] = frag(st.lo, wm + m * 16 + fr, lc);
+                ah[m] = frag<T::CH>(st.hi, wm + m * 16 + fr, lc);
+                al[m] = frag<T::CH>(st.lo, wm + m * 16 + fr, lc);
             }
 #pragma unroll
-            for (int q = 0; q < FN; ++q) b[q] = frag(st.w, wn + q * 16 + fr, lc);
+            for (int q = 0; q < FN; ++q) b[q] = frag<T::CH>(st.w, wn + q * 16 + fr, lc);
 #pragma unroll
             for (int m = 0; m < FM; ++m)
 #pragma unroll
@@ -201,13 +205,13 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
             }
 }
 
-__global__ __launch_bounds__(NTHR, 2) void gemm_kernel(Segs sg, const uint16_t *__restrict__ hi,
+__global__ __launch_bounds__(Small::NT, 2) void gemm_kernel(Segs sg, const uint16_t *__restrict__ hi,
                                                         const uint16_t *__restrict__ lo, int n, int cols,
                                                         float *__restrict__ part, int ksplit) {
     gemm_tile<Small>(seg_tile(sg, blockIdx.x * Small::BN), hi, lo, n, cols, part, ksplit);
 }
 
-__global__ __launch_bounds__(NTHR, 1) void gemm_large_kernel(Segs sg, const uint16_t *__restrict__ hi,
+__global__ __launch_bounds__(Large::NT, 1) void gemm_large_kernel(Segs sg, const uint16_t *__restrict__ hi,
                                                               const uint16_t *__restrict__ lo, int n, int cols,
                                                               float *__restrict__ part, int ksplit) {
     gemm_tile<Large>(seg_tile(sg, blockIdx.x * Large::BN), hi, lo, n, cols, part, ksplit);
@@ -308,10 +312,10 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
     if (total / Small::BN > 65535) return hipErrorInvalidValue;
     if (use_large(n, outs, n_outs, ksplit)) {
         dim3 grid((unsigned)(total / Large::BN), (unsigned)((n + Large::BM - 1) / Large::BM), 1);
-        gemm_large_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, 1);
+        gemm_large_kernel<<<grid, Large::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, 1);
     } else {
         dim3 grid((unsigned)(total / Small::BN), (unsigned)((n + Small::BM - 1) / Small::BM), (unsigned)ksplit);
-        gemm_kernel<<<grid, NTHR, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+        gemm_kernel<<<grid, Small::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
     }
     return hipGetLastError();
 }
