@@ -23,6 +23,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -108,6 +110,138 @@ def prefill_bench(dev, model, cfg, n: int, kv: int, seed: int) -> dict:
             "roofline": {"bound": "mfma", "achieved": fl / (ms / 1000.0) / 1e12, "peak": MFMA_BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": fl / (ms / 1000.0) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
                          "flops": fl}}
+
+
+# Isolated decode kernels at the Qwen3-0.6B shapes: (name, rows, cols) of each
+# GEMV, out = W x with W bf16 [rows, cols] and x f32 [cols].
+KERNEL_GEMVS = [("q 1024->2048", 2048, 1024), ("k or v 1024->1024", 1024, 1024), ("o 2048->1024", 1024, 2048),
+                ("gate+up 1024->6144", 6144, 1024), ("down 3072->1024", 1024, 3072),
+                ("lm_head 1024->151936", 151936, 1024)]
+KERNEL_CONTEXTS = [512, 4096, 32768]
+ROTATE_BYTES = 1 << 30  # operand copies cycled per timed graph: well past the 256 MB last-level cache
+
+
+def _graph_time(dev, calls, reps: int = 3) -> float:
+    """Milliseconds of one replay of a graph holding `calls` (a list of
+    zero-argument device calls), the median of `reps` timed replays after
+    one untimed replay."""
+    dev.graph_begin()
+    try:
+        for c in calls:
+            c()
+    finally:
+        g = dev.graph_end()
+    g.launch()
+    dev.synchronize()
+    times = []
+    for _ in range(reps):
+        dev.timer_begin()
+        g.launch()
+        times.append(dev.timer_end())
+    g.free()
+    return sorted(times)[len(times) // 2]
+
+
+def kernel_bench(dev, seed: int) -> dict:
+    """Decode kernels alone: the GEMVs, RMSNorm and RoPE at the Qwen3-0.6B
+    shapes (bf16 W and f32 x ~ N(0, 1)), and GQA decode attention (16 q heads,
+    8 KV heads, head_dim 128) at contexts 512, 4096 and 32768 on the C ABI's
+    f32 caches holding bf16-rounded N(0, 1). Each call is captured many times
+    into one HIP graph over rotating copies of its operands (together past the
+    last-level cache, so every call reads HBM), and a replay is timed with HIP
+    events: the time per call includes the graph's gap between kernels
+    (about 1.5 us). GB/s counts the algorithmic bytes of a call."""
+    from titania_amd import Tensor
+    from titania_amd.synth import bf16_to_f32, normal_bf16
+
+    out = {"gemv": [], "norm_rope": [], "attention_f32_cache": []}
+    rng = np.random.default_rng(seed)
+    for name, rows, cols in KERNEL_GEMVS:
+        wbits = normal_bf16(rows * cols, seed + rows + cols, name)
+        copies = max(2, -(-ROTATE_BYTES // (2 * rows * cols)))
+        ws = [dev.upload(Tensor((rows, cols), wbits)) for _ in range(copies)]
+        x = dev.alloc(cols)
+        dev.write(x, rng.standard_normal(cols).astype(np.float32))
+        y = dev.alloc(rows)
+        calls = [(lambda w=w: dev.matmul(y, w, x)) for w in ws] * max(1, 64 // copies)
+        ms = _graph_time(dev, calls)
+        us = ms * 1000.0 / len(calls)
+        nbytes = 2 * rows * cols + 4 * cols + 4 * rows
+        out["gemv"].append({"kernel": name, "us": us, "bytes": nbytes, "GB/s": nbytes / us / 1e3,
+                            "frac": nbytes / us / 1e3 / HBM_PEAK_GBS, "copies": copies})
+        for w in ws:
+            w.free()
+        x.free()
+        y.free()
+    gain = dev.upload(Tensor((1024,), normal_bf16(1024, seed, "gain")))
+    hgain = dev.upload(Tensor((128,), normal_bf16(128, seed, "hgain")))
+    xr = dev.alloc(1024)
+    xh = dev.alloc(24 * 128)
+    inv = (1e6 ** (-np.arange(64, dtype=np.float64) * 2.0 / 128)).astype(np.float32)
+    ang = np.arange(4096, dtype=np.float32)[:, None] * inv[None, :]
+    table = np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32).reshape(-1)  # [pos][64][cos, sin]
+    tb = dev.alloc(table.size)
+    dev.write(tb, table)
+    for name, call in [("rmsnorm 1 x 1024", lambda: dev.rmsnorm(xr, gain, 1e-6)),
+                       ("rmsnorm 24 x 128 (q/k heads)", lambda: dev.rmsnorm(xh, hgain, 1e-6)),
+                       ("rope 16 + 8 heads x 128", lambda: dev.rope(xh, tb, 4000, 24, 128))]:
+        ms = _graph_time(dev, [call] * 64)
+        out["norm_rope"].append({"kernel": name, "us": ms * 1000.0 / 64})
+    for b in (gain, hgain):
+        b.free()
+    for b in (xr, xh, tb):
+        b.free()
+    H, KVH, hd = 16, 8, 128
+    for ctx in KERNEL_CONTEXTS:
+        n = ctx * KVH * hd
+        kv_bytes = 2 * 4 * n
+        copies = max(2, -(-ROTATE_BYTES // kv_bytes))
+        kh = bf16_to_f32(normal_bf16(n, ctx, "k"))
+        vh = bf16_to_f32(normal_bf16(n, ctx, "v"))
+        ks, vs = [dev.alloc(n) for _ in range(copies)], [dev.alloc(n) for _ in range(copies)]
+        for k, v in zip(ks, vs):
+            dev.write(k, kh)
+            dev.write(v, vh)
+        q = dev.alloc(H * hd)
+        dev.write(q, bf16_to_f32(normal_bf16(H * hd, ctx, "q")))
+        o = dev.alloc(H * hd)
+        dev.attention(o, q, ks[0], vs[0], ctx - 1, H, hd, KVH)  # sizes the device scratch before the capture
+        calls = [(lambda k=k, v=v: dev.attention(o, q, k, v, ctx - 1, H, hd, KVH))
+                 for k, v in zip(ks, vs)] * max(1, 32 // copies)
+        ms = _graph_time(dev, calls)
+        us = ms * 1000.0 / len(calls)
+        nbytes = kv_bytes + 2 * 4 * H * hd
+        out["attention_f32_cache"].append({"context": ctx, "us": us, "bytes": nbytes, "GB/s": nbytes / us / 1e3,
+                                           "frac": nbytes / us / 1e3 / HBM_PEAK_GBS, "copies": copies})
+        for b in ks + vs + [q, o]:
+            b.free()
+    return out
+
+
+def long_context_decode(dev, model, cfg, kv: int, kv_elem: int, steps: int, seed: int) -> list:
+    """Greedy decode of the whole model (one graph replay a step) after prompts
+    of 512, 4096 and 32768 tokens, the product path's decode attention on the
+    state's cache: ms per step and the step's algorithmic HBM rate (weights,
+    the KV rows read and written, the logits)."""
+    from titania_amd import TH_PATH_FUSED, synth
+    from titania_amd.model import State
+
+    rows = []
+    for ctx in KERNEL_CONTEXTS:
+        prompt = synth.prompt(ctx, cfg.vocab_size, seed=seed + ctx)
+        st = State(model, ctx + steps + 1, kv)
+        model.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+        model.decode(st, ctx, 2)  # captures the step graph
+        model.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+        dev.synchronize()
+        dev.timer_begin()
+        model.decode(st, ctx, steps)
+        ms = dev.timer_end() / steps
+        st.close()
+        nbytes = cfg.weight_bytes_per_token() + kv_bytes_per_token(cfg, ctx, steps, kv_elem) + 4 * cfg.vocab_size
+        rows.append({"context": ctx, "ms_per_step": ms, "tokens_per_s": 1000.0 / ms, "bytes_per_step": nbytes,
+                     "GB/s": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS})
+    return rows
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "decode_traffic.json"
@@ -225,6 +359,10 @@ def main() -> int:
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="instead of benchmarking, summarize two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                          "'bench.py --calibrate-copy MIB --steps K' into HBM bytes per decode step")
+    ap.add_argument("--kernels", action="store_true",
+                    help="instead of the decode benchmark, time the decode kernels alone (GEMVs, norms, RoPE, "
+                         "attention at contexts 512 / 4096 / 32768) and whole-model decode after prompts of those "
+                         "lengths; prints one JSON line")
     ap.add_argument("--trace", type=int, default=0,
                     help="trace the first N timed steps of the persistent decode kernel and print a per-phase "
                          "breakdown to stderr")
@@ -246,6 +384,17 @@ def main() -> int:
     cfg = QWEN3_0_6B if args.model == "qwen3-0.6b" else QWEN3_4B
     kv = TH_KV_F32 if args.kv == "f32" else TH_KV_BF16
     kv_elem = 4 if kv == TH_KV_F32 else 2
+
+    if args.kernels:
+        dev = Hip(0)
+        res = {"mode": "kernels", "data": "synthetic (seeded N(0,1) operands; model weights N(0,0.02))",
+               "peak_GB/s": HBM_PEAK_GBS, "isolated": kernel_bench(dev, args.seed)}
+        print(json.dumps(res["isolated"]), file=sys.stderr, flush=True)
+        model = Model(dev, cfg, synth.weights(cfg, seed=args.seed))
+        res["decode_after_prompt"] = {"model": args.model, "kv": args.kv, "steps": args.steps,
+                                      "rows": long_context_decode(dev, model, cfg, kv, kv_elem, args.steps, args.seed)}
+        print(json.dumps(res))
+        return 0
 
     t = time.perf_counter()
     weights = synth.weights(cfg, seed=args.seed)

@@ -97,6 +97,26 @@ TH_API int th_silu_mul(th_device *dev, th_buffer *gate, const th_buffer *up);
 TH_API int th_timer_begin(th_device *dev);
 TH_API int th_timer_end(th_device *dev, float *ms);
 
+/* HIP graphs of the device's stream, for launch-bound sequences of calls (no
+ * counterpart in model/device.rs; the graph_begin / graph_end / graph_launch
+ * extension of the Device boundary). th_graph_begin starts capturing the
+ * stream in thread-local mode: the compute calls that follow (copy, matmul of
+ * fewer than 16 tokens, add, rmsnorm, rope, attention, silu_mul, the fused
+ * extensions) are recorded, not run. th_graph_end stops the capture and
+ * instantiates it; th_graph_launch queues one replay on the stream, reading
+ * and writing the buffers named at capture time. While capturing, the calls
+ * that allocate, move data to or from the host, wait or free (upload, alloc,
+ * read, write, embed, argmax, sample, the timer, synchronize, the frees and
+ * destroys, the model and state calls, a matmul of 16 or more tokens, and an
+ * attention whose partials outgrow the device's scratch) return
+ * TH_ERR_INVALID (the frees leave their handle valid); the capture stays open
+ * until th_graph_end. th_device_destroy discards an open capture. */
+typedef struct th_graph th_graph;
+TH_API int th_graph_begin(th_device *dev);
+TH_API int th_graph_end(th_device *dev, th_graph **out);
+TH_API int th_graph_launch(th_device *dev, const th_graph *graph);
+TH_API void th_graph_free(th_device *dev, th_graph *graph);
+
 /* ---- fused extensions (each equals its composition of trait methods) ---- */
 
 /* x += y, then xb = rmsnorm(x) with `weight` (the add, copy and rmsnorm of

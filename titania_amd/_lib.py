@@ -57,6 +57,10 @@ SIGNATURES: dict[str, tuple] = {
     "th_device_synchronize": (_I, [_P]),
     "th_timer_begin": (_I, [_P]),
     "th_timer_end": (_I, [_P, C.POINTER(C.c_float)]),
+    "th_graph_begin": (_I, [_P]),
+    "th_graph_end": (_I, [_P, C.POINTER(_P)]),
+    "th_graph_launch": (_I, [_P, _P]),
+    "th_graph_free": (None, [_P, _P]),
     "th_upload": (_I, [_P, _P, C.POINTER(_SZ), _SZ, C.POINTER(_P)]),
     "th_weight_free": (None, [_P, _P]),
     "th_weight_shape": (_I, [_P, C.POINTER(_SZ), C.POINTER(_SZ)]),

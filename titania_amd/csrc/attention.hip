@@ -303,11 +303,12 @@ int attention_splits(size_t n, size_t n_heads, size_t n_kv_heads, size_t max_len
         while (ns < 8 && blocks * ns < 1024 && tiles >= 4 * ns) ns *= 2;
         return (int)ns;
     }
-    // One split while a block's share is short; otherwise about two blocks per
-    // CU, each split covering at least 64 positions.
-    if (max_len <= 512) return 1;
+    // Few tokens: split the positions until the launch has about 1024 blocks
+    // (a block walks its positions one 256-row pass at a time, so short
+    // splits in many blocks keep more rows in flight), each split covering at
+    // least 64 positions, at most 256 splits.
     size_t blocks_per_split = n * n_kv_heads;
-    size_t want = (512 + blocks_per_split - 1) / blocks_per_split;
+    size_t want = (1024 + blocks_per_split - 1) / blocks_per_split;
     size_t cap = (max_len + 63) / 64;
     size_t s = std::min(want, cap);
     return (int)std::max<size_t>(1, std::min<size_t>(s, 256));

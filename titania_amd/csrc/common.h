@@ -25,6 +25,8 @@ struct th_device {
     uint32_t *token_out = nullptr;
     // th_timer_begin / th_timer_end.
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+    // Between th_graph_begin and th_graph_end: the stream is being captured.
+    bool capturing = false;
 };
 
 // A model takes ownership of weight handles it frees on destruction (the
@@ -67,6 +69,12 @@ void *scratch(th_device *dev, size_t bytes);
     do {                                                       \
         if (!(cond)) return th::fail(TH_ERR_INVALID, __VA_ARGS__); \
     } while (0)
+
+// Calls that allocate, move data to or from the host or wait are refused while
+// the device's stream is being captured (th_graph_begin .. th_graph_end).
+#define TH_NOT_CAPTURING(dev, what)                                                                        \
+    TH_REQUIRE(!(dev)->capturing, "%s cannot run while the device's stream is being captured (th_graph_begin)", \
+               what)
 
 // Returns the status of `call` from the enclosing function unless it is TH_OK.
 #define TRY(call)                 \

@@ -8,6 +8,7 @@
 #include <string>
 
 #include "common.h"
+#include "gemm.h"
 #include "sample.h"
 
 namespace {
@@ -30,6 +31,10 @@ void clear_error() { g_error.clear(); }
 
 void *scratch(th_device *dev, size_t bytes) {
     if (bytes <= dev->scratch_bytes) return dev->scratch;
+    if (dev->capturing) {  // growing it would wait for the stream and allocate
+        fail(TH_ERR_INVALID, "%zu bytes of device scratch: more than it held when the capture began", bytes);
+        return nullptr;
+    }
     size_t want = std::max(bytes, dev->scratch_bytes * 2);
     want = (want + 255) & ~(size_t)255;
     if (dev->scratch) {
@@ -103,6 +108,11 @@ int th_device_create(int ordinal, th_device **out) {
 void th_device_destroy(th_device *dev) {
     if (!dev) return;
     (void)hipSetDevice(dev->ordinal);
+    if (dev->capturing) {  // an open capture is discarded
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(dev->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        dev->capturing = false;
+    }
     if (dev->stream) (void)hipStreamSynchronize(dev->stream);
     if (dev->tokens) (void)hipFree(dev->tokens);
     if (dev->scratch) (void)hipFree(dev->scratch);
@@ -113,20 +123,78 @@ void th_device_destroy(th_device *dev) {
     delete dev;
 }
 
+struct th_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int th_graph_begin(th_device *dev) {
+    TH_REQUIRE(dev, "th_graph_begin: null device");
+    TH_REQUIRE(!dev->capturing, "the device's stream is already being captured");
+    TH_HIP(hipSetDevice(dev->ordinal));
+    TH_HIP(hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal));
+    dev->capturing = true;
+    return TH_OK;
+}
+
+int th_graph_end(th_device *dev, th_graph **out) {
+    TH_REQUIRE(dev && out, "th_graph_end: null argument");
+    TH_REQUIRE(dev->capturing, "th_graph_end without th_graph_begin");
+    dev->capturing = false;
+    hipGraph_t graph = nullptr;
+    TH_HIP(hipStreamEndCapture(dev->stream, &graph));
+    auto *g = new (std::nothrow) th_graph();
+    if (!g) {
+        (void)hipGraphDestroy(graph);
+        return fail(TH_ERR_NOMEM, "out of host memory");
+    }
+    g->graph = graph;
+    const hipError_t e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        delete g;
+        return fail(TH_ERR_HIP, "hipGraphInstantiate failed: %s", hipGetErrorString(e));
+    }
+    *out = g;
+    return TH_OK;
+}
+
+int th_graph_launch(th_device *dev, const th_graph *g) {
+    TH_REQUIRE(dev && g, "th_graph_launch: null argument");
+    TH_NOT_CAPTURING(dev, "th_graph_launch");
+    TH_HIP(hipGraphLaunch(g->exec, dev->stream));
+    return TH_OK;
+}
+
+void th_graph_free(th_device *dev, th_graph *g) {
+    if (!g) return;
+    if (dev && dev->capturing) {
+        th::fail(TH_ERR_INVALID, "th_graph_free cannot run while the device's stream is being captured");
+        return;
+    }
+    if (dev) (void)hipStreamSynchronize(dev->stream);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
 int th_device_synchronize(th_device *dev) {
     TH_REQUIRE(dev, "null device");
+    TH_NOT_CAPTURING(dev, "th_device_synchronize");
     TH_HIP(hipStreamSynchronize(dev->stream));
     return TH_OK;
 }
 
 int th_timer_begin(th_device *dev) {
     TH_REQUIRE(dev, "null device");
+    TH_NOT_CAPTURING(dev, "th_timer_begin");
     TH_HIP(hipEventRecord(dev->ev_begin, dev->stream));
     return TH_OK;
 }
 
 int th_timer_end(th_device *dev, float *ms) {
     TH_REQUIRE(dev && ms, "th_timer_end: null argument");
+    TH_NOT_CAPTURING(dev, "th_timer_end");
     TH_HIP(hipEventRecord(dev->ev_end, dev->stream));
     TH_HIP(hipEventSynchronize(dev->ev_end));
     TH_HIP(hipEventElapsedTime(ms, dev->ev_begin, dev->ev_end));
@@ -135,6 +203,7 @@ int th_timer_end(th_device *dev, float *ms) {
 
 int th_upload(th_device *dev, const uint16_t *data, const size_t *shape, size_t ndim, th_weight **out) {
     TH_REQUIRE(dev && shape && out, "th_upload: null argument");
+    TH_NOT_CAPTURING(dev, "th_upload");
     TH_REQUIRE(ndim == 1 || ndim == 2, "a weight has 1 or 2 dimensions, not %zu", ndim);
     size_t numel = 1;
     for (size_t i = 0; i < ndim; ++i) numel *= shape[i];
@@ -161,6 +230,10 @@ int th_upload(th_device *dev, const uint16_t *data, const size_t *shape, size_t 
 
 void th_weight_free(th_device *dev, th_weight *w) {
     if (!w) return;
+    if (dev && dev->capturing) {  // the handle stays valid: free it after th_graph_end
+        th::fail(TH_ERR_INVALID, "th_weight_free cannot run while the device's stream is being captured");
+        return;
+    }
     if (dev) (void)hipStreamSynchronize(dev->stream);
     if (w->ptr) (void)hipFree(w->ptr);
     delete w;
@@ -176,6 +249,7 @@ int th_weight_shape(const th_weight *w, size_t *shape, size_t *ndim) {
 
 int th_alloc(th_device *dev, size_t len, th_buffer **out) {
     TH_REQUIRE(dev && out, "th_alloc: null argument");
+    TH_NOT_CAPTURING(dev, "th_alloc");
     auto *b = new (std::nothrow) th_buffer();
     if (!b) return fail(TH_ERR_NOMEM, "out of host memory");
     size_t bytes = std::max<size_t>(len * sizeof(float), 16);
@@ -195,6 +269,10 @@ int th_alloc(th_device *dev, size_t len, th_buffer **out) {
 
 void th_buffer_free(th_device *dev, th_buffer *b) {
     if (!b) return;
+    if (dev && dev->capturing) {  // the handle stays valid: free it after th_graph_end
+        th::fail(TH_ERR_INVALID, "th_buffer_free cannot run while the device's stream is being captured");
+        return;
+    }
     if (dev) (void)hipStreamSynchronize(dev->stream);
     if (b->ptr) (void)hipFree(b->ptr);
     delete b;
@@ -212,6 +290,7 @@ size_t th_buffer_len(const th_buffer *b) { return b ? b->len : 0; }
 
 int th_read(th_device *dev, const th_buffer *b, float *out, size_t len) {
     TH_REQUIRE(dev && b, "th_read: null argument");
+    TH_NOT_CAPTURING(dev, "th_read");
     TH_REQUIRE(len == b->len, "reading %zu activations from a buffer of %zu", len, b->len);
     TH_REQUIRE(len == 0 || out, "th_read: null output");
     if (len) TH_HIP(hipMemcpyAsync(out, b->ptr, len * sizeof(float), hipMemcpyDeviceToHost, dev->stream));
@@ -222,6 +301,7 @@ int th_read(th_device *dev, const th_buffer *b, float *out, size_t len) {
 // model/titania.rs:133-137: data.len must equal the buffer's length.
 int th_write(th_device *dev, th_buffer *b, const float *data, size_t len) {
     TH_REQUIRE(dev && b, "th_write: null argument");
+    TH_NOT_CAPTURING(dev, "th_write");
     TH_REQUIRE(len == b->len, "writing %zu activations into a buffer of %zu", len, b->len);
     TH_REQUIRE(len == 0 || data, "th_write: null data");
     if (len) TH_HIP(hipMemcpyAsync(b->ptr, data, len * sizeof(float), hipMemcpyHostToDevice, dev->stream));
@@ -244,6 +324,7 @@ int th_copy(th_device *dev, th_buffer *dst, size_t dst_offset, const th_buffer *
 // model/cpu.rs:38-47 / model/titania.rs:145-151
 int th_embed(th_device *dev, th_buffer *out, const th_weight *table, const uint32_t *tokens, size_t n) {
     TH_REQUIRE(dev && out && table, "th_embed: null argument");
+    TH_NOT_CAPTURING(dev, "th_embed");
     TH_REQUIRE(table->ndim == 2, "an embedding table has 2 dimensions");
     size_t dim = table->shape[1];
     TH_REQUIRE(out->len == n * dim, "embedding %zu tokens of %zu into a buffer of %zu", n, dim, out->len);
@@ -266,6 +347,8 @@ int th_matmul(th_device *dev, th_buffer *out, const th_weight *w, const th_buffe
     TH_REQUIRE(x->len == n * cols, "x holds %zu activations, not a whole number of %zu-long rows", x->len, cols);
     TH_REQUIRE(out->len == n * rows, "out holds %zu activations, not %zu tokens x %zu rows", out->len, n, rows);
     TH_REQUIRE(out->ptr != x->ptr || n == 0, "matmul cannot write its input");
+    if (n >= th::kGemmMinTokens && th::gemm_supported(rows, cols))
+        TH_NOT_CAPTURING(dev, "a matmul of 16 or more tokens (stream-ordered scratch)");
     TH_HIP(th::launch_matmul(dev->stream, out->ptr, w->ptr, rows, cols, x->ptr, n));
     return TH_OK;
 }
@@ -366,6 +449,7 @@ int th_add_rmsnorm(th_device *dev, th_buffer *x, const th_buffer *y, th_buffer *
 
 int th_argmax(th_device *dev, const th_buffer *logits, uint32_t *token) {
     TH_REQUIRE(dev && logits && token, "th_argmax: null argument");
+    TH_NOT_CAPTURING(dev, "th_argmax");
     TH_REQUIRE(logits->len > 0, "argmax of an empty buffer");
     size_t m = th::argmax_partials(logits->len);
     auto *partials = static_cast<uint64_t *>(th::scratch(dev, m * sizeof(uint64_t)));
@@ -379,6 +463,7 @@ int th_argmax(th_device *dev, const th_buffer *logits, uint32_t *token) {
 int th_sample(th_device *dev, const th_buffer *logits, float temperature, size_t top_k, float top_p, uint64_t *rng,
               uint32_t *token) {
     TH_REQUIRE(dev && logits && rng && token, "th_sample: null argument");
+    TH_NOT_CAPTURING(dev, "th_sample");
     TH_REQUIRE(logits->len > 0, "sampling from an empty buffer");
     if (temperature == 0.0f) return th_argmax(dev, logits, token);
     const size_t k = std::min(std::max<size_t>(top_k, 1), logits->len);

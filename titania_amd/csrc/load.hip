@@ -424,6 +424,7 @@ int th_config_load(const char *path, th_config *out) {
 
 int th_model_load(th_device *dev, const char *dir, th_model **out) {
     TH_REQUIRE(dev && dir && out, "th_model_load: null argument");
+    TH_NOT_CAPTURING(dev, "th_model_load");
     const std::string d(dir);
     th_config c;
     TRY(parse_config(d + "/config.json", c));

@@ -800,6 +800,7 @@ extern "C" {
 int th_model_create(th_device *dev, const th_config *config, const th_weight *const *weights, size_t n_weights,
                     th_model **out) {
     TH_REQUIRE(dev && config && weights && out, "th_model_create: null argument");
+    TH_NOT_CAPTURING(dev, "th_model_create");
     const th_config &c = *config;
     TH_REQUIRE(c.hidden_size > 0 && c.intermediate_size > 0 && c.num_hidden_layers > 0 && c.num_attention_heads > 0 &&
                    c.num_key_value_heads > 0 && c.head_dim > 0 && c.vocab_size > 0,
@@ -852,6 +853,10 @@ int th_model_create(th_device *dev, const th_config *config, const th_weight *co
 
 void th_model_destroy(th_model *m) {
     if (!m) return;
+    if (m->dev->capturing) {  // the handle stays valid: destroy it after th_graph_end
+        th::fail(TH_ERR_INVALID, "th_model_destroy cannot run while the device's stream is being captured");
+        return;
+    }
     for (th_weight *w : m->owned) th_weight_free(m->dev, w);
     delete m;
 }
@@ -864,6 +869,7 @@ int th_model_config(const th_model *m, th_config *out) {
 
 int th_state_create(th_model *m, size_t max_len, int kv_dtype, th_state **out) {
     TH_REQUIRE(m && out, "th_state_create: null argument");
+    TH_NOT_CAPTURING(m->dev, "th_state_create");
     TH_REQUIRE(max_len > 0, "max_len must be positive");
     TH_REQUIRE(kv_dtype == TH_KV_F32 || kv_dtype == TH_KV_BF16, "unknown KV dtype %d", kv_dtype);
     auto *s = new (std::nothrow) th_state();
@@ -886,6 +892,10 @@ int th_state_create(th_model *m, size_t max_len, int kv_dtype, th_state **out) {
 void th_state_destroy(th_state *s) {
     if (!s) return;
     th_device *d = s->m->dev;
+    if (d->capturing) {  // the handle stays valid: destroy it after th_graph_end
+        th::fail(TH_ERR_INVALID, "th_state_destroy cannot run while the device's stream is being captured");
+        return;
+    }
     (void)hipStreamSynchronize(d->stream);
     if (s->graph_exec) (void)hipGraphExecDestroy(s->graph_exec);
     if (s->graph) (void)hipGraphDestroy(s->graph);
@@ -905,6 +915,7 @@ void th_state_destroy(th_state *s) {
 
 int th_forward(th_model *m, th_state *s, const uint32_t *tokens, size_t n, size_t pos, float *logits, int path) {
     TH_REQUIRE(m && s && s->m == m, "th_forward: null argument or a state of another model");
+    TH_NOT_CAPTURING(m->dev, "th_forward");
     TH_REQUIRE(n > 0 && tokens, "no tokens to run");  // model.rs:84
     TH_REQUIRE(pos + n <= s->max_len, "tokens past the end of the cache");  // model.rs:85
     TH_REQUIRE(path == TH_PATH_OPS || path == TH_PATH_FUSED, "unknown path %d", path);
@@ -925,6 +936,7 @@ int th_forward(th_model *m, th_state *s, const uint32_t *tokens, size_t n, size_
 
 int th_decode_trace(th_state *s, uint64_t *out, size_t cap, size_t *n) {
     TH_REQUIRE(s && n, "th_decode_trace: null argument");
+    TH_NOT_CAPTURING(s->m->dev, "th_decode_trace");
     *n = s->trace ? s->trace_words : 0;
     if (!s->trace || !out) return TH_OK;
     TH_REQUIRE(cap >= s->trace_words, "trace needs %zu words", s->trace_words);
@@ -949,6 +961,7 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
            bool *hit_stop = nullptr) {
     if (hit_stop) *hit_stop = false;
     TH_REQUIRE(m && s && s->m == m && out_tokens, "th_decode: null argument or a state of another model");
+    TH_NOT_CAPTURING(m->dev, "th_decode");
     TH_REQUIRE(n_stop <= (size_t)th::kStepMaxStops && (n_stop == 0 || stops), "at most %d stop tokens",
                th::kStepMaxStops);
     if (n_out) *n_out = 0;
@@ -1093,6 +1106,7 @@ int th_decode_sample(th_model *m, th_state *s, size_t pos, size_t steps, float t
 int th_generate(th_model *m, th_state *s, size_t pos, size_t max_tokens, const uint32_t *stop, size_t n_stop,
                 float temperature, size_t top_k, float top_p, uint64_t *rng, uint32_t *out_tokens, size_t *n_out) {
     TH_REQUIRE(m && n_out, "th_generate: null argument");
+    TH_NOT_CAPTURING(m->dev, "th_generate");
     *n_out = 0;
     TH_REQUIRE(n_stop >= 1 && n_stop <= (size_t)th::kStepMaxStops && stop, "th_generate: 1 to %d stop tokens",
                th::kStepMaxStops);

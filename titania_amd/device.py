@@ -41,12 +41,38 @@ class Weight:
 
     def free(self) -> None:
         if self.handle:
+            self._dev._refuse_while_capturing("free a weight")
             lib().th_weight_free(self._dev.handle, self.handle)
             self.handle = None
 
     def __del__(self):
         try:
             if self._dev.handle:
+                self.free()
+        except Exception:
+            pass
+
+
+class Graph:
+    """A captured sequence of device calls (th_graph_end): each launch() queues
+    one replay on the device's stream over the buffers named at capture time."""
+
+    def __init__(self, dev: "Hip", handle: int):
+        self._dev = dev
+        self.handle = handle
+
+    def launch(self) -> None:
+        check(lib().th_graph_launch(self._dev.handle, self.handle))
+
+    def free(self) -> None:
+        if self.handle:
+            self._dev._refuse_while_capturing("free a graph")
+            lib().th_graph_free(self._dev.handle, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self._dev.handle and not self._dev._capturing:
                 self.free()
         except Exception:
             pass
@@ -64,6 +90,7 @@ class Buffer:
 
     def free(self) -> None:
         if self.handle:
+            self._dev._refuse_while_capturing("free a buffer")
             lib().th_buffer_free(self._dev.handle, self.handle)
             self.handle = None
 
@@ -83,6 +110,7 @@ class Hip:
     """A GPU running the model's operations (the `hip` device)."""
 
     def __init__(self, ordinal: int = 0):
+        self._capturing = False
         h = C.c_void_p()
         check(lib().th_device_create(ordinal, C.byref(h)))
         self.handle = h.value
@@ -94,6 +122,25 @@ class Hip:
 
     def synchronize(self) -> None:
         check(lib().th_device_synchronize(self.handle))
+
+    # ---- HIP graphs of the device's stream (th_graph_*) ----
+
+    def graph_begin(self) -> None:
+        """Starts capturing: the compute calls that follow are recorded, not run,
+        until graph_end (calls that allocate, copy to or from the host or wait
+        raise meanwhile)."""
+        check(lib().th_graph_begin(self.handle))
+        self._capturing = True
+
+    def graph_end(self) -> Graph:
+        self._capturing = False
+        out = C.c_void_p()
+        check(lib().th_graph_end(self.handle, C.byref(out)))
+        return Graph(self, out.value)
+
+    def _refuse_while_capturing(self, what: str) -> None:
+        if self._capturing:
+            raise RuntimeError(f"cannot {what} while the device's stream is being captured (graph_begin)")
 
     def timer_begin(self) -> None:
         check(lib().th_timer_begin(self.handle))
