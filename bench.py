@@ -121,10 +121,22 @@ KERNEL_CONTEXTS = [512, 4096, 32768]
 ROTATE_BYTES = 1 << 30  # operand copies cycled per timed graph: well past the 256 MB last-level cache
 
 
-def _graph_time(dev, calls, reps: int = 3) -> float:
+def _graph_time(dev, calls, reps: int = 3, graph: bool = True) -> float:
     """Milliseconds of one replay of a graph holding `calls` (a list of
     zero-argument device calls), the median of `reps` timed replays after
-    one untimed replay."""
+    one untimed replay; without `graph`, of the calls launched one by one
+    (the host's launch rate then bounds short kernels)."""
+    if not graph:
+        for c in calls:
+            c()
+        dev.synchronize()
+        times = []
+        for _ in range(reps):
+            dev.timer_begin()
+            for c in calls:
+                c()
+            times.append(dev.timer_end())
+        return sorted(times)[len(times) // 2]
     dev.graph_begin()
     try:
         for c in calls:
@@ -142,7 +154,7 @@ def _graph_time(dev, calls, reps: int = 3) -> float:
     return sorted(times)[len(times) // 2]
 
 
-def kernel_bench(dev, seed: int) -> dict:
+def kernel_bench(dev, seed: int, graph: bool = True) -> dict:
     """Decode kernels alone: the GEMVs, RMSNorm and RoPE at the Qwen3-0.6B
     shapes (bf16 W and f32 x ~ N(0, 1)), and GQA decode attention (16 q heads,
     8 KV heads, head_dim 128) at contexts 512, 4096 and 32768 on the C ABI's
@@ -164,7 +176,7 @@ def kernel_bench(dev, seed: int) -> dict:
         dev.write(x, rng.standard_normal(cols).astype(np.float32))
         y = dev.alloc(rows)
         calls = [(lambda w=w: dev.matmul(y, w, x)) for w in ws] * max(1, 64 // copies)
-        ms = _graph_time(dev, calls)
+        ms = _graph_time(dev, calls, graph=graph)
         us = ms * 1000.0 / len(calls)
         nbytes = 2 * rows * cols + 4 * cols + 4 * rows
         out["gemv"].append({"kernel": name, "us": us, "bytes": nbytes, "GB/s": nbytes / us / 1e3,
@@ -185,7 +197,7 @@ def kernel_bench(dev, seed: int) -> dict:
     for name, call in [("rmsnorm 1 x 1024", lambda: dev.rmsnorm(xr, gain, 1e-6)),
                        ("rmsnorm 24 x 128 (q/k heads)", lambda: dev.rmsnorm(xh, hgain, 1e-6)),
                        ("rope 16 + 8 heads x 128", lambda: dev.rope(xh, tb, 4000, 24, 128))]:
-        ms = _graph_time(dev, [call] * 64)
+        ms = _graph_time(dev, [call] * 64, graph=graph)
         out["norm_rope"].append({"kernel": name, "us": ms * 1000.0 / 64})
     for b in (gain, hgain):
         b.free()
@@ -208,7 +220,7 @@ def kernel_bench(dev, seed: int) -> dict:
         dev.attention(o, q, ks[0], vs[0], ctx - 1, H, hd, KVH)  # sizes the device scratch before the capture
         calls = [(lambda k=k, v=v: dev.attention(o, q, k, v, ctx - 1, H, hd, KVH))
                  for k, v in zip(ks, vs)] * max(1, 32 // copies)
-        ms = _graph_time(dev, calls)
+        ms = _graph_time(dev, calls, graph=graph)
         us = ms * 1000.0 / len(calls)
         nbytes = kv_bytes + 2 * 4 * H * hd
         out["attention_f32_cache"].append({"context": ctx, "us": us, "bytes": nbytes, "GB/s": nbytes / us / 1e3,
@@ -363,6 +375,8 @@ def main() -> int:
                     help="instead of the decode benchmark, time the decode kernels alone (GEMVs, norms, RoPE, "
                          "attention at contexts 512 / 4096 / 32768) and whole-model decode after prompts of those "
                          "lengths; prints one JSON line")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="with --kernels, launch the calls one by one instead of replaying them in HIP graphs")
     ap.add_argument("--trace", type=int, default=0,
                     help="trace the first N timed steps of the persistent decode kernel and print a per-phase "
                          "breakdown to stderr")
@@ -388,7 +402,8 @@ def main() -> int:
     if args.kernels:
         dev = Hip(0)
         res = {"mode": "kernels", "data": "synthetic (seeded N(0,1) operands; model weights N(0,0.02))",
-               "peak_GB/s": HBM_PEAK_GBS, "isolated": kernel_bench(dev, args.seed)}
+               "peak_GB/s": HBM_PEAK_GBS, "graphs": not args.no_graph,
+               "isolated": kernel_bench(dev, args.seed, graph=not args.no_graph)}
         print(json.dumps(res["isolated"]), file=sys.stderr, flush=True)
         model = Model(dev, cfg, synth.weights(cfg, seed=args.seed))
         res["decode_after_prompt"] = {"model": args.model, "kv": args.kv, "steps": args.steps,
