@@ -24,6 +24,7 @@ constexpr size_t kAttnTileMin = 8; // tokens from which a launch uses the matrix
 constexpr size_t kMKTiles = 32;    // positions per key tile of the one-head-a-block kernel
 constexpr int kMQT = 64;           // tokens per block of that kernel
 constexpr int kGqaRows = 128, kGqaKeys = 64;  // (token, head) rows a block, keys a tile: GQA kernel
+constexpr size_t kRowPassH = 64;    // positions a pass of the few-token kernel (kRowPass)
 
 template <typename KV>
 __device__ __forceinline__ void load8(const KV *p, float f[8]);
@@ -185,6 +186,162 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnKernelArgs a) {
     }
 }
 
+// Attention of a few tokens (decode) with head_dim 128: one block per (token,
+// KV head, split of the positions); a split walks its positions in passes of
+// kRowPass rows whose keys and values every thread requests into registers at
+// once (the next pass's keys while this pass's softmax and P.V run). Keys:
+// thread t holds a quarter (32 dimensions) of row t / 4; the G query heads
+// come from LDS as broadcasts, and a quad of lanes sums a row's score. Values:
+// thread t holds dimensions 2 (t % 64) + {0, 1} of rows 16 (t / 64) + [0, 16)
+// and accumulates p . v for each head; the four row groups are summed in LDS
+// at the end. Scores, probabilities and the per-head statistics live in LDS.
+constexpr int kRowPass = (int)kRowPassH;
+
+template <typename KV>
+__global__ __launch_bounds__(256) void attn_rows_kernel(AttnKernelArgs a) {
+    constexpr int HD = 128, P = kRowPass, G_MAX = kAttnMaxGroup;
+    constexpr bool F32 = sizeof(KV) == 4;
+    constexpr int KV8 = 16 / sizeof(KV);  // elements of a 16-byte load
+    __shared__ __align__(16) float qs[G_MAX][HD];
+    __shared__ float sc[G_MAX][P];
+    __shared__ __align__(16) float red[4][G_MAX][HD];
+    __shared__ float st_m[G_MAX], st_l[G_MAX], st_a[G_MAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x % a.nsplit;
+    const int g = (blockIdx.x / a.nsplit) % a.n_kv_heads;
+    const long long t = blockIdx.x / (a.nsplit * a.n_kv_heads);
+    const int G = a.group;
+    const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
+    const long long len = pos + t + 1;  // the token attends up to its own position
+    const long long chunk = ((len + a.nsplit - 1) / a.nsplit + P - 1) / P * P;
+    const long long s0 = (long long)split * chunk;
+    const long long s1 = s0 + chunk < len ? s0 + chunk : len;
+    const KV *kb = reinterpret_cast<const KV *>(a.k) + (long long)g * a.head_stride;
+    const KV *vb = reinterpret_cast<const KV *>(a.v) + (long long)g * a.head_stride;
+
+    const int kr = tid >> 2, kq = tid & 3;     // key row, quarter of its dimensions
+    const int vd = 2 * (tid & 63), vq = tid >> 6;  // value dimension pair, row group
+    KV kreg[32];
+    float vreg[16][2];
+    auto fetch_k = [&](long long c0) {
+        const long long r = c0 + kr < s1 ? c0 + kr : s1 - 1;  // rows past the split repeat its last row
+        const uint4 *src = reinterpret_cast<const uint4 *>(kb + r * a.pos_stride + 32 * kq);
+#pragma unroll
+        for (int i = 0; i < 32 / KV8; ++i) reinterpret_cast<uint4 *>(kreg)[i] = src[i];
+    };
+    auto fetch_v = [&](long long c0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const long long r0 = c0 + 16 * vq + i, r = r0 < s1 ? r0 : s1 - 1;
+            const KV *src = vb + r * a.pos_stride + vd;
+            if constexpr (F32) {
+                const float2 v = *reinterpret_cast<const float2 *>(src);
+                vreg[i][0] = v.x;
+                vreg[i][1] = v.y;
+            } else {
+                const uint32_t w = *reinterpret_cast<const uint32_t *>(src);
+                vreg[i][0] = bf16_lo(w);
+                vreg[i][1] = bf16_hi(w);
+            }
+        }
+    };
+    if (s0 < s1) {
+        fetch_k(s0);
+        fetch_v(s0);
+    }
+    for (int i = tid; i < G * HD; i += 256)
+        qs[i / HD][i % HD] = a.q[((t * a.n_heads) + (long long)g * G + i / HD) * HD + i % HD];
+    if (tid < G_MAX) {
+        st_m[tid] = -INFINITY;
+        st_l[tid] = 0.f;
+    }
+    float acc[G_MAX][2];
+#pragma unroll
+    for (int gg = 0; gg < G_MAX; ++gg) acc[gg][0] = acc[gg][1] = 0.f;
+    __syncthreads();
+
+    for (long long c0 = s0; c0 < s1; c0 += P) {
+        // Scores of row c0 + kr for every head: a quad of lanes sums the quarters.
+        float kf[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) kf[j] = F32 ? (float)kreg[j] : bf16_to_f32((uint16_t)kreg[j]);
+        const bool row_in = c0 + kr < s1;
+#pragma unroll
+        for (int gg = 0; gg < G_MAX; ++gg) {
+            if (gg < G) {
+                const float4 *qv = reinterpret_cast<const float4 *>(&qs[gg][32 * kq]);
+                float d = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float4 q4 = qv[j];
+                    d = fmaf(q4.x, kf[4 * j], d);
+                    d = fmaf(q4.y, kf[4 * j + 1], d);
+                    d = fmaf(q4.z, kf[4 * j + 2], d);
+                    d = fmaf(q4.w, kf[4 * j + 3], d);
+                }
+                d += dpp_get<0xB1>(d, 0.f);
+                d += dpp_get<0x4E>(d, 0.f);
+                if (kq == 0) sc[gg][kr] = row_in ? a.scale * d : -INFINITY;
+            }
+        }
+        if (c0 + P < s1) fetch_k(c0 + P);
+        __syncthreads();
+        // Online softmax per head, one wave per head.
+        for (int gg = wave; gg < G; gg += 4) {
+            const float v = sc[gg][lane];
+            const float m_old = st_m[gg];
+            const float m_new = fmaxf(m_old, wave_max_dpp(v));
+            const float p = v == -INFINITY ? 0.f : expf(v - m_new);
+            sc[gg][lane] = p;
+            const float l = wave_sum_dpp(p);
+            if (lane == 0) {
+                const float al = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
+                st_a[gg] = al;
+                st_l[gg] = st_l[gg] * al + l;
+                st_m[gg] = m_new;
+            }
+        }
+        __syncthreads();
+        // acc = acc * alpha + p . v over this thread's 16 rows.
+#pragma unroll
+        for (int gg = 0; gg < G_MAX; ++gg) {
+            if (gg < G) {
+                const float al = st_a[gg];
+                float x0 = acc[gg][0] * al, x1 = acc[gg][1] * al;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float p = sc[gg][16 * vq + i];
+                    x0 = fmaf(p, vreg[i][0], x0);
+                    x1 = fmaf(p, vreg[i][1], x1);
+                }
+                acc[gg][0] = x0;
+                acc[gg][1] = x1;
+            }
+        }
+        if (c0 + P < s1) fetch_v(c0 + P);
+        __syncthreads();  // sc and st_a are rewritten by the next pass
+    }
+#pragma unroll
+    for (int gg = 0; gg < G_MAX; ++gg)
+        if (gg < G) *reinterpret_cast<float2 *>(&red[vq][gg][vd]) = make_float2(acc[gg][0], acc[gg][1]);
+    __syncthreads();
+    for (int i = tid; i < G * HD; i += 256) {
+        const int gg = i / HD, d = i % HD;
+        const float v = red[0][gg][d] + red[1][gg][d] + red[2][gg][d] + red[3][gg][d];
+        const long long h = (long long)g * G + gg;
+        if (a.nsplit == 1) {
+            a.out[(t * a.n_heads + h) * HD + d] = v / st_l[gg];
+        } else {
+            const long long slot = (t * a.n_heads + h) * a.nsplit + split;
+            a.part_acc[slot * HD + d] = v;
+            if (d == 0) {
+                a.part_ml[slot * 2] = st_m[gg];
+                a.part_ml[slot * 2 + 1] = st_l[gg];
+            }
+        }
+    }
+}
+
 // Merges the splits of one (token, head): rescales each split's sum and
 // accumulator by exp(m_split - m_max); empty splits (m = -inf) add nothing.
 // Every split's statistics and accumulator rows are read in parallel (threads
@@ -303,7 +460,12 @@ int attention_splits(size_t n, size_t n_heads, size_t n_kv_heads, size_t max_len
         while (ns < 8 && blocks * ns < 1024 && tiles >= 4 * ns) ns *= 2;
         return (int)ns;
     }
-    // Few tokens: split the positions until the launch has about 1024 blocks
+    // Few tokens, head_dim 128 (attn_rows_kernel): one split per pass of 64
+    // positions, at most 256 splits (longer contexts walk several passes a
+    // split).
+    if (head_dim == 128 && n_kv_heads && n_heads / n_kv_heads <= (size_t)kAttnMaxGroup)
+        return (int)std::max<size_t>(1, std::min<size_t>((max_len + kRowPassH - 1) / kRowPassH, 256));
+    // Otherwise split the positions until the launch has about 1024 blocks
     // (a block walks its positions one 256-row pass at a time, so short
     // splits in many blocks keep more rows in flight), each split covering at
     // least 64 positions, at most 256 splits.
@@ -869,7 +1031,12 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
 template <int HD>
 static hipError_t attn_launch(hipStream_t s, AttnKernelArgs k, size_t n) {
     dim3 grid((unsigned)(n * (size_t)k.n_kv_heads * (size_t)k.nsplit));
-    if (k.kv_bf16)
+    if (HD == 128 && k.group >= 1 && k.group <= kAttnMaxGroup) {
+        if (k.kv_bf16)
+            attn_rows_kernel<uint16_t><<<grid, 256, 0, s>>>(k);
+        else
+            attn_rows_kernel<float><<<grid, 256, 0, s>>>(k);
+    } else if (k.kv_bf16)
         attn_split_kernel<HD, uint16_t><<<grid, 256, 0, s>>>(k);
     else
         attn_split_kernel<HD, float><<<grid, 256, 0, s>>>(k);
