@@ -216,6 +216,27 @@ def test_qwen_prefill_gemm(hip, name, n):
     assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
 
 
+@pytest.mark.parametrize("rows,cols,n", [(6144, 1024, 2000), (4096, 6144, 1024)])
+def test_large_tile_gemm(hip, rows, cols, n):
+    """The 128 x 128 tile: a launch of 768 tiles with a ragged last token tile,
+    and a single matrix of 256 tiles and 96 K steps, which splits K in two.
+    Against a float64 product: the relative error bar and an elementwise
+    bound of a few fp32 ulps of the row."""
+    rng = np.random.default_rng(rows + cols + n)
+    wbits = normal_bf16(rows * cols, 106, "large")
+    x = rng.standard_normal(n * cols).astype(np.float32)
+    w64 = bf16_to_f32(wbits).astype(np.float64).reshape(rows, cols)
+    expected = (x.astype(np.float64).reshape(n, cols) @ w64.T).reshape(-1)
+    xb = hip.alloc(n * cols)
+    hip.write(xb, x)
+    out = hip.alloc(n * rows)
+    hip.matmul(out, hip.upload(Tensor((rows, cols), wbits)), xb)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-5
+    bound = (np.abs(x.astype(np.float64).reshape(n, cols)) @ np.abs(w64).T).reshape(-1)
+    assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
+
+
 def test_qwen_norms_and_rope(hip):
     # RMSNorm over 1024 and per head over 128 (16 q heads + 8 k heads), gains 1 + N(0, .1).
     for rows, dim, seed in [(1, 1024, 110), (16, 128, 111), (8, 128, 112)]:
@@ -258,6 +279,29 @@ def test_qwen_decode_attention(hip, ctx):
     got = hip.read(out)
     assert rel_error(got, expected) <= 1e-3
     assert_close(got, expected, rel=1e-4, abs_=1e-5, what=f"attention ctx={ctx}")
+
+
+@pytest.mark.parametrize("n,pos,H,KVH", [(1, 0, 16, 8), (2, 100, 16, 8), (7, 1000, 32, 8), (3, 63, 8, 8),
+                                         (5, 200, 16, 2), (1, 17000, 12, 4)])
+def test_few_token_attention(hip, n, pos, H, KVH):
+    """head_dim 128 with fewer tokens than the matrix-core kernels take: one
+    block per (token, KV head, 64-position split), groups of 1 to 8 heads, a
+    split boundary inside the context (pos 63, 1000), two passes a split
+    (17001 positions: more than 256 splits of 64)."""
+    hd = 128
+    L = pos + n
+    kv = bf16_to_f32(normal_bf16(L * KVH * hd, n + pos, "fk"))
+    vv = bf16_to_f32(normal_bf16(L * KVH * hd, n + pos, "fv"))
+    q = bf16_to_f32(normal_bf16(n * H * hd, n + pos, "fq"))
+    expected = ref.attention(q, kv, vv, pos, H, hd, KVH)
+    bk, bv, bq, out = hip.alloc(kv.size), hip.alloc(vv.size), hip.alloc(q.size), hip.alloc(q.size)
+    hip.write(bk, kv)
+    hip.write(bv, vv)
+    hip.write(bq, q)
+    hip.attention(out, bq, bk, bv, pos, H, hd, KVH)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-5
+    assert_close(got, expected, rel=1e-4, abs_=1e-5, what=f"few-token attention n={n} pos={pos}")
 
 
 def test_prefill_attention(hip):

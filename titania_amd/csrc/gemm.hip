@@ -253,17 +253,29 @@ namespace {
 // of one-block-a-CU tiles partly empty, and the small tile, two blocks a CU
 // over four times the grid, finishes first (measured on the Qwen3 prefill
 // shapes: 2048 tokens x 19456 x 2560 607 against 703 us, 512 tokens x 19456 x
-// 2560 203 against 180 us).
+// 2560 203 against 180 us). A single matrix with one to three large tiles a
+// CU and a deep K range (at least 96 steps) takes the large tile with K split
+// in two (2048 tokens x 2560 x 9728: 311 against 346 us; with 64 steps,
+// 2560 x 4096, the small tile stays ahead).
 constexpr size_t kLargeMinTiles = 768;
 
-bool use_large(size_t n, const GemmOut *outs, int n_outs, int ksplit) {
-    if (ksplit != 1) return false;
-    size_t total = 0;
-    for (int i = 0; i < n_outs; ++i) {
-        if (outs[i].rows % Large::BN) return false;
-        total += outs[i].rows;
-    }
-    return (total / Large::BN) * ((n + Large::BM - 1) / Large::BM) >= kLargeMinTiles;
+struct Plan {
+    bool large;
+    int ksplit;
+};
+
+Plan gemm_plan(size_t n, size_t rows, size_t cols, int n_outs, bool rows_large) {
+    const size_t nk = cols / BK;
+    const size_t lt = rows_large ? (rows / Large::BN) * ((n + Large::BM - 1) / Large::BM) : 0;
+    if (lt >= kLargeMinTiles) return {true, 1};
+    if (n_outs == 1 && lt >= kLargeMinTiles / 3 && nk >= 96) return {true, 2};
+    if (n_outs != 1) return {false, 1};
+    // Small tiles: a single matrix with few row tiles (o, down) splits K so
+    // that the launch still fills the chip, keeping at least 4 K steps a split.
+    const size_t tiles = (rows / Small::BN) * ((n + Small::BM - 1) / Small::BM);
+    int ksplit = 1;
+    while (ksplit < kGemmMaxSplitK && tiles * ksplit < 512 && (size_t)ksplit * 2 * 4 <= nk) ksplit *= 2;
+    return {false, ksplit};
 }
 
 }  // namespace
@@ -282,14 +294,8 @@ hipError_t launch_gemm_split(hipStream_t s, const float *x, size_t n, size_t col
     return hipGetLastError();
 }
 
-// A single matrix with few output tiles (o, down: 1024 rows) splits K so that
-// the launch still fills the chip, keeping at least 4 K steps per split.
 int gemm_ksplit(size_t n, size_t rows, size_t cols, int n_outs) {
-    if (n_outs != 1) return 1;
-    const size_t tiles = (rows / Small::BN) * ((n + Small::BM - 1) / Small::BM), nk = cols / BK;
-    int ksplit = 1;
-    while (ksplit < kGemmMaxSplitK && tiles * ksplit < 512 && (size_t)ksplit * 2 * 4 <= nk) ksplit *= 2;
-    return ksplit;
+    return gemm_plan(n, rows, cols, n_outs, rows % Large::BN == 0).ksplit;
 }
 
 hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
@@ -310,9 +316,12 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
     }
     sg.n = n_outs;
     if (total / Small::BN > 65535) return hipErrorInvalidValue;
-    if (use_large(n, outs, n_outs, ksplit)) {
-        dim3 grid((unsigned)(total / Large::BN), (unsigned)((n + Large::BM - 1) / Large::BM), 1);
-        gemm_large_kernel<<<grid, Large::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, 1);
+    bool rows_large = true;
+    for (int i = 0; i < n_outs; ++i) rows_large = rows_large && outs[i].rows % Large::BN == 0;
+    const Plan plan = gemm_plan(n, total, cols, n_outs, rows_large);
+    if (plan.large && plan.ksplit == ksplit) {
+        dim3 grid((unsigned)(total / Large::BN), (unsigned)((n + Large::BM - 1) / Large::BM), (unsigned)ksplit);
+        gemm_large_kernel<<<grid, Large::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
     } else {
         dim3 grid((unsigned)(total / Small::BN), (unsigned)((n + Small::BM - 1) / Small::BM), (unsigned)ksplit);
         gemm_kernel<<<grid, Small::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
