@@ -44,6 +44,13 @@ int gemm_ksplit(size_t n, size_t rows, size_t cols, int n_outs);
 hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
                           const GemmOut *outs, int n_outs, float *part, int ksplit);
 
+// The gate and up GEMMs on split activations hi/lo [n][cols] with the SiLU
+// epilogue of model/cpu.rs:151-155: h = silu(x . gate) * (x . up) for the
+// [inter, cols] gate and up, written as split_bf16 terms h_hi / h_lo
+// [n][inter] (the down projection's GEMM input). inter % 64 == 0.
+hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
+                            const uint16_t *gate, const uint16_t *up, size_t inter, uint16_t *h_hi, uint16_t *h_lo);
+
 // Bytes of scratch launch_gemm_multi needs for n tokens of `cols` columns and
 // single-matrix outputs of up to `rows` rows (room for the split-K partials).
 size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows);

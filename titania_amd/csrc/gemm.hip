@@ -90,11 +90,13 @@ struct Segs {
 };
 
 // Queues the loads of K step k0 into stage st: each wave fills whole 1 KB
-// spans (64 lanes x 16 B) of the stage. Token rows past n read row n - 1
+// spans (64 lanes x 16 B) of the stage. Weight rows [0, BN/2) of the tile
+// come from wa, the rest from wb. Token rows past n read row n - 1
 // (their results are never stored).
 template <class T>
 __device__ __forceinline__ void issue_step(typename T::Stage &st, const uint16_t *hi, const uint16_t *lo,
-                                           const uint16_t *w, int t0, int n, int cols, int k0) {
+                                           const uint16_t *wa, const uint16_t *wb, int t0, int n, int cols,
+                                           int k0) {
     static_assert(T::TA == T::TB, "square tiles: one span of each tile per iteration");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
@@ -105,7 +107,8 @@ __device__ __forceinline__ void issue_step(typename T::Stage &st, const uint16_t
         const size_t off = (size_t)t * cols + k0 + (pc ^ swz<T::CH>(row)) * 8;
         dma16(hi + off, st.hi + span * 64);
         dma16(lo + off, st.lo + span * 64);
-        dma16(w + (size_t)row * cols + k0 + (pc ^ swz<T::CH>(row)) * 8, st.w + span * 64);
+        const uint16_t *wr = row < T::BN / 2 ? wa + (size_t)row * cols : wb + (size_t)(row - T::BN / 2) * cols;
+        dma16(wr + k0 + (pc ^ swz<T::CH>(row)) * 8, st.w + span * 64);
     }
 }
 
@@ -124,6 +127,14 @@ struct SegTile {
     int rows, local;
 };
 
+// A paired tile (SiLU epilogue): weight rows [r0, r0 + BN/2) of gate and of
+// up, and the h = silu(gate) * up output as hi/lo terms [n][inter].
+struct PairTile {
+    const uint16_t *gate, *up;
+    uint16_t *h_hi, *h_lo;
+    int inter, r0;
+};
+
 __device__ __forceinline__ SegTile seg_tile(const Segs &s, int r0) {
     const int n0 = s.rows[0], n1 = s.rows[1];
     if (r0 < n0) return SegTile{s.w[0], s.out[0], n0, r0};
@@ -134,10 +145,10 @@ __device__ __forceinline__ SegTile seg_tile(const Segs &s, int r0) {
 // With ksplit > 1 (one matrix), block z of the grid's third dimension takes
 // K steps [z nk / ksplit, (z + 1) nk / ksplit) and stores its partial tile in
 // part[z][t][r]; the consumer sums the partials in z order.
-template <class T>
+template <class T, bool PAIRED = false>
 __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict__ hi,
                                           const uint16_t *__restrict__ lo, int n, int cols,
-                                          float *__restrict__ part, int ksplit) {
+                                          float *__restrict__ part, int ksplit, PairTile pt = {}) {
     constexpr int FM = T::FM, FN = T::FN, kStages = T::kStages;
     __shared__ typename T::Stage ring[kStages];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -147,7 +158,10 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
     const int fr = lane & 15, fq = lane >> 4;  // fragment row, quarter of the K slice
     const int nk_all = cols / T::BK, z = blockIdx.z;
     const int kb = (int)((long long)z * nk_all / ksplit), nk = (int)((long long)(z + 1) * nk_all / ksplit) - kb;
-    const uint16_t *w = sg.w + (size_t)rl * cols + (size_t)kb * T::BK;
+    const uint16_t *wa = PAIRED ? pt.gate + (size_t)pt.r0 * cols + (size_t)kb * T::BK
+                                : sg.w + (size_t)rl * cols + (size_t)kb * T::BK;
+    const uint16_t *wb = PAIRED ? pt.up + (size_t)pt.r0 * cols + (size_t)kb * T::BK
+                                : wa + (size_t)(T::BN / 2) * cols;
     hi += (size_t)kb * T::BK;
     lo += (size_t)kb * T::BK;
 
@@ -159,7 +173,7 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
 
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s)
-        if (s < nk) issue_step<T>(ring[s], hi, lo, w, t0, n, cols, s * T::BK);
+        if (s < nk) issue_step<T>(ring[s], hi, lo, wa, wb, t0, n, cols, s * T::BK);
 
     for (int k = 0; k < nk; ++k) {
         // This wave's loads of step k are done once at most the later steps'
@@ -169,7 +183,8 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
         else wait_vm<0>();
         stage_barrier();
         if (k + kStages - 1 < nk)
-            issue_step<T>(ring[(k + kStages - 1) % kStages], hi, lo, w, t0, n, cols, (k + kStages - 1) * T::BK);
+            issue_step<T>(ring[(k + kStages - 1) % kStages], hi, lo, wa, wb, t0, n, cols,
+                          (k + kStages - 1) * T::BK);
         const typename T::Stage &st = ring[k % kStages];
 #pragma unroll
         for (int ks = 0; ks < T::BK / 32; ++ks) {
@@ -192,6 +207,34 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
         }
     }
     // D[4 (l / 16) + i][l % 16]: token rows, weight-row columns.
+    if constexpr (PAIRED) {
+        // gate and up of a row sit in different waves: through LDS (the ring
+        // is free once every wave has left the K loop), then h = silu(g) * u
+        // as hi/lo terms, four outputs a thread.
+        constexpr int EPS = T::BN + 4, HALF = T::BN / 2;
+        static_assert(sizeof(ring) >= sizeof(float) * T::BM * EPS, "the epilogue tile fits the ring");
+        float *ep = reinterpret_cast<float *>(ring);
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < FM; ++m)
+#pragma unroll
+            for (int q = 0; q < FN; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ep[(wm + m * 16 + fq * 4 + i) * EPS + wn + q * 16 + fr] = acc[m][q][i];
+        __syncthreads();
+        for (int e = tid; e < T::BM * HALF / 4; e += T::NT) {
+            const int row = e / (HALF / 4), c = 4 * (e % (HALF / 4));
+            if (t0 + row >= n) continue;
+            const float4 g = *reinterpret_cast<const float4 *>(ep + row * EPS + c);
+            const float4 u = *reinterpret_cast<const float4 *>(ep + row * EPS + HALF + c);
+            uint2 h, l;
+            split_bf16x4(make_float4(silu(g.x) * u.x, silu(g.y) * u.y, silu(g.z) * u.z, silu(g.w) * u.w), h, l);
+            const size_t o = (size_t)(t0 + row) * pt.inter + pt.r0 + c;
+            *reinterpret_cast<uint2 *>(pt.h_hi + o) = h;
+            *reinterpret_cast<uint2 *>(pt.h_lo + o) = l;
+        }
+        return;
+    }
     const int rows = sg.rows;
     float *out = ksplit > 1 ? part + (size_t)z * n * rows : sg.out;
 #pragma unroll
@@ -215,6 +258,17 @@ __global__ __launch_bounds__(Large::NT, 1) void gemm_large_kernel(Segs sg, const
                                                               const uint16_t *__restrict__ lo, int n, int cols,
                                                               float *__restrict__ part, int ksplit) {
     gemm_tile<Large>(seg_tile(sg, blockIdx.x * Large::BN), hi, lo, n, cols, part, ksplit);
+}
+
+// gate and up in one launch, block x taking rows [x BN/2, (x + 1) BN/2) of
+// each, with the SiLU * up epilogue.
+template <class T>
+__global__ __launch_bounds__(T::NT, T::NT == 256 ? 2 : 1) void gemm_silu_kernel(
+    const uint16_t *__restrict__ gate, const uint16_t *__restrict__ up, const uint16_t *__restrict__ hi,
+    const uint16_t *__restrict__ lo, int n, int cols, int inter, uint16_t *__restrict__ h_hi,
+    uint16_t *__restrict__ h_lo) {
+    const PairTile pt{gate, up, h_hi, h_lo, inter, (int)blockIdx.x * (T::BN / 2)};
+    gemm_tile<T, true>(SegTile{}, hi, lo, n, cols, nullptr, 1, pt);
 }
 
 // split_bf16 of 4 elements a thread.
@@ -325,6 +379,26 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
     } else {
         dim3 grid((unsigned)(total / Small::BN), (unsigned)((n + Small::BM - 1) / Small::BM), (unsigned)ksplit);
         gemm_kernel<<<grid, Small::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
+                            const uint16_t *gate, const uint16_t *up, size_t inter, uint16_t *h_hi, uint16_t *h_lo) {
+    if (n == 0) return hipSuccess;
+    if (!hi || !lo || !gate || !up || !h_hi || !h_lo || !gemm_supported(inter, cols) || inter > ((size_t)1 << 24) ||
+        n > ((size_t)1 << 24) || (n + Small::BM - 1) / Small::BM > 65535 || inter % (Large::BN / 2) ||
+        ((uintptr_t)h_hi | (uintptr_t)h_lo) % 8)
+        return hipErrorInvalidValue;
+    const Plan plan = gemm_plan(n, 2 * inter, cols, 2, true);
+    if (plan.large) {
+        dim3 grid((unsigned)(inter / (Large::BN / 2)), (unsigned)((n + Large::BM - 1) / Large::BM));
+        gemm_silu_kernel<Large><<<grid, Large::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
+                                                           h_lo);
+    } else {
+        dim3 grid((unsigned)(inter / (Small::BN / 2)), (unsigned)((n + Small::BM - 1) / Small::BM));
+        gemm_silu_kernel<Small><<<grid, Small::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
+                                                           h_lo);
     }
     return hipGetLastError();
 }

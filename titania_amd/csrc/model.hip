@@ -496,9 +496,9 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
     const float *res = nullptr;
     int nres = 0;
     size_t res_stride = 0;
-    auto single_gemm = [&](const uint16_t *w, size_t cols, int ks) -> int {
+    auto single_gemm = [&](const uint16_t *w, size_t cols, int ks, const uint16_t *xh, const uint16_t *xl) -> int {
         const th::GemmOut o{w, H, s->fy};
-        TH_HIP(th::launch_gemm_hl(st, hi, lo, n, cols, &o, 1, part, ks));
+        TH_HIP(th::launch_gemm_hl(st, xh, xl, n, cols, &o, 1, part, ks));
         res = ks > 1 ? part : s->fy;
         nres = ks;
         res_stride = n * H;
@@ -571,13 +571,21 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         TH_HIP(th::launch_attention(st, aa, n, hd));
 
         if (hl) {
-            TRY(single_gemm(L.o->ptr, qd, ks_o));
+            TRY(single_gemm(L.o->ptr, qd, ks_o, hi, lo));
             TH_HIP(th::launch_add_rmsnorm_parts(st, s->fx, res, nres, res_stride, nullptr, hi, lo, n,
                                                 L.mlp_norm->ptr, H, eps));
-            const th::GemmOut o[2] = {{L.gate->ptr, I, s->fgate}, {L.up->ptr, I, s->fup}};
-            TH_HIP(th::launch_gemm_hl(st, hi, lo, n, H, o, 2, nullptr, 1));
-            TH_HIP(th::launch_silu_mul_split(st, s->fgate, s->fup, n * I, hi, lo));
-            TRY(single_gemm(L.down->ptr, I, ks_down));
+            if (I % 64 == 0) {
+                // gate/up with the SiLU * up epilogue, whose hi/lo output takes
+                // fgate's bytes (fb x I x 4).
+                uint16_t *h_hi = reinterpret_cast<uint16_t *>(s->fgate), *h_lo = h_hi + s->fb * I;
+                TH_HIP(th::launch_gemm_silu(st, hi, lo, n, H, L.gate->ptr, L.up->ptr, I, h_hi, h_lo));
+                TRY(single_gemm(L.down->ptr, I, ks_down, h_hi, h_lo));
+            } else {
+                const th::GemmOut o[2] = {{L.gate->ptr, I, s->fgate}, {L.up->ptr, I, s->fup}};
+                TH_HIP(th::launch_gemm_hl(st, hi, lo, n, H, o, 2, nullptr, 1));
+                TH_HIP(th::launch_silu_mul_split(st, s->fgate, s->fup, n * I, hi, lo));
+                TRY(single_gemm(L.down->ptr, I, ks_down, hi, lo));
+            }
             continue;
         }
         if (use_gemm(qd) && th::gemm_supported(H, qd)) {
