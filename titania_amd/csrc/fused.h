@@ -105,4 +105,41 @@ hipError_t launch_keep_logits(hipStream_t s, const float *logits, size_t vocab, 
 __device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }
 __device__ __forceinline__ void store_kv(uint16_t *p, float v) { *p = f32_to_bf16(v); }
 
+// The q/k post-processing of one (token, head) row of head_dim <= 512 by a
+// wave: lane i holds the RoPE pairs (i + 64 k, i + 64 k + head_dim/2) in
+// av[k], bv[k] (zero past head_dim/2). RMSNorm of the row with `gain` (if not
+// null; model/cpu.rs:85-94) and the rotation by the table row `ang`
+// (model/cpu.rs:96-111), in registers. The post kernel and the q/k/v GEMM's
+// epilogue share it, so both paths round alike.
+__device__ __forceinline__ void norm_rope_pairs(float av[4], float bv[4], int lane, int hd, const uint16_t *gain,
+                                                float eps, const float *ang) {
+    const int half = hd / 2;
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ss += av[k] * av[k] + bv[k] * bv[k];
+    if (gain) {
+        ss = wave_sum(ss);
+        const float scale = 1.0f / sqrtf(ss / (float)hd + eps);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = lane + 64 * k;
+            if (i < half) {
+                av[k] = av[k] * (scale * bf16_to_f32(gain[i]));
+                bv[k] = bv[k] * (scale * bf16_to_f32(gain[i + half]));
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = lane + 64 * k;
+        if (i < half) {
+            const float c = ang[2 * i], sn = ang[2 * i + 1];
+            const float x0 = av[k] * c - bv[k] * sn;
+            const float x1 = bv[k] * c + av[k] * sn;
+            av[k] = x0;
+            bv[k] = x1;
+        }
+    }
+}
+
 }  // namespace th

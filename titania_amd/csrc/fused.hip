@@ -29,42 +29,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkvPostArgs a)
 
     // Pairs i = lane, lane + 64, ... (at most 4 per lane: head_dim <= 512).
     float av[4], bv[4];
-    float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         int i = lane + 64 * k;
-        if (i < half) {
-            av[k] = src[i];
-            bv[k] = src[i + half];
-            ss += av[k] * av[k] + bv[k] * bv[k];
-        } else {
-            av[k] = bv[k] = 0.f;
-        }
+        av[k] = i < half ? src[i] : 0.f;
+        bv[k] = i < half ? src[i + half] : 0.f;
     }
-    if (gain) {
-        ss = wave_sum(ss);
-        const float scale = 1.0f / sqrtf(ss / (float)hd + a.eps);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int i = lane + 64 * k;
-            if (i < half) {
-                av[k] = av[k] * (scale * bf16_to_f32(gain[i]));
-                bv[k] = bv[k] * (scale * bf16_to_f32(gain[i + half]));
-            }
-        }
-    }
-    const float *ang = a.rope + pos * hd;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        int i = lane + 64 * k;
-        if (i < half) {
-            float c = ang[2 * i], s = ang[2 * i + 1];
-            float x0 = av[k] * c - bv[k] * s;
-            float x1 = bv[k] * c + av[k] * s;
-            av[k] = x0;
-            bv[k] = x1;
-        }
-    }
+    norm_rope_pairs(av, bv, lane, hd, gain, a.eps, a.rope + pos * hd);
     if (is_q) {
         float *dst = a.q + (t * a.n_heads + h) * hd;
 #pragma unroll

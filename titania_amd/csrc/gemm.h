@@ -51,6 +51,19 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
 hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
                             const uint16_t *gate, const uint16_t *up, size_t inter, uint16_t *h_hi, uint16_t *h_lo);
 
+// Whether the q/k/v GEMM of n tokens takes launch_gemm_qkv: head_dim 128 and
+// a launch the large tile would not take.
+bool gemm_qkv_fused(size_t n, size_t q_rows, size_t kv_rows, size_t cols, size_t head_dim);
+
+// The q, k and v GEMMs on split activations hi/lo [a.n][cols] (weights
+// [n_heads * 128, cols] and [n_kv_heads * 128, cols] x 2) with the
+// post-processing of launch_qk_norm_rope_append in the epilogue: q heads
+// RMSNorm'd and rotated into a.q, k heads RMSNorm'd, rotated and v heads
+// copied into the caches at positions pos + t. a.k and a.v are unused.
+struct QkvPostArgs;
+hipError_t launch_gemm_qkv(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t cols, const uint16_t *wq,
+                           const uint16_t *wk, const uint16_t *wv, const QkvPostArgs &a);
+
 // Bytes of scratch launch_gemm_multi needs for n tokens of `cols` columns and
 // single-matrix outputs of up to `rows` rows (room for the split-K partials).
 size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows);

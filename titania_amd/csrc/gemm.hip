@@ -24,6 +24,7 @@
 #include "gemm.h"
 
 #include "device_util.h"
+#include "fused.h"
 
 namespace th {
 namespace {
@@ -51,6 +52,7 @@ struct Tile {
 };
 using Small = Tile<64, 64, 64, 3>;    // 24 KB a stage: two blocks a CU
 using Large = Tile<128, 128, 64, 3, 4, 2>;  // 48 KB a stage: one block a CU, eight waves of 32 x 64
+using Head = Tile<32, 128, 64, 3>;          // one attention head's 128 rows: 24 KB a stage, two blocks a CU
 
 template <int CH>
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & (CH - 1); }
@@ -97,18 +99,37 @@ template <class T>
 __device__ __forceinline__ void issue_step(typename T::Stage &st, const uint16_t *hi, const uint16_t *lo,
                                            const uint16_t *wa, const uint16_t *wb, int t0, int n, int cols,
                                            int k0) {
-    static_assert(T::TA == T::TB, "square tiles: one span of each tile per iteration");
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    auto w_row = [&](int row) {
+        return row < T::BN / 2 ? wa + (size_t)row * cols : wb + (size_t)(row - T::BN / 2) * cols;
+    };
+    if constexpr (T::TA == T::TB) {
 #pragma unroll
-    for (int i = 0; i < T::TA / T::NT; ++i) {
-        const int span = wave * (T::TA / T::NT) + i;
-        const int p = span * 64 + lane, row = p / T::CH, pc = p % T::CH;
-        const int t = min(t0 + row, n - 1);
-        const size_t off = (size_t)t * cols + k0 + (pc ^ swz<T::CH>(row)) * 8;
-        dma16(hi + off, st.hi + span * 64);
-        dma16(lo + off, st.lo + span * 64);
-        const uint16_t *wr = row < T::BN / 2 ? wa + (size_t)row * cols : wb + (size_t)(row - T::BN / 2) * cols;
-        dma16(wr + k0 + (pc ^ swz<T::CH>(row)) * 8, st.w + span * 64);
+        for (int i = 0; i < T::TA / T::NT; ++i) {
+            const int span = wave * (T::TA / T::NT) + i;
+            const int p = span * 64 + lane, row = p / T::CH, pc = p % T::CH;
+            const int t = min(t0 + row, n - 1);
+            const size_t off = (size_t)t * cols + k0 + (pc ^ swz<T::CH>(row)) * 8;
+            dma16(hi + off, st.hi + span * 64);
+            dma16(lo + off, st.lo + span * 64);
+            dma16(w_row(row) + k0 + (pc ^ swz<T::CH>(row)) * 8, st.w + span * 64);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < T::TA / T::NT; ++i) {
+            const int span = wave * (T::TA / T::NT) + i;
+            const int p = span * 64 + lane, row = p / T::CH, pc = p % T::CH;
+            const int t = min(t0 + row, n - 1);
+            const size_t off = (size_t)t * cols + k0 + (pc ^ swz<T::CH>(row)) * 8;
+            dma16(hi + off, st.hi + span * 64);
+            dma16(lo + off, st.lo + span * 64);
+        }
+#pragma unroll
+        for (int i = 0; i < T::TB / T::NT; ++i) {
+            const int span = wave * (T::TB / T::NT) + i;
+            const int p = span * 64 + lane, row = p / T::CH, pc = p % T::CH;
+            dma16(w_row(row) + k0 + (pc ^ swz<T::CH>(row)) * 8, st.w + span * 64);
+        }
     }
 }
 
@@ -145,10 +166,22 @@ __device__ __forceinline__ SegTile seg_tile(const Segs &s, int r0) {
 // With ksplit > 1 (one matrix), block z of the grid's third dimension takes
 // K steps [z nk / ksplit, (z + 1) nk / ksplit) and stores its partial tile in
 // part[z][t][r]; the consumer sums the partials in z order.
-template <class T, bool PAIRED = false>
+// Epilogues: store the tile (or its split-K partial), SiLU * up of paired
+// gate/up rows, or the q/k/v post-processing of one attention head.
+enum Epi { kStoreTile, kSiluPairs, kQkvHead };
+
+// The head of a q/k/v head tile: role 0 q, 1 k, 2 v; index within the role.
+struct HeadTile {
+    const QkvPostArgs *a;
+    int role, head;
+};
+
+template <class T, int EPI = kStoreTile, typename KV = float>
 __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict__ hi,
                                           const uint16_t *__restrict__ lo, int n, int cols,
-                                          float *__restrict__ part, int ksplit, PairTile pt = {}) {
+                                          float *__restrict__ part, int ksplit, PairTile pt = {},
+                                          HeadTile ht = {}) {
+    constexpr bool PAIRED = EPI == kSiluPairs;
     constexpr int FM = T::FM, FN = T::FN, kStages = T::kStages;
     __shared__ typename T::Stage ring[kStages];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -162,6 +195,7 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
                                 : sg.w + (size_t)rl * cols + (size_t)kb * T::BK;
     const uint16_t *wb = PAIRED ? pt.up + (size_t)pt.r0 * cols + (size_t)kb * T::BK
                                 : wa + (size_t)(T::BN / 2) * cols;
+    (void)ht;
     hi += (size_t)kb * T::BK;
     lo += (size_t)kb * T::BK;
 
@@ -235,6 +269,48 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
         }
         return;
     }
+    if constexpr (EPI == kQkvHead) {
+        // The head's 128 columns of each token through LDS; then a wave per
+        // token: q and k heads get RMSNorm + RoPE at their position (q back
+        // to the attention's input, k to the cache), v heads go to the cache.
+        constexpr int EPS = T::BN + 4;
+        static_assert(T::BN == 128, "one head of 128 dimensions a tile");
+        static_assert(sizeof(ring) >= sizeof(float) * T::BM * EPS, "the epilogue tile fits the ring");
+        float *ep = reinterpret_cast<float *>(ring);
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < FM; ++m)
+#pragma unroll
+            for (int q = 0; q < FN; ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ep[(wm + m * 16 + fq * 4 + i) * EPS + wn + q * 16 + fr] = acc[m][q][i];
+        __syncthreads();
+        const QkvPostArgs &a = *ht.a;
+        const long long pos0 = a.pos_dev ? *a.pos_dev : a.pos;
+        for (int tl = wave; tl < T::BM; tl += T::NT / 64) {
+            const long long t = t0 + tl;
+            if (t >= n) break;
+            float av[4] = {ep[tl * EPS + lane], 0.f, 0.f, 0.f}, bv[4] = {ep[tl * EPS + 64 + lane], 0.f, 0.f, 0.f};
+            const long long pos = pos0 + t;
+            if (ht.role == 2) {
+                KV *vc = reinterpret_cast<KV *>(a.v_cache) + (long long)ht.head * a.head_stride + pos * a.pos_stride;
+                store_kv(vc + lane, av[0]);
+                store_kv(vc + lane + 64, bv[0]);
+                continue;
+            }
+            norm_rope_pairs(av, bv, lane, 128, ht.role == 0 ? a.q_norm : a.k_norm, a.eps, a.rope + pos * 128);
+            if (ht.role == 0) {
+                float *dst = a.q + (t * a.n_heads + ht.head) * 128;
+                dst[lane] = av[0];
+                dst[lane + 64] = bv[0];
+            } else {
+                KV *kc = reinterpret_cast<KV *>(a.k_cache) + (long long)ht.head * a.head_stride + pos * a.pos_stride;
+                store_kv(kc + lane, av[0]);
+                store_kv(kc + lane + 64, bv[0]);
+            }
+        }
+        return;
+    }
     const int rows = sg.rows;
     float *out = ksplit > 1 ? part + (size_t)z * n * rows : sg.out;
 #pragma unroll
@@ -268,7 +344,25 @@ __global__ __launch_bounds__(T::NT, T::NT == 256 ? 2 : 1) void gemm_silu_kernel(
     const uint16_t *__restrict__ lo, int n, int cols, int inter, uint16_t *__restrict__ h_hi,
     uint16_t *__restrict__ h_lo) {
     const PairTile pt{gate, up, h_hi, h_lo, inter, (int)blockIdx.x * (T::BN / 2)};
-    gemm_tile<T, true>(SegTile{}, hi, lo, n, cols, nullptr, 1, pt);
+    gemm_tile<T, kSiluPairs>(SegTile{}, hi, lo, n, cols, nullptr, 1, pt);
+}
+
+// q, k and v in one launch, block x taking attention head x of the
+// concatenation (q heads, then k, then v) for 32 tokens, with the q/k/v
+// post-processing epilogue (the work of qk_norm_rope_append).
+template <typename KV>
+__global__ __launch_bounds__(Head::NT, 2) void gemm_qkv_kernel(const uint16_t *__restrict__ wq,
+                                                               const uint16_t *__restrict__ wk,
+                                                               const uint16_t *__restrict__ wv,
+                                                               const uint16_t *__restrict__ hi,
+                                                               const uint16_t *__restrict__ lo, int n, int cols,
+                                                               QkvPostArgs a) {
+    const int h = blockIdx.x, nq = a.n_heads, nkv = a.n_kv_heads;
+    const int role = h < nq ? 0 : h < nq + nkv ? 1 : 2;
+    const int head = role == 0 ? h : role == 1 ? h - nq : h - nq - nkv;
+    const uint16_t *w = (role == 0 ? wq : role == 1 ? wk : wv) + (size_t)head * 128 * cols;
+    SegTile sg{w, nullptr, 128, 0};
+    gemm_tile<Head, kQkvHead, KV>(sg, hi, lo, n, cols, nullptr, 1, PairTile{}, HeadTile{&a, role, head});
 }
 
 // split_bf16 of 4 elements a thread.
@@ -400,6 +494,25 @@ hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *l
         gemm_silu_kernel<Small><<<grid, Small::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
                                                            h_lo);
     }
+    return hipGetLastError();
+}
+
+bool gemm_qkv_fused(size_t n, size_t q_rows, size_t kv_rows, size_t cols, size_t head_dim) {
+    return head_dim == 128 && q_rows % 128 == 0 && kv_rows % 128 == 0 && cols % BK == 0 &&
+           !gemm_plan(n, q_rows + 2 * kv_rows, cols, 3, true).large;
+}
+
+hipError_t launch_gemm_qkv(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t cols, const uint16_t *wq,
+                           const uint16_t *wk, const uint16_t *wv, const QkvPostArgs &a) {
+    if (a.n == 0) return hipSuccess;
+    if (!hi || !lo || !wq || !wk || !wv || a.head_dim != 128 || cols % BK || cols >= ((size_t)1 << 20) ||
+        a.n_heads < 1 || a.n_kv_heads < 1 || (a.n + Head::BM - 1) / Head::BM > 65535)
+        return hipErrorInvalidValue;
+    dim3 grid((unsigned)(a.n_heads + 2 * a.n_kv_heads), (unsigned)((a.n + Head::BM - 1) / Head::BM));
+    if (a.kv_bf16)
+        gemm_qkv_kernel<uint16_t><<<grid, Head::NT, 0, s>>>(wq, wk, wv, hi, lo, a.n, (int)cols, a);
+    else
+        gemm_qkv_kernel<float><<<grid, Head::NT, 0, s>>>(wq, wk, wv, hi, lo, a.n, (int)cols, a);
     return hipGetLastError();
 }
 

@@ -508,24 +508,6 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
     TH_HIP(th::launch_embed(st, s->fx, m->embed->ptr, H, tokens, n));
     for (size_t i = 0; i < m->layers.size(); ++i) {
         const Layer &L = m->layers[i];
-        // Residual add of the previous layer's MLP output, then the attention norm.
-        if (hl) {
-            TH_HIP(th::launch_add_rmsnorm_parts(st, s->fx, res, nres, res_stride, nullptr, hi, lo, n,
-                                                L.attn_norm->ptr, H, eps));
-            const th::GemmOut o[3] = {{L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
-            TH_HIP(th::launch_gemm_hl(st, hi, lo, n, H, o, 3, nullptr, 1));
-        } else {
-            TH_HIP(th::launch_add_rmsnorm(st, s->fx, i ? s->fy : nullptr, s->fxb, n, L.attn_norm->ptr, H, eps));
-            if (use_gemm(H) && th::gemm_supported(qd, H) && th::gemm_supported(nkv * hd, H)) {
-                const th::GemmOut o[3] = {
-                    {L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
-                TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 3, s->fsplit, s->fsplit_bytes));
-            } else {
-                TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
-                TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
-                TH_HIP(th::launch_matmul(st, s->fv, L.v->ptr, nkv * hd, H, s->fxb, n));
-            }
-        }
         th::QkvPostArgs qa{};
         qa.q = s->fq;
         qa.k = s->fk;
@@ -545,7 +527,32 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         qa.head_dim = (int)hd;
         qa.kv_bf16 = kv_bf16;
         qa.eps = eps;
-        TH_HIP(th::launch_qk_norm_rope_append(st, qa));
+        // Residual add of the previous layer's MLP output, then the attention norm.
+        if (hl) {
+            TH_HIP(th::launch_add_rmsnorm_parts(st, s->fx, res, nres, res_stride, nullptr, hi, lo, n,
+                                                L.attn_norm->ptr, H, eps));
+            if (th::gemm_qkv_fused(n, qd, nkv * hd, H, hd)) {
+                // q/k/v GEMM with the q/k norm + RoPE + KV append epilogue.
+                TH_HIP(th::launch_gemm_qkv(st, hi, lo, H, L.q->ptr, L.k->ptr, L.v->ptr, qa));
+            } else {
+                const th::GemmOut o[3] = {
+                    {L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
+                TH_HIP(th::launch_gemm_hl(st, hi, lo, n, H, o, 3, nullptr, 1));
+                TH_HIP(th::launch_qk_norm_rope_append(st, qa));
+            }
+        } else {
+            TH_HIP(th::launch_add_rmsnorm(st, s->fx, i ? s->fy : nullptr, s->fxb, n, L.attn_norm->ptr, H, eps));
+            if (use_gemm(H) && th::gemm_supported(qd, H) && th::gemm_supported(nkv * hd, H)) {
+                const th::GemmOut o[3] = {
+                    {L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};
+                TH_HIP(th::launch_gemm_multi(st, s->fxb, n, H, o, 3, s->fsplit, s->fsplit_bytes));
+            } else {
+                TH_HIP(th::launch_matmul(st, s->fq, L.q->ptr, qd, H, s->fxb, n));
+                TH_HIP(th::launch_matmul(st, s->fk, L.k->ptr, nkv * hd, H, s->fxb, n));
+                TH_HIP(th::launch_matmul(st, s->fv, L.v->ptr, nkv * hd, H, s->fxb, n));
+            }
+            TH_HIP(th::launch_qk_norm_rope_append(st, qa));
+        }
 
         th::AttnKernelArgs aa{};
         aa.out = s->fatt;
