@@ -451,7 +451,7 @@ def main() -> int:
     kernel = {
         "persistent": "decode step inside the persistent decode kernel (one launch for all steps)",
         "eager": "decode step (one token's kernels launched one by one)",
-    }.get(mode, "decode step (one HIP graph replay: one token's kernels)")
+    }.get(mode, "decode step (one token's kernels; HIP graphs of eight steps replayed)")
     traffic = measured_traffic(args.model, args.kv, mode)
 
     out = {
