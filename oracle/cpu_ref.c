@@ -4,7 +4,8 @@
  * pass that sequences them (model/model.rs).
  *
  * THIS IS TEST INFRASTRUCTURE. Only tests/, the smoke check and bench.py's
- * cpu_baseline leg load it, as the checker or as the timed CPU baseline. The
+ * cpu_baseline leg load it, as the results to compare against or as the timed
+ * CPU baseline. The
  * product path never links, loads or falls back to it.
  *
  * Floating-point semantics follow the Rust source exactly: no FMA contraction

@@ -1,7 +1,8 @@
 """ctypes binding of the CPU oracle (liboracle.so, built from cpu_ref.c).
 
 Test infrastructure: only tests/, the smoke check and bench.py's CPU-baseline
-leg use it, as the checker or as the timed baseline, never as the product.
+leg use it, as the results to compare against or as the timed baseline, never
+as the product.
 """
 
 from __future__ import annotations

@@ -4,7 +4,7 @@ The first group restates the reference's own differential tests
 (model/titania.rs:268-370): same shapes, same closed-form xorshift inputs, same
 tolerance |a - e| <= 1e-5 + 1e-4 |e|. The second runs the Qwen3-0.6B decode
 shapes (bf16 weights, f32 activations N(0, 1), seeded) and the GQA decode
-attention at contexts 512, 4096 and 32768, against the north-star bar of
+attention at contexts 512, 4096 and 32768, against the per-kernel bar of
 relative error <= 1e-3 (and tighter elementwise bounds where fp32 rounding
 allows).
 """

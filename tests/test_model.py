@@ -1,7 +1,7 @@
 """End-to-end parity of the forward pass and the greedy decode loop against the
 CPU oracle (model/model.rs:83-149 restated in oracle/cpu_ref.c).
 
-Bars (the north star's): final logits within 2e-2 max-abs, identical greedy
+Bars: final logits within 2e-2 max-abs of the oracle's, identical greedy
 token streams. A token stream may only differ at a step where the oracle's two
 largest logits are closer than the logit error bound; with fp32 caches the
 error is ~1e-5, so on these seeds the streams must match exactly.
