@@ -5,8 +5,7 @@
  *
  * THIS IS TEST INFRASTRUCTURE. Only tests/, the smoke check and bench.py's
  * cpu_baseline leg load it, as the results to compare against or as the timed
- * CPU baseline. The
- * product path never links, loads or falls back to it.
+ * CPU baseline. The product path never links, loads or falls back to it.
  *
  * Floating-point semantics follow the Rust source exactly: no FMA contraction
  * (build with -ffp-contract=off, no -ffast-math), every float sum a left fold
