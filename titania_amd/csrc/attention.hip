@@ -930,15 +930,17 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
         // Causal mask and online softmax of the lane's row; p overwrites st.
 #pragma unroll
         for (int s = 0; s < SETS; ++s) {
+            // Key c0 + 16 j + 4 lg + e is visible to the row when 16 j + e <=
+            // lim (32-bit: the tile holds 64 keys); a row past n sees none.
             const long long qpos = pos + t0 + qloc[s];
-            const bool in = qloc[s] < nq;
+            const long long d = qpos - c0 - 4 * lg;
+            const int lim = qloc[s] >= nq ? -1 : d > KT ? KT : (int)d;
             float mx = -INFINITY;
 #pragma unroll
             for (int j = 0; j < KT / 16; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const long long key = c0 + 16 * j + 4 * lg + e;
-                    const float v = in && key <= qpos ? st[s][j][e] * scale2 : -INFINITY;
+                    const float v = 16 * j + e <= lim ? st[s][j][e] * scale2 : -INFINITY;
                     st[s][j][e] = v;
                     mx = fmaxf(mx, v);
                 }
