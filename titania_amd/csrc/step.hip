@@ -384,9 +384,14 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
 // the first blocks, and after them one block per q head that attends from
 // those words. Blocks start in index order and the GEMV blocks never wait, so
 // the attention blocks' polls always end.
+// Rows a wave of the q/k/v GEMV blocks in qkv_attn_kernel (Qwen3-0.6B step:
+// 0.6114 ms with 2, 0.6094 with 4, 0.645 with 1; fewer GEMV blocks let the
+// attention blocks, which come after them, start sooner).
+constexpr int kQkvRowsPerWave = 4;
+
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
-    constexpr int RPW = 2, RPB = RPW * kWaves;
+    constexpr int RPW = kQkvRowsPerWave, RPB = RPW * kWaves;
     const int ngemv = (a.n_rows + RPB - 1) / RPB;
     const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
@@ -427,7 +432,8 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
 
 template <int CPL, int G>
 hipError_t qkv_attn_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a) {
-    dim3 grid((unsigned)((a.n_rows + 7) / 8 + q.at.n_heads * q.chunks));
+    constexpr int RPB = kQkvRowsPerWave * kWaves;
+    dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB + q.at.n_heads * q.chunks));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
         qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(q, a);
