@@ -44,6 +44,7 @@ struct GemvArgs {
 // One block: RPW rows per wave, CPL 16-byte chunks per lane per row.
 template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+    static_assert(EPI != kSiluPairs || RPW % 2 == 0, "a wave holds whole (gate, up) pairs");
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     __shared__ uint64_t red64[kWaves];
