@@ -126,7 +126,7 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs &a) {
     case 5: return gemv_launch<RPW, 5, PRO, EPI>(s, a);
     case 6: return gemv_launch<RPW, 6, PRO, EPI>(s, a);
     case 8: return gemv_launch<RPW, 8, PRO, EPI>(s, a);
-    case 19: return gemv_launch<(RPW > 1 ? 1 : RPW), 19, PRO, EPI>(s, a);
+    case 19: return gemv_launch<(RPW > 1 && EPI != kSiluPairs ? 1 : RPW), 19, PRO, EPI>(s, a);
     default: return hipErrorInvalidValue;
     }
 }
