@@ -312,44 +312,6 @@ def pmc_summary(fetch_dir: str, write_dir: str, steps: int, copy_mib: int) -> di
     return out
 
 
-PHASES = ["norm+qkv", "attention", "o+residual", "norm+gate/up", "down+residual"]
-
-
-def print_trace(trace, n_layers: int, steps: int) -> None:
-    """Per-phase timing of block 0 (microseconds, mean over the traced steps and
-    layers) from the persistent kernel's trace: waiting for the input, waiting
-    for staged weights, computing, publishing."""
-    if trace is None:
-        print("trace: not available (graph decode path)", file=sys.stderr)
-        return
-    import numpy as np
-
-    per = n_layers * 5 + 2
-    t = trace[1:].reshape(steps, per, 4).astype(np.int64)
-    start = int(trace[0])
-    rows = {}
-    prev_end = start
-    for s in range(steps):
-        for k in range(per):
-            name = PHASES[k % 5] if k < n_layers * 5 else ("lm_head" if k == n_layers * 5 else "pick")
-            p0, p1, p2, p3 = (int(v) for v in t[s, k])
-            p1 = p1 or p0
-            p2 = p2 or p1
-            wait = (p0 - prev_end) & 0xFFFFFFFF
-            parts = [wait, (p1 - p0) & 0xFFFFFFFF, (p2 - p1) & 0xFFFFFFFF, (p3 - p2) & 0xFFFFFFFF]
-            prev_end = p3
-            acc = rows.setdefault(name, [0, 0, 0, 0, 0])
-            for i in range(4):
-                acc[i] += parts[i] / 100.0
-            acc[4] += 1
-    total = sum(sum(v[:4]) for v in rows.values()) / steps
-    print(f"trace: {total:.1f} us per step (block 0); per phase: wait | staged | compute | publish (us)",
-          file=sys.stderr)
-    for name, (w, r, c, p, n) in rows.items():
-        print(f"  {name:14s} {w / n:6.2f} | {r / n:6.2f} | {c / n:6.2f} | {p / n:6.2f}   x{n // steps}/step "
-              f"= {(w + r + c + p) / steps:7.1f} us/step", file=sys.stderr)
-
-
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -377,12 +339,7 @@ def main() -> int:
                          "lengths; prints one JSON line")
     ap.add_argument("--no-graph", action="store_true",
                     help="with --kernels, launch the calls one by one instead of replaying them in HIP graphs")
-    ap.add_argument("--trace", type=int, default=0,
-                    help="trace the first N timed steps of the persistent decode kernel and print a per-phase "
-                         "breakdown to stderr")
     args = ap.parse_args()
-    if args.trace:
-        os.environ["TITANIA_TRACE"] = str(args.trace)
 
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary, steps=args.steps, copy_mib=args.calibrate_copy)))
@@ -449,7 +406,6 @@ def main() -> int:
     achieved = bytes_per_token / (gpu_ms / 1000.0 / K) / 1e9
     mode = os.environ.get("TITANIA_DECODE", "graph")
     kernel = {
-        "persistent": "decode step inside the persistent decode kernel (one launch for all steps)",
         "eager": "decode step (one token's kernels launched one by one)",
     }.get(mode, "decode step (one token's kernels; HIP graphs of eight steps replayed)")
     traffic = measured_traffic(args.model, args.kv, mode)
@@ -494,8 +450,6 @@ def main() -> int:
         cb = cpu_baseline(cfg, weights, prompt, K, args.cpu_repeats)
         out["parity_tokens_match"] = [int(x) for x in tokens] == cb.pop("tokens")
         out["cpu_baseline"] = cb
-    if args.trace:
-        print_trace(state.trace(), cfg.num_hidden_layers, args.trace)
     print(json.dumps(out))
     state.close()
     model.close()

@@ -229,16 +229,6 @@ TH_API int th_generate(th_model *model, th_state *state, size_t pos, size_t max_
                        size_t n_stop, float temperature, size_t top_k, float top_p, uint64_t *rng,
                        uint32_t *out_tokens, size_t *n_out);
 
-/* Phase trace of the last th_decode on the persistent path, when the state was
- * created with TITANIA_TRACE=<steps> in the environment: word 0 is the kernel's
- * start tick, then for each traced step and each phase (5 per layer: attention
- * norm + QKV, attention, o projection, MLP norm + gate/up, down; then output
- * projection and greedy pick) four ticks of block 0: its input arrived, its
- * staged weights were ready, it had computed, it had published (0 where a
- * phase has no such point; low 32 bits of the 100 MHz clock). Writes the word
- * count to *n (0 when tracing is off) and, if out is not NULL, the words. */
-TH_API int th_decode_trace(th_state *state, uint64_t *out, size_t cap, size_t *n);
-
 #ifdef __cplusplus
 }
 #endif

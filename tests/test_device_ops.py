@@ -198,14 +198,19 @@ QWEN_GEMM = {"q": (2048, 1024), "k/v": (1024, 1024), "o": (1024, 2048), "gate/up
 @pytest.mark.parametrize("n", [100, 512])
 def test_qwen_prefill_gemm(hip, name, n):
     """MFMA path with f32 activations that bf16 cannot hold exactly: the
-    relative error bar and an elementwise bound of a few fp32 ulps of the row."""
+    relative error bar and an elementwise bound of a few fp32 ulps of the row.
+    The o projection at 512 tokens takes the split-K plan of the small tile."""
     rows, cols = QWEN_GEMM[name]
-    if n == 512 and name not in ("q", "down"):
-        pytest.skip("one 512-token case per K size keeps the oracle fast")
     rng = np.random.default_rng(n + rows + cols)
     wbits = normal_bf16(rows * cols, 105, name)
     x = rng.standard_normal(n * cols).astype(np.float32)
-    expected = ref.matmul(wbits, rows, cols, x)
+    if n == 512 and name not in ("q", "down"):
+        # A float64 product stands in for the oracle here (faster); both
+        # bounds below hold against either.
+        w64 = bf16_to_f32(wbits).astype(np.float64).reshape(rows, cols)
+        expected = (x.astype(np.float64).reshape(n, cols) @ w64.T).reshape(-1)
+    else:
+        expected = ref.matmul(wbits, rows, cols, x)
     xb = hip.alloc(n * cols)
     hip.write(xb, x)
     out = hip.alloc(n * rows)
@@ -213,6 +218,34 @@ def test_qwen_prefill_gemm(hip, name, n):
     got = hip.read(out)
     assert rel_error(got, expected) <= 1e-5
     bound = _row_bound(wbits, rows, cols, x, n)
+    assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
+
+
+# The prefill GEMM shapes of Qwen3-4B, against a float64 product.
+QWEN4B_GEMM = {"q": (4096, 2560), "k/v": (1024, 2560), "o": (2560, 4096), "gate/up": (9728, 2560),
+               "down": (2560, 9728)}
+
+
+@pytest.mark.parametrize("name", list(QWEN4B_GEMM))
+@pytest.mark.parametrize("n", [100, 512, 2048])
+def test_qwen4b_prefill_gemm(hip, name, n):
+    """Every tile plan the Qwen3-4B shapes take: the small tile with and
+    without a K split (100 and 512 tokens) and, at 2048 tokens, the large
+    tile (gate/up) and the large tile with K split in two (down, 320 tiles
+    and 152 K steps)."""
+    rows, cols = QWEN4B_GEMM[name]
+    rng = np.random.default_rng(n + rows + cols + 7)
+    wbits = normal_bf16(rows * cols, 107, name)
+    x = rng.standard_normal(n * cols).astype(np.float32)
+    w64 = bf16_to_f32(wbits).astype(np.float64).reshape(rows, cols)
+    expected = (x.astype(np.float64).reshape(n, cols) @ w64.T).reshape(-1)
+    xb = hip.alloc(n * cols)
+    hip.write(xb, x)
+    out = hip.alloc(n * rows)
+    hip.matmul(out, hip.upload(Tensor((rows, cols), wbits)), xb)
+    got = hip.read(out)
+    assert rel_error(got, expected) <= 1e-5
+    bound = (np.abs(x.astype(np.float64).reshape(n, cols)) @ np.abs(w64).T).reshape(-1)
     assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
 
 

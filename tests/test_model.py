@@ -176,11 +176,12 @@ def decode_mode(request):
         os.environ["TITANIA_DECODE"] = old
 
 
-@pytest.mark.parametrize("decode_mode", ["persistent", "graph"], indirect=True)
+@pytest.mark.parametrize("decode_mode", ["graph", "eager"], indirect=True)
 @pytest.mark.parametrize("prompt_len,steps,kv", [(9, 24, TH_KV_F32), (300, 20, TH_KV_F32), (300, 12, TH_KV_BF16)])
 def test_tiny_decode_modes(tiny, decode_mode, prompt_len, steps, kv):
-    """Both decode implementations against the oracle, on one split of the
-    context and (past 256 positions) several splits merged on the device."""
+    """The captured decode step (graph replays) and the same kernels launched
+    one by one (eager) against the oracle, on one attention chunk of the
+    context and (past 256 positions) several chunks merged on the device."""
     m, r = tiny
     c = QWEN3_TINY
     prompt = synth.prompt(prompt_len, c.vocab_size, seed=prompt_len)
@@ -198,7 +199,7 @@ def test_tiny_decode_modes(tiny, decode_mode, prompt_len, steps, kv):
     st.close()
 
 
-# Eight KV heads (one per XCD) at a small size, for the XCD-parallel decode kernel.
+# Eight KV heads at a small size.
 QWEN3_TINY8 = Config(hidden_size=1024, intermediate_size=2048, num_hidden_layers=2, num_attention_heads=16,
                      num_key_value_heads=8, vocab_size=1000, head_dim_=128)
 
@@ -211,12 +212,13 @@ def tiny8(hip):
     m.close()
 
 
-@pytest.mark.parametrize("decode_mode", ["xcd", "graph"], indirect=True)
+@pytest.mark.parametrize("decode_mode", ["graph"], indirect=True)
 @pytest.mark.parametrize("prompt_len,steps,kv", [(9, 24, TH_KV_F32), (300, 16, TH_KV_F32), (300, 12, TH_KV_BF16),
                                                  (700, 8, TH_KV_F32)])
 def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
-    """Decode with one KV head per XCD against the oracle: one attention split
-    per head, and (700 positions) three splits merged by every block."""
+    """Decode with eight KV heads against the oracle: one attention chunk per
+    head, several chunks merged, and (700 positions) the split attention kernel
+    with its combine."""
     m, r = tiny8
     c = QWEN3_TINY8
     prompt = synth.prompt(prompt_len, c.vocab_size, seed=prompt_len + 1)
@@ -233,42 +235,6 @@ def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
     st.close()
 
 
-def test_xcd_mode_refuses_unsupported_shape(tiny, decode_mode_xcd):
-    """An explicit TITANIA_DECODE=xcd on a model without one KV head per XCD is an error, not a fallback."""
-    m, _ = tiny
-    st = State(m, 32)
-    m.forward(st, [1, 2, 3], 0, TH_PATH_FUSED, want_logits=False)
-    with pytest.raises(Exception, match="XCD"):
-        m.decode(st, 3, 2)
-    st.close()
-
-
-@pytest.fixture
-def decode_mode_xcd():
-    old = os.environ.get("TITANIA_DECODE")
-    os.environ["TITANIA_DECODE"] = "xcd"
-    yield "xcd"
-    if old is None:
-        del os.environ["TITANIA_DECODE"]
-    else:
-        os.environ["TITANIA_DECODE"] = old
-
-
-def test_qwen06_greedy_xcd(qwen06, decode_mode_xcd):
-    """Qwen3-0.6B shape on the XCD-parallel kernel: 32 greedy steps match the oracle."""
-    m, r = qwen06
-    c = QWEN3_0_6B
-    prompt = synth.prompt(16, c.vocab_size, seed=0)
-    steps = 32
-    st = State(m, 16 + steps)
-    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
-    toks, logits = m.decode(st, 16, steps, keep_logits=True)
-    rtoks, gaps, last = r.generate(r.state(16 + steps), prompt, steps)
-    err = float(np.max(np.abs(logits[-1] - last)))
-    assert err <= LOGIT_TOL, err
-    first_diff = next((i for i in range(steps) if toks[i] != rtoks[i]), None)
-    assert first_diff is None, (first_diff, float(gaps[first_diff]), err)
-    st.close()
 
 
 def _long_context_check(model, cfg, n_prompt, steps, kv, tol, seed):

@@ -93,7 +93,6 @@ SIGNATURES: dict[str, tuple] = {
     "th_decode_sample": (_I, [_P, _P, _SZ, _SZ, C.c_float, _SZ, C.c_float, C.POINTER(C.c_uint64), _P]),
     "th_generate": (_I, [_P, _P, _SZ, _SZ, _P, _SZ, C.c_float, _SZ, C.c_float, C.POINTER(C.c_uint64), _P,
                          C.POINTER(_SZ)]),
-    "th_decode_trace": (_I, [_P, _P, _SZ, C.POINTER(_SZ)]),
 }
 
 _lib: C.CDLL | None = None

@@ -1,6 +1,7 @@
 // The C ABI of the hip device: one entry point per method of the reference's
 // Device trait (model/device.rs:9-89), argument checks mirroring the
 // reference's asserts, and the fused extensions.
+#include <cstdint>
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
@@ -206,7 +207,9 @@ int th_upload(th_device *dev, const uint16_t *data, const size_t *shape, size_t 
     TH_NOT_CAPTURING(dev, "th_upload");
     TH_REQUIRE(ndim == 1 || ndim == 2, "a weight has 1 or 2 dimensions, not %zu", ndim);
     size_t numel = 1;
-    for (size_t i = 0; i < ndim; ++i) numel *= shape[i];
+    for (size_t i = 0; i < ndim; ++i)
+        TH_REQUIRE(!__builtin_mul_overflow(numel, shape[i], &numel) && numel <= SIZE_MAX / 2,
+                   "th_upload: the element count of the shape overflows");
     TH_REQUIRE(numel == 0 || data, "th_upload: null data");
     auto *w = new (std::nothrow) th_weight();
     if (!w) return fail(TH_ERR_NOMEM, "out of host memory");

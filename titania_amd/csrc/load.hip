@@ -5,6 +5,7 @@
 // safetensors: an 8-byte little-endian header length, a JSON header mapping
 // each tensor name to {dtype, shape, data_offsets} (plus "__metadata__"),
 // then the tensor bytes, offsets relative to the end of the header.
+#include <cstdint>
 #include <fcntl.h>
 #include <sys/stat.h>
 #include <unistd.h>
@@ -395,8 +396,12 @@ struct SafeTensors {
         const Entry &e = it->second;
         if (e.dtype != "BF16")
             return fail(TH_ERR_INVALID, "tensor '%s' is %s, expected BF16", name.c_str(), e.dtype.c_str());
+        // The element count and its byte size, refused when either overflows
+        // (a crafted shape could otherwise wrap to the size of its data).
         size_t n = 1;
-        for (size_t d : e.shape) n *= d;
+        for (size_t d : e.shape)
+            if (__builtin_mul_overflow(n, d, &n) || n > SIZE_MAX / 2)
+                return fail(TH_ERR_INVALID, "tensor '%s': the element count of its shape overflows", name.c_str());
         if (e.end - e.begin != 2 * (uint64_t)n)
             return fail(TH_ERR_INVALID, "tensor '%s': %llu bytes for %zu bf16 values", name.c_str(),
                         (unsigned long long)(e.end - e.begin), n);

@@ -17,12 +17,10 @@
 #include <cstdlib>
 
 #include "common.h"
-#include "decode.h"
 #include "fused.h"
 #include "gemm.h"
 #include "sample.h"
 #include "step.h"
-#include "xdecode.h"
 
 namespace {
 
@@ -87,23 +85,6 @@ struct th_state {
     hipGraph_t graph_n = nullptr;  // kGraphSteps decode steps
     hipGraphExec_t graph_n_exec = nullptr;
 
-    // The persistent decode kernel (when the shape allows it).
-    bool persistent = false;
-    int blocks = 0;
-    th::LayerWeights *dev_layers = nullptr;
-    unsigned long long *xchg = nullptr;  // all exchange buffers, one allocation
-    unsigned long long *xchg_x = nullptr, *xchg_qkv = nullptr, *xchg_att = nullptr, *xchg_h = nullptr,
-                       *xchg_am = nullptr;
-    float *att_part = nullptr;
-    unsigned *att_count = nullptr;
-    unsigned *status = nullptr;
-    unsigned epoch_base = 0;
-    int chunk = 256, n_splits = 1;
-    // The XCD-parallel decode kernel (TITANIA_DECODE=xcd, when the shape allows it).
-    bool xcd = false;
-    unsigned long long *xx = nullptr;  // all its exchange words, one allocation
-    unsigned long long *xx_x = nullptr, *xx_qkv = nullptr, *xx_att = nullptr, *xx_h = nullptr, *xx_part = nullptr,
-                       *xx_am = nullptr;
     // The captured decode step's buffers (fixed addresses for the graph).
     bool step_fused = false;
     float *sx_a = nullptr, *sx_b = nullptr, *s_y = nullptr, *s_qkv = nullptr, *s_att = nullptr, *s_o = nullptr,
@@ -118,9 +99,6 @@ struct th_state {
     th::SampleState *s_sample = nullptr;
     void *s_cand = nullptr;
     bool sampling = false;
-    unsigned long long *trace = nullptr;  // per-phase ticks of the last decode (TITANIA_TRACE steps)
-    int trace_steps = 0;
-    size_t trace_words = 0;
 };
 
 namespace {
@@ -236,79 +214,6 @@ int forward_batch_ops(th_state *s, const uint32_t *tokens, size_t n, size_t pos)
     return TH_OK;
 }
 
-// Resources of the persistent decode kernel: the layer table, the exchange
-// buffers (zeroed: epoch 0 precedes every epoch used), attention partials and
-// counters. Decode runs as a captured graph of step kernels unless
-// TITANIA_DECODE=persistent selects this kernel.
-int ensure_persistent(th_state *s) {
-    th_model *m = s->m;
-    const th_config &c = m->c;
-    const char *mode = getenv("TITANIA_DECODE");
-    s->blocks = th::decode_blocks(m->dev->ordinal);
-    s->persistent = mode && strcmp(mode, "persistent") == 0 &&
-                    th::decode_supported((int)c.hidden_size, (int)c.intermediate_size, (int)c.num_attention_heads,
-                                         (int)c.num_key_value_heads, (int)c.head_dim, (int)c.vocab_size, s->blocks);
-    s->xcd = mode && strcmp(mode, "xcd") == 0 &&
-             th::xdecode_supported((int)c.hidden_size, (int)c.intermediate_size, (int)c.num_attention_heads,
-                                   (int)c.num_key_value_heads, (int)c.head_dim, (int)c.vocab_size, s->blocks);
-    if (!s->persistent && !s->xcd) return TH_OK;
-    std::vector<th::LayerWeights> lw;
-    for (const Layer &L : m->layers)
-        lw.push_back({L.attn_norm->ptr, L.q->ptr, L.k->ptr, L.v->ptr, L.o->ptr, L.q_norm ? L.q_norm->ptr : nullptr,
-                      L.k_norm ? L.k_norm->ptr : nullptr, L.mlp_norm->ptr, L.gate->ptr, L.up->ptr, L.down->ptr});
-    TH_HIP(hipMalloc(&s->dev_layers, lw.size() * sizeof(th::LayerWeights)));
-    TH_HIP(hipMemcpy(s->dev_layers, lw.data(), lw.size() * sizeof(th::LayerWeights), hipMemcpyHostToDevice));
-    TH_HIP(hipMalloc(&s->status, 64));
-    TH_HIP(hipMemset(s->status, 0, 64));
-    s->epoch_base = 0;
-    const char *tr = getenv("TITANIA_TRACE");
-    s->trace_steps = tr ? std::max(0, atoi(tr)) : 0;
-    if (s->trace_steps) {
-        s->trace_words = th::decode_trace_words((int)c.num_hidden_layers, s->trace_steps);
-        TH_HIP(hipMalloc(&s->trace, s->trace_words * sizeof(unsigned long long)));
-        TH_HIP(hipMemset(s->trace, 0, s->trace_words * sizeof(unsigned long long)));
-    }
-    if (s->xcd) {
-        // Exchange words, zeroed (epoch 0 precedes every epoch used). Every
-        // XCD's region is a multiple of 256 bytes, so no cache line is written
-        // by two XCDs.
-        const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
-        const size_t G = (size_t)(c.num_attention_heads / c.num_key_value_heads), X = th::kXcds;
-        const size_t nx = X * H, nqkv = X * (G + 2) * hd, natt = X * th::kXBlocksPerXcd * G * (hd + 2),
-                     nh = I, npart = 2 * X * H, nam = 2 * (size_t)s->blocks;
-        auto up = [](size_t n) { return (n + 31) / 32 * 32; };
-        const size_t total = up(nx) + up(nqkv) + up(natt) + up(nh) + up(npart) + up(nam);
-        TH_HIP(hipMalloc(&s->xx, total * sizeof(unsigned long long)));
-        TH_HIP(hipMemset(s->xx, 0, total * sizeof(unsigned long long)));
-        s->xx_x = s->xx;
-        s->xx_qkv = s->xx_x + up(nx);
-        s->xx_att = s->xx_qkv + up(nqkv);
-        s->xx_h = s->xx_att + up(natt);
-        s->xx_part = s->xx_h + up(nh);
-        s->xx_am = s->xx_part + up(npart);
-        return TH_OK;
-    }
-    const size_t H = (size_t)c.hidden_size, I = (size_t)c.intermediate_size, hd = (size_t)c.head_dim;
-    const size_t qd = (size_t)c.num_attention_heads * hd, kvd = (size_t)c.num_key_value_heads * hd;
-    const size_t R = th::kReplicas;
-    const size_t nx = R * H, nqkv = qd + 2 * kvd, natt = R * qd, nh = R * I, nam = R * 2 * (size_t)s->blocks;
-    const size_t total = nx + nqkv + natt + nh + nam;
-    TH_HIP(hipMalloc(&s->xchg, total * sizeof(unsigned long long)));
-    TH_HIP(hipMemset(s->xchg, 0, total * sizeof(unsigned long long)));
-    s->xchg_x = s->xchg;
-    s->xchg_qkv = s->xchg_x + nx;
-    s->xchg_att = s->xchg_qkv + nqkv;
-    s->xchg_h = s->xchg_att + natt;
-    s->xchg_am = s->xchg_h + nh;
-    s->chunk = 256;
-    s->n_splits = (int)((s->max_len + s->chunk - 1) / s->chunk);
-    TH_HIP(hipMalloc(&s->att_part, (size_t)c.num_attention_heads * s->n_splits * (hd + 2) * sizeof(float)));
-    const size_t ncount = (size_t)c.num_hidden_layers * (size_t)c.num_key_value_heads;
-    TH_HIP(hipMalloc(&s->att_count, ncount * sizeof(unsigned)));
-    TH_HIP(hipMemset(s->att_count, 0, ncount * sizeof(unsigned)));
-    return TH_OK;
-}
-
 int ensure_fused_state(th_state *s) {
     if (s->fx) return TH_OK;
     th_model *m = s->m;
@@ -364,7 +269,7 @@ int ensure_fused_state(th_state *s) {
         TH_HIP(hipMemset(s->s_err, 0, sizeof(unsigned)));
 
     }
-    return ensure_persistent(s);
+    return TH_OK;
 }
 
 // What a pick writes for the next step of the fused step kernels: the picked
@@ -730,110 +635,6 @@ int capture_or_keep(th_state *s, bool keep, bool sampling) {
     return capture_steps(s, kGraphSteps, &s->graph_n, &s->graph_n_exec);
 }
 
-// All `steps` decode steps in one launch of the persistent kernel; the first
-// pick (from the logits the last forward left) runs just before it.
-int decode_persistent(th_state *s, size_t steps) {
-    th_model *m = s->m;
-    const th_config &c = m->c;
-    hipStream_t st = m->dev->stream;
-    TH_HIP(th::launch_pick(st, s->logits->ptr, (size_t)c.vocab_size, s->argmax_part, s->step, 0));
-    TH_HIP(hipMemsetAsync(s->status, 0, 64, st));
-    th::DecodeParams p{};
-    p.layers = s->dev_layers;
-    p.embed = m->embed->ptr;
-    p.norm = m->norm->ptr;
-    p.lm_head = m->out_proj()->ptr;
-    p.rope = s->rope->ptr;
-    p.kv = s->kv;
-    p.kv_bf16 = s->kv_dtype == TH_KV_BF16;
-    p.logits = s->logits->ptr;
-    p.step = s->step;
-    p.xchg_x = s->xchg_x;
-    p.xchg_qkv = s->xchg_qkv;
-    p.xchg_att = s->xchg_att;
-    p.xchg_h = s->xchg_h;
-    p.xchg_am = s->xchg_am;
-    p.att_part = s->att_part;
-    p.att_count = s->att_count;
-    p.status = s->status;
-    p.epoch_base = s->epoch_base;
-    p.steps = (int)steps;
-    p.hidden = (int)c.hidden_size;
-    p.intermediate = (int)c.intermediate_size;
-    p.n_layers = (int)c.num_hidden_layers;
-    p.n_heads = (int)c.num_attention_heads;
-    p.n_kv_heads = (int)c.num_key_value_heads;
-    p.head_dim = (int)c.head_dim;
-    p.vocab = (int)c.vocab_size;
-    p.max_len = (int)s->max_len;
-    p.chunk = s->chunk;
-    p.n_splits = s->n_splits;
-    p.eps = c.rms_norm_eps;
-    p.timeout_ticks = 200000000LL;  // 2 s at the 100 MHz reference clock
-    p.trace = s->trace;
-    p.trace_steps = s->trace_steps;
-    TH_HIP(th::launch_decode(st, p, s->blocks));
-    s->epoch_base += (unsigned)steps * th::decode_epochs_per_step((int)c.num_hidden_layers);
-    unsigned status[2] = {0, 0};
-    TH_HIP(hipMemcpyAsync(status, s->status, sizeof status, hipMemcpyDeviceToHost, st));
-    TH_HIP(hipStreamSynchronize(st));
-    if (status[0] || status[1])
-        return fail(TH_ERR_HIP, "persistent decode stopped: %u timeouts/aborts, %u protocol errors", status[0],
-                    status[1]);
-    return TH_OK;
-}
-
-// All `steps` decode steps in one launch of the XCD-parallel kernel; the first
-// pick (from the logits the last forward left) runs just before it.
-int decode_xcd(th_state *s, size_t steps) {
-    th_model *m = s->m;
-    const th_config &c = m->c;
-    hipStream_t st = m->dev->stream;
-    TH_HIP(th::launch_pick(st, s->logits->ptr, (size_t)c.vocab_size, s->argmax_part, s->step, 0));
-    TH_HIP(hipMemsetAsync(s->status, 0, 64, st));
-    th::XDecodeParams p{};
-    p.layers = s->dev_layers;
-    p.embed = m->embed->ptr;
-    p.norm = m->norm->ptr;
-    p.lm_head = m->out_proj()->ptr;
-    p.rope = s->rope->ptr;
-    p.kv = s->kv;
-    p.kv_bf16 = s->kv_dtype == TH_KV_BF16;
-    p.logits = s->logits->ptr;
-    p.step = s->step;
-    p.x_loc = s->xx_x;
-    p.qkv_loc = s->xx_qkv;
-    p.att_loc = s->xx_att;
-    p.h_loc = s->xx_h;
-    p.part = s->xx_part;
-    p.am = s->xx_am;
-    p.status = s->status;
-    p.epoch_base = s->epoch_base;
-    p.steps = (int)steps;
-    p.hidden = (int)c.hidden_size;
-    p.intermediate = (int)c.intermediate_size;
-    p.n_layers = (int)c.num_hidden_layers;
-    p.n_heads = (int)c.num_attention_heads;
-    p.n_kv_heads = (int)c.num_key_value_heads;
-    p.head_dim = (int)c.head_dim;
-    p.vocab = (int)c.vocab_size;
-    p.max_len = (int)s->max_len;
-    p.eps = c.rms_norm_eps;
-    p.timeout_ticks = 200000000LL;  // 2 s at the 100 MHz reference clock
-    p.trace = s->trace;
-    p.trace_steps = s->trace_steps;
-    TH_HIP(th::launch_xdecode(st, p, s->blocks));
-    s->epoch_base += (unsigned)steps * th::xdecode_epochs_per_step((int)c.num_hidden_layers);
-    unsigned status[3] = {0, 0, 0};
-    TH_HIP(hipMemcpyAsync(status, s->status, sizeof status, hipMemcpyDeviceToHost, st));
-    TH_HIP(hipStreamSynchronize(st));
-    if (status[2])
-        return fail(TH_ERR_HIP, "XCD decode: %u blocks ran on another XCD than their index implies", status[2]);
-    if (status[0] || status[1])
-        return fail(TH_ERR_HIP, "XCD decode stopped: %u timeouts/aborts, %u protocol errors", status[0], status[1]);
-    return TH_OK;
-}
-
 }  // namespace
 
 extern "C" {
@@ -948,8 +749,7 @@ void th_state_destroy(th_state *s) {
     for (th_buffer *b : s->v_cache) th_buffer_free(d, b);
     void *ptrs[] = {s->fx,      s->fxb,        s->fq,   s->fk,         s->fv,         s->fatt,
                     s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
-                    s->step,    s->tokens_dev, s->logits_dev, s->dev_layers, s->xchg, s->att_part,
-                    s->att_count, s->status, s->trace, s->xx, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
+                    s->step,    s->tokens_dev, s->logits_dev, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
                     s->s_att, s->s_o, s->s_h, s->s_part, s->s_words, s->s_err, s->fsplit, s->s_sample,
                     s->s_cand};
     for (void *p : ptrs) free_dev(p);
@@ -974,16 +774,6 @@ int th_forward(th_model *m, th_state *s, const uint32_t *tokens, size_t n, size_
     }
     if (logits) return th_read(m->dev, s->logits, logits, s->logits->len);
     TH_HIP(hipStreamSynchronize(m->dev->stream));
-    return TH_OK;
-}
-
-int th_decode_trace(th_state *s, uint64_t *out, size_t cap, size_t *n) {
-    TH_REQUIRE(s && n, "th_decode_trace: null argument");
-    TH_NOT_CAPTURING(s->m->dev, "th_decode_trace");
-    *n = s->trace ? s->trace_words : 0;
-    if (!s->trace || !out) return TH_OK;
-    TH_REQUIRE(cap >= s->trace_words, "trace needs %zu words", s->trace_words);
-    TH_HIP(hipMemcpy(out, s->trace, s->trace_words * sizeof(uint64_t), hipMemcpyDeviceToHost));
     return TH_OK;
 }
 
@@ -1049,8 +839,6 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
     if (sampling) TH_HIP(hipMemcpyAsync(s->s_sample, sp, sizeof *sp, hipMemcpyHostToDevice, st));
     TH_HIP(hipStreamSynchronize(st));  // `init` is a stack temporary
     const char *mode = getenv("TITANIA_DECODE");
-    if (mode && strcmp(mode, "xcd") == 0 && !s->xcd)
-        return fail(TH_ERR_INVALID, "TITANIA_DECODE=xcd: the XCD-parallel kernel does not support this model's shape");
     // The first pick comes from the logits the last forward left.
     auto first_pick = [&]() {
         return sampling ? th::launch_sample(st, s->logits->ptr, vocab, s->s_cand, s->s_sample, s->step, 0,
@@ -1077,11 +865,6 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
             launched += n;
             TRY(look());
         }
-    } else if (s->xcd && !sampling) {
-        TRY(decode_xcd(s, steps));
-        launched = steps;
-    } else if (s->persistent && !sampling) {
-        TRY(decode_persistent(s, steps));
     } else if (mode && strcmp(mode, "eager") == 0 && s->step_fused) {
         // The same step kernels launched one by one (no graph): for profilers
         // that do not follow graph launches.

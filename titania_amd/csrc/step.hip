@@ -109,15 +109,19 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
 hipError_t gemv_launch(hipStream_t s, const GemvArgs &a) {
     constexpr int RPB = RPW * kWaves;
-    const int rows = EPI == kSiluPairs ? a.n_rows : a.n_rows;
-    dim3 grid((unsigned)((rows + RPB - 1) / RPB));
+    dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB));
     gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, a.cols * sizeof(float), s>>>(a);
     return hipGetLastError();
 }
 
-// Dispatch on chunks per lane (cols / 512).
+// Dispatch on chunks per lane (cols / 512). Rows of 19 chunks (the 9728
+// columns of the Qwen3-4B down projection) keep one row a wave, or two for the
+// paired SiLU epilogue, to bound the registers that hold them; the output
+// projection's argmax partials assume four rows a wave, so its columns never
+// take that case (step_supported keeps hidden sizes to at most 8 chunks).
 template <int RPW, Prologue PRO, Epilogue EPI>
 hipError_t gemv_dispatch(hipStream_t s, const GemvArgs &a) {
+    static_assert(EPI != kLogits || RPW == 4, "the argmax partials count blocks of four rows a wave");
     switch (a.cols / 512) {
     case 1: return gemv_launch<RPW, 1, PRO, EPI>(s, a);
     case 2: return gemv_launch<RPW, 2, PRO, EPI>(s, a);
@@ -126,7 +130,9 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs &a) {
     case 5: return gemv_launch<RPW, 5, PRO, EPI>(s, a);
     case 6: return gemv_launch<RPW, 6, PRO, EPI>(s, a);
     case 8: return gemv_launch<RPW, 8, PRO, EPI>(s, a);
-    case 19: return gemv_launch<(RPW > 1 && EPI != kSiluPairs ? 1 : RPW), 19, PRO, EPI>(s, a);
+    case 19:
+        if (EPI == kLogits) return hipErrorInvalidValue;
+        return gemv_launch<(RPW > 1 && EPI != kSiluPairs ? 1 : RPW), 19, PRO, EPI>(s, a);
     default: return hipErrorInvalidValue;
     }
 }
@@ -381,9 +387,9 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
     attend<HD, G, KV, false, kStageRows>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, nullptr, 0, nullptr);
 }
 
-// The q/k/v rows of launch_step_qkv (two per wave) published as epoch words by
-// the first blocks, and after them one block per q head that attends from
-// those words. Blocks start in index order and the GEMV blocks never wait, so
+// The q/k/v rows of launch_step_qkv (kQkvRowsPerWave per wave) published as
+// epoch words by the first blocks, and after them one block per q head and
+// chunk of the cache that attends from those words. Blocks start in index order and the GEMV blocks never wait, so
 // the attention blocks' polls always end.
 // Rows a wave of the q/k/v GEMV blocks in qkv_attn_kernel (Qwen3-0.6B step:
 // 0.6114 ms with 2, 0.6094 with 4, 0.645 with 1; fewer GEMV blocks let the
@@ -491,11 +497,14 @@ bool step_supported(int hidden, int intermediate, int n_heads, int n_kv_heads, i
     if (head_dim != 128 || n_kv_heads <= 0 || n_heads % n_kv_heads) return false;
     const int g = n_heads / n_kv_heads;
     if (g != 1 && g != 2 && g != 4 && g != 8) return false;
+    // Input lengths of the GEMVs: hidden (q/k/v, gate/up, output projection),
+    // n_heads * head_dim (o) and intermediate (down); only the down projection
+    // takes rows of 19 chunks (9728 columns).
     const int cols[3] = {hidden, n_heads * head_dim, intermediate};
-    for (int c : cols) {
-        if (c % 512) return false;
-        const int cpl = c / 512;
-        if (cpl > 8 && cpl != 19) return false;
+    for (int i = 0; i < 3; ++i) {
+        if (cols[i] % 512) return false;
+        const int cpl = cols[i] / 512;
+        if (cpl > 8 && !(i == 2 && cpl == 19)) return false;
     }
     return true;
 }

@@ -127,17 +127,6 @@ class State:
         self.handle = out.value
         self.max_len = max_len
 
-    def trace(self) -> np.ndarray | None:
-        """Phase ticks (100 MHz) of the last persistent decode, or None when
-        tracing is off (set TITANIA_TRACE=<steps> before creating the state)."""
-        n = C.c_size_t()
-        check(lib().th_decode_trace(self.handle, None, 0, C.byref(n)))
-        if n.value == 0:
-            return None
-        out = np.empty(n.value, dtype=np.uint64)
-        check(lib().th_decode_trace(self.handle, out.ctypes.data, n.value, C.byref(n)))
-        return out
-
     def close(self) -> None:
         if self.handle:
             lib().th_state_destroy(self.handle)
