@@ -88,6 +88,19 @@ TH_API int th_rope(th_device *dev, th_buffer *x, const th_buffer *table, size_t 
 /* model/device.rs:68-85 `attention`: caches laid out [position][n_kv_heads][head_dim]. */
 TH_API int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
                  const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads);
+/* th_attention without any allocation: its split partials go to a fixed
+ * 8 MiB array that the library holds on each GPU until the process ends, so
+ * that callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc) can call it. No counterpart
+ * in model/device.rs. Same arguments, checks and results as th_attention; a
+ * call whose partials need more than 8 MiB (n * n_heads * splits *
+ * (head_dim + 2) floats: e.g. one token of 64 heads at any context fits, a
+ * 2048-token prompt does not) returns TH_ERR_INVALID. Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (two device handles of one GPU, two
+ * threads) race. */
+TH_API int th_attention_noalloc(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
+                                const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim,
+                                size_t n_kv_heads);
 /* model/device.rs:87-88 `silu_mul`: gate = silu(gate) * up. */
 TH_API int th_silu_mul(th_device *dev, th_buffer *gate, const th_buffer *up);
 

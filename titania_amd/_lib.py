@@ -77,6 +77,7 @@ SIGNATURES: dict[str, tuple] = {
     "th_rmsnorm": (_I, [_P, _P, _P, C.c_float]),
     "th_rope": (_I, [_P, _P, _P, _SZ, _SZ, _SZ]),
     "th_attention": (_I, [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ]),
+    "th_attention_noalloc": (_I, [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ]),
     "th_silu_mul": (_I, [_P, _P, _P]),
     "th_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, C.c_float]),
     "th_argmax": (_I, [_P, _P, C.POINTER(C.c_uint32)]),

@@ -21,6 +21,9 @@ struct th_device {
     // demand outside graph capture.
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // The device address of the no-alloc entry points' fixed array (looked up
+    // once, at th_device_create, with this device current).
+    void *noalloc_scratch = nullptr;
     // One u32 the argmax kernels leave their result in.
     uint32_t *token_out = nullptr;
     // th_timer_begin / th_timer_end.
@@ -54,6 +57,11 @@ void clear_error();
 
 // Makes sure the device scratch holds at least `bytes`; returns its pointer or null.
 void *scratch(th_device *dev, size_t bytes);
+
+// The fixed array of the no-alloc entry points: its size, and its address on
+// the current device.
+size_t noalloc_scratch_bytes();
+int noalloc_scratch_address(void **ptr);
 
 }  // namespace th
 

@@ -94,6 +94,10 @@ int th_device_create(int ordinal, th_device **out) {
     if (!dev) return fail(TH_ERR_NOMEM, "out of host memory");
     dev->ordinal = ordinal;
     dev->num_cus = prop.multiProcessorCount;
+    if (th::noalloc_scratch_address(&dev->noalloc_scratch) != TH_OK) {  // the message is set
+        delete dev;
+        return TH_ERR_HIP;
+    }
     hipError_t e = hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&dev->token_out, 256);
     if (e == hipSuccess) e = hipEventCreate(&dev->ev_begin);
@@ -386,8 +390,14 @@ int th_rope(th_device *dev, th_buffer *x, const th_buffer *table, size_t pos, si
 }
 
 // model/cpu.rs:113-149 / model/titania.rs:186-209
-int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
-                 const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads) {
+}  // extern "C"
+
+namespace {
+
+// th_attention, with its split partials in the device's growable scratch, or
+// (fixed) in the no-alloc array, refusing calls whose partials outgrow it.
+int attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache, const th_buffer *v_cache,
+              size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads, bool fixed) {
     TH_REQUIRE(dev && out && q && k_cache && v_cache, "th_attention: null argument");
     TH_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
                "%zu query heads do not split into groups over %zu KV heads", n_heads, n_kv_heads);
@@ -405,7 +415,12 @@ int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_bu
     int nsplit = th::attention_splits(n, n_heads, n_kv_heads, pos + n, head_dim);
     size_t floats = th::attention_scratch(n, n_heads, head_dim, nsplit);
     float *scr = nullptr;
-    if (floats) {
+    if (floats && fixed) {
+        TH_REQUIRE(floats * sizeof(float) <= th::noalloc_scratch_bytes(),
+                   "th_attention_noalloc: %zu bytes of split partials exceed its fixed %zu-byte scratch",
+                   floats * sizeof(float), th::noalloc_scratch_bytes());
+        scr = static_cast<float *>(dev->noalloc_scratch);
+    } else if (floats) {
         scr = static_cast<float *>(th::scratch(dev, floats * sizeof(float)));
         if (!scr) return fail(TH_ERR_NOMEM, "no scratch for attention (%zu floats)", floats);
     }
@@ -428,6 +443,20 @@ int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_bu
     a.part_ml = scr ? scr + n * n_heads * (size_t)nsplit * head_dim : nullptr;
     TH_HIP(th::launch_attention(dev->stream, a, n, head_dim));
     return TH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
+                 const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads) {
+    return attention(dev, out, q, k_cache, v_cache, pos, n_heads, head_dim, n_kv_heads, false);
+}
+
+int th_attention_noalloc(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
+                         const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads) {
+    return attention(dev, out, q, k_cache, v_cache, pos, n_heads, head_dim, n_kv_heads, true);
 }
 
 // model/cpu.rs:151-155 (zip: the shorter length)

@@ -203,6 +203,13 @@ class Hip:
         check(lib().th_attention(self.handle, out.handle, q.handle, k_cache.handle, v_cache.handle, int(pos),
                                  int(n_heads), int(head_dim), int(n_kv_heads)))
 
+    def attention_noalloc(self, out: Buffer, q: Buffer, k_cache: Buffer, v_cache: Buffer, pos: int, n_heads: int,
+                          head_dim: int, n_kv_heads: int) -> None:
+        """attention() with its split partials in the library's fixed per-GPU
+        array (no allocation); calls whose partials exceed it raise."""
+        check(lib().th_attention_noalloc(self.handle, out.handle, q.handle, k_cache.handle, v_cache.handle,
+                                         int(pos), int(n_heads), int(head_dim), int(n_kv_heads)))
+
     def silu_mul(self, gate: Buffer, up: Buffer) -> None:
         check(lib().th_silu_mul(self.handle, gate.handle, up.handle))
 
