@@ -9,6 +9,7 @@ from pathlib import Path
 
 import pytest
 
+import cabi
 from titania_amd import _lib
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "titania_hip.h"
@@ -35,6 +36,62 @@ def test_library_exports_every_declared_symbol():
 
 def test_binding_matches_header():
     assert sorted(_lib.SIGNATURES) == declared()
+
+
+def test_ctypes_argtypes_match_header():
+    """Every ctypes restype and argtype against the header's declaration: the
+    same number of arguments, each of the same kind (pointer, size_t, int,
+    float, fixed-width integer)."""
+    header = cabi.header_signatures()
+    bound = cabi.ctypes_signatures(_lib.SIGNATURES)
+    bad = {n: (cabi.as_ctypes_kinds(header[n]), bound[n]) for n in header
+           if cabi.as_ctypes_kinds(header[n]) != bound[n]}
+    assert not bad, bad
+
+
+def test_rust_sys_crate_matches_header():
+    """The Rust FFI crate's extern block (titania_amd/rust/hip-sys/lib.rs,
+    not compiled here) declares every header function with the same argument
+    count and kinds and the same return kind."""
+    header = cabi.header_signatures()
+    rust = cabi.rust_signatures()
+    assert sorted(rust) == sorted(header)
+    bad = {n: (header[n], rust[n]) for n in header if header[n] != rust[n]}
+    assert not bad, bad
+
+
+def test_signature_parsers_see_a_planted_mismatch(tmp_path):
+    """The checks above can fail: a copy of the crate with one argument
+    dropped and one changed from usize to i32 is caught."""
+    text = cabi.RUST_SYS.read_text()
+    text = text.replace("pub fn th_buffer_len(buf: *const th_buffer) -> usize;", "pub fn th_buffer_len() -> usize;")
+    text = text.replace("pub fn th_resize(dev: *mut th_device, buf: *mut th_buffer, len: usize)",
+                        "pub fn th_resize(dev: *mut th_device, buf: *mut th_buffer, len: i32)")
+    p = tmp_path / "lib.rs"
+    p.write_text(text)
+    rust = cabi.rust_signatures(p)
+    header = cabi.header_signatures()
+    assert rust["th_buffer_len"] != header["th_buffer_len"]
+    assert rust["th_resize"] != header["th_resize"]
+    assert rust["th_read"] == header["th_read"]
+
+
+# The methods of model/device.rs:9-89 `trait Device`.
+TRAIT_METHODS = ["upload", "alloc", "resize", "read", "write", "copy", "embed", "matmul", "add", "rmsnorm", "rope",
+                 "attention", "silu_mul"]
+
+
+def test_rust_device_impl_covers_the_trait():
+    """titania_amd/rust/model/hip.rs implements every trait method, each
+    through the header function of the same name, and calls only functions
+    the header declares."""
+    text = (cabi.ROOT / "titania_amd" / "rust" / "model" / "hip.rs").read_text()
+    impl = text[text.index("impl Device for Hip"):]
+    for m in TRAIT_METHODS:
+        assert re.search(rf"\bfn {m}\(", impl), m
+        assert f"sys::th_{m}(" in impl, m
+    called = set(re.findall(r"sys::(th_\w+)\(", text))
+    assert called <= set(cabi.header_signatures()), called - set(cabi.header_signatures())
 
 
 def test_errors_without_gpu_are_reported():
