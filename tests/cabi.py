@@ -10,6 +10,7 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "titania_hip.h"
+TEST_HEADER = ROOT / "include" / "titania_hip_test.h"
 RUST_SYS = ROOT / "titania_amd" / "rust" / "hip-sys" / "lib.rs"
 
 _C_SCALARS = {"int": "i32", "size_t": "size", "float": "f32", "uint32_t": "u32", "uint64_t": "u64",
@@ -28,9 +29,9 @@ def _c_kind(decl: str) -> str:
     return _C_SCALARS[base]
 
 
-def header_signatures() -> dict[str, tuple[str, list[str]]]:
+def header_signatures(path: Path = HEADER) -> dict[str, tuple[str, list[str]]]:
     """name -> (return kind, [argument kinds]) of every TH_API declaration."""
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
     out = {}
     for m in re.finditer(r"^TH_API\s+([^;]*?)\b(th_\w+)\s*\(([^)]*)\)\s*;", text, re.M | re.S):
         ret, name, args = m.group(1), m.group(2), m.group(3).strip()

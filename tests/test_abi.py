@@ -49,6 +49,20 @@ def test_ctypes_argtypes_match_header():
     assert not bad, bad
 
 
+def test_test_entry_points_exported_and_bound():
+    """The test-only entry points of include/titania_hip_test.h: exported,
+    and bound by tests/test_fused_kernels.py with the header's kinds."""
+    import test_fused_kernels as fk
+
+    header = cabi.header_signatures(cabi.TEST_HEADER)
+    assert len(header) == 8 and sorted(header) == sorted(fk.TEST_SIGNATURES)
+    lib = C.CDLL(str(_lib.LIB_PATH))
+    assert all(hasattr(lib, n) for n in header)
+    bound = cabi.ctypes_signatures({n: (C.c_int, a) for n, a in fk.TEST_SIGNATURES.items()})
+    bad = {n: (cabi.as_ctypes_kinds(header[n]), bound[n]) for n in header if cabi.as_ctypes_kinds(header[n]) != bound[n]}
+    assert not bad, bad
+
+
 def test_rust_sys_crate_matches_header():
     """The Rust FFI crate's extern block (titania_amd/rust/hip-sys/lib.rs,
     not compiled here) declares every header function with the same argument

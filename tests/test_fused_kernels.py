@@ -1,0 +1,307 @@
+"""Per-kernel parity of the fused kernels against the oracle's composition of
+the reference's primitives (model/cpu.rs, in the order model/model.rs:93-149
+calls them), at the Qwen3-0.6B and Qwen3-4B shapes, through the test-only
+entry points of include/titania_hip_test.h.
+
+Kernels: the decode step's q/k/v GEMV (residual add + RMSNorm prologue), its
+gate/up GEMV (SiLU epilogue), its plain GEMV (o, down; 19 chunks a lane at
+the 4B down shape), its output projection (argmax epilogue + pick), its fused
+q/k/v + attention launch (q/k norm, RoPE, KV append, chunked attention); the
+prefill's q/k/v GEMM (norm + RoPE + KV append epilogue), gate/up GEMM (SiLU
+epilogue) and residual-partials + RMSNorm kernel.
+
+Bar: the north star's per-kernel relative error <= 1e-3 (normwise), and an
+elementwise bound of a few fp32 rounding steps of each output's magnitude.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import ref
+from titania_amd import Tensor
+from titania_amd._lib import LIB_PATH, check
+from titania_amd.synth import bf16_to_f32, f32_to_bf16, normal_bf16
+from util import assert_close, rel_error
+
+pytestmark = pytest.mark.gpu
+
+_P, _SZ, _F = C.c_void_p, C.c_size_t, C.c_float
+TEST_SIGNATURES = {
+    "th_test_step_qkv": [_P, _P, _P, _P, _P, _P, _P, _F, _P, _P],
+    "th_test_step_gate_up": [_P, _P, _P, _P, _P, _P, _F, _P, _P],
+    "th_test_step_gemv": [_P, _P, _P, _P],
+    "th_test_step_logits": [_P, _P, _P, _P, _P, _F, _P, C.POINTER(C.c_uint32)],
+    "th_test_step_qkv_attn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P],
+    "th_test_gemm_qkv": [_P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P],
+    "th_test_gemm_silu": [_P, _P, _P, _P, _SZ, _P],
+    "th_test_add_rmsnorm_parts": [_P, _P, _P, _SZ, _P, _F, _P],
+}
+EPS = 1e-6
+
+
+@pytest.fixture(scope="module")
+def tlib(hip):
+    L = C.CDLL(str(LIB_PATH))
+    for name, args in TEST_SIGNATURES.items():
+        f = getattr(L, name)
+        f.restype = C.c_int
+        f.argtypes = args
+    return L
+
+
+def h(x):
+    """The handle of a buffer the caller keeps alive, or NULL."""
+    return None if x is None else x.handle
+
+
+def weight(hip, rows, cols, seed, name, std=0.05):
+    bits = normal_bf16(rows * cols, seed, name, std)
+    return bits, hip.upload(Tensor((rows, cols), bits))
+
+
+def gains(hip, n, seed, name):
+    g = f32_to_bf16(1.0 + bf16_to_f32(normal_bf16(n, seed, name, 0.1)))
+    return g, hip.upload(Tensor((n,), g))
+
+
+def buf(hip, values):
+    values = np.ascontiguousarray(values, np.float32).reshape(-1)
+    b = hip.alloc(values.size)
+    hip.write(b, values)
+    return b
+
+
+def gemv_bound(wbits, rows, cols, x):
+    """Elementwise bound: a few fp32 rounding steps of sum_c |w x|."""
+    w = np.abs(bf16_to_f32(wbits).reshape(rows, cols))
+    s = (w @ np.abs(np.asarray(x, np.float32).reshape(-1, cols)).T).T.reshape(-1)
+    return 3e-5 * s.astype(np.float64) + 1e-6
+
+
+def split_sigma(wbits, rows, cols, x):
+    """6 standard deviations of sum_c w[r, c] d[c] with d[c] uniform in
+    +-2^-17 |x[c]| (x rounded to bf16 hi + lo), per output row and x row."""
+    w2 = np.square(bf16_to_f32(wbits).reshape(rows, cols))
+    x2 = np.square(np.asarray(x, np.float32).reshape(-1, cols))
+    return 6 * 2.0 ** -17 / np.sqrt(3) * np.sqrt((x2 @ w2.T).astype(np.float64)).reshape(-1)
+
+
+SHAPES = {  # hidden, q heads, kv heads, intermediate
+    "0.6b": (1024, 16, 8, 3072),
+    "4b": (2560, 32, 8, 9728),
+}
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_step_qkv(hip, tlib, shape):
+    H, nh, nkv, _ = SHAPES[shape]
+    qd, kvd = nh * 128, nkv * 128
+    wq, Wq = weight(hip, qd, H, 1, "q")
+    wk, Wk = weight(hip, kvd, H, 1, "k")
+    wv, Wv = weight(hip, kvd, H, 1, "v")
+    g, G = gains(hip, H, 1, "g")
+    rng = np.random.default_rng(H)
+    x, y = rng.standard_normal(H).astype(np.float32), rng.standard_normal(H).astype(np.float32)
+    X, Y, xo, qkv = buf(hip, x), buf(hip, y), hip.alloc(H), hip.alloc(qd + 2 * kvd)
+    check(tlib.th_test_step_qkv(hip.handle, Wq.handle, Wk.handle, Wv.handle, X.handle, Y.handle,
+                                G.handle, EPS, xo.handle, qkv.handle))
+    xs = ref.add(x, y)
+    xn = ref.rmsnorm(xs, g, EPS)
+    exp = np.concatenate([ref.matmul(wq, qd, H, xn), ref.matmul(wk, kvd, H, xn), ref.matmul(wv, kvd, H, xn)])
+    assert np.array_equal(hip.read(xo), xs), "x + y is exact"
+    got = hip.read(qkv)
+    assert rel_error(got, exp) <= 1e-3
+    bound = np.concatenate([gemv_bound(wq, qd, H, xn), gemv_bound(wk, kvd, H, xn), gemv_bound(wv, kvd, H, xn)])
+    assert np.all(np.abs(got.astype(np.float64) - exp) <= bound + 1e-5 * np.abs(exp))
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_step_gate_up(hip, tlib, shape):
+    H, _, _, I = SHAPES[shape]
+    wg, Wg = weight(hip, I, H, 2, "gate")
+    wu, Wu = weight(hip, I, H, 2, "up")
+    g, G = gains(hip, H, 2, "g")
+    rng = np.random.default_rng(I)
+    x1, o = rng.standard_normal(H).astype(np.float32), rng.standard_normal(H).astype(np.float32)
+    X1, O, xo, hh = buf(hip, x1), buf(hip, o), hip.alloc(H), hip.alloc(I)
+    check(tlib.th_test_step_gate_up(hip.handle, Wg.handle, Wu.handle, X1.handle, O.handle, G.handle,
+                                    EPS, xo.handle, hh.handle))
+    xs = ref.add(x1, o)
+    n = ref.rmsnorm(xs, g, EPS)
+    exp = ref.silu_mul(ref.matmul(wg, I, H, n), ref.matmul(wu, I, H, n))
+    assert np.array_equal(hip.read(xo), xs)
+    got = hip.read(hh)
+    assert rel_error(got, exp) <= 1e-3
+    assert_close(got, exp, rel=1e-4, abs_=2e-5, what=f"gate/up {shape}")
+
+
+@pytest.mark.parametrize("name,rows,cols", [("o 0.6b", 1024, 2048), ("down 0.6b", 1024, 3072),
+                                            ("o 4b", 2560, 4096), ("down 4b", 2560, 9728)])
+def test_step_gemv(hip, tlib, name, rows, cols):
+    w, W = weight(hip, rows, cols, 3, name, std=1.0)
+    x = np.random.default_rng(rows + cols).standard_normal(cols).astype(np.float32)
+    X, out = buf(hip, x), hip.alloc(rows)
+    check(tlib.th_test_step_gemv(hip.handle, W.handle, X.handle, out.handle))
+    exp = ref.matmul(w, rows, cols, x)
+    got = hip.read(out)
+    assert rel_error(got, exp) <= 1e-3
+    assert np.all(np.abs(got.astype(np.float64) - exp) <= gemv_bound(w, rows, cols, x))
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_step_logits(hip, tlib, shape):
+    H = SHAPES[shape][0]
+    V = 151936
+    w, W = weight(hip, V, H, 4, "lm_head", std=0.02)
+    g, G = gains(hip, H, 4, "g")
+    rng = np.random.default_rng(V + H)
+    x, y = rng.standard_normal(H).astype(np.float32), rng.standard_normal(H).astype(np.float32)
+    X, Y, lg = buf(hip, x), buf(hip, y), hip.alloc(V)
+    tok = C.c_uint32()
+    check(tlib.th_test_step_logits(hip.handle, W.handle, X.handle, Y.handle, G.handle, EPS, lg.handle,
+                                   C.byref(tok)))
+    xn = ref.rmsnorm(ref.add(x, y), g, EPS)
+    exp = ref.matmul(w, V, H, xn)
+    got = hip.read(lg)
+    assert rel_error(got, exp) <= 1e-3
+    assert np.all(np.abs(got.astype(np.float64) - exp) <= gemv_bound(w, V, H, xn))
+    # The pick is the argmax of the device's own logits; it is the oracle's
+    # unless the oracle's top two are closer than the logits' error.
+    assert tok.value == int(np.argmax(got))
+    s = np.sort(exp)
+    if s[-1] - s[-2] > 1e-4:
+        assert tok.value == ref.argmax(exp)
+
+
+def _head_norm_rope(x, gain, table, pos, n_heads):
+    """Per-head RMSNorm then RoPE, as model.rs:111-118 applies them."""
+    x = ref.rmsnorm(x, gain, EPS) if gain is not None else np.asarray(x, np.float32)
+    return ref.rope(x, table, pos, n_heads, 128)
+
+
+@pytest.mark.parametrize("shape,pos", [("0.6b", 0), ("0.6b", 47), ("0.6b", 300), ("4b", 5), ("4b", 600)])
+def test_step_qkv_attn(hip, tlib, shape, pos):
+    """The fused launch against q/k/v GEMV, per-head norms, RoPE, the cache
+    append and the attention over positions 0..pos; 300 and 600 positions
+    span several 64-position chunks, merged by each head's first chunk."""
+    H, nh, nkv, _ = SHAPES[shape]
+    hd, qd, kvd = 128, nh * 128, nkv * 128
+    max_len = pos + 24
+    wq, Wq = weight(hip, qd, H, 5, "q")
+    wk, Wk = weight(hip, kvd, H, 5, "k")
+    wv, Wv = weight(hip, kvd, H, 5, "v")
+    g, G = gains(hip, H, 5, "g")
+    qn, QN = gains(hip, hd, 5, "qn")
+    kn, KN = gains(hip, hd, 5, "kn")
+    rng = np.random.default_rng(pos + H)
+    x, y = rng.standard_normal(H).astype(np.float32), rng.standard_normal(H).astype(np.float32)
+    table = ref.rope_table(max_len, hd, 1e6)
+    # Earlier positions' keys and values, device layout [kv head][max_len][128]
+    # plus the tail of 128 rows the attention may read past the last head.
+    kc = np.zeros((nkv, max_len, hd), np.float32)
+    vc = np.zeros((nkv, max_len, hd), np.float32)
+    kc[:, :pos] = rng.standard_normal((nkv, pos, hd))
+    vc[:, :pos] = rng.standard_normal((nkv, pos, hd))
+    tail = np.zeros(128 * hd, np.float32)
+    Kc, Vc = buf(hip, np.concatenate([kc.reshape(-1), tail])), buf(hip, np.concatenate([vc.reshape(-1), tail]))
+    X, Y, T, xo, att = buf(hip, x), buf(hip, y), buf(hip, table), hip.alloc(H), hip.alloc(qd)
+    check(tlib.th_test_step_qkv_attn(hip.handle, Wq.handle, Wk.handle, Wv.handle, X.handle, Y.handle,
+                                     G.handle, QN.handle, KN.handle, EPS, T.handle, Kc.handle, Vc.handle,
+                                     max_len, pos, nh, nkv, xo.handle, att.handle))
+    xs = ref.add(x, y)
+    xn = ref.rmsnorm(xs, g, EPS)
+    q = _head_norm_rope(ref.matmul(wq, qd, H, xn), qn, table, pos, nh)
+    k = _head_norm_rope(ref.matmul(wk, kvd, H, xn), kn, table, pos, nkv)
+    v = ref.matmul(wv, kvd, H, xn)
+    kc[:, pos], vc[:, pos] = k.reshape(nkv, hd), v.reshape(nkv, hd)
+    # The oracle's caches are position-major: [position][kv head][128].
+    exp = ref.attention(q, kc.transpose(1, 0, 2).copy(), vc.transpose(1, 0, 2).copy(), pos, nh, hd, nkv)
+    assert np.array_equal(hip.read(xo), xs)
+    got = hip.read(att)
+    assert rel_error(got, exp) <= 1e-3
+    assert_close(got, exp, rel=1e-4, abs_=1e-5, what=f"qkv+attention {shape} pos {pos}")
+    dk = hip.read(Kc)[: nkv * max_len * hd].reshape(nkv, max_len, hd)
+    dv = hip.read(Vc)[: nkv * max_len * hd].reshape(nkv, max_len, hd)
+    assert_close(dk[:, pos], kc[:, pos], rel=1e-4, abs_=1e-5, what="appended key")
+    assert_close(dv[:, pos], vc[:, pos], rel=1e-4, abs_=1e-5, what="appended value")
+    assert np.array_equal(dk[:, :pos], kc[:, :pos]), "earlier keys untouched"
+
+
+@pytest.mark.parametrize("shape,n,pos", [("0.6b", 100, 0), ("0.6b", 512, 37), ("4b", 100, 20)])
+def test_gemm_qkv(hip, tlib, shape, n, pos):
+    H, nh, nkv, _ = SHAPES[shape]
+    hd, qd, kvd = 128, nh * 128, nkv * 128
+    max_len = pos + n + 3
+    wq, Wq = weight(hip, qd, H, 6, "q")
+    wk, Wk = weight(hip, kvd, H, 6, "k")
+    wv, Wv = weight(hip, kvd, H, 6, "v")
+    qn, QN = gains(hip, hd, 6, "qn")
+    kn, KN = gains(hip, hd, 6, "kn")
+    xn = np.random.default_rng(n + H).standard_normal(n * H).astype(np.float32)
+    table = ref.rope_table(max_len, hd, 1e6)
+    Kc, Vc = hip.alloc(nkv * max_len * hd), hip.alloc(nkv * max_len * hd)
+    XN, T, qo = buf(hip, xn), buf(hip, table), hip.alloc(n * qd)
+    check(tlib.th_test_gemm_qkv(hip.handle, XN.handle, Wq.handle, Wk.handle, Wv.handle, QN.handle, KN.handle,
+                                EPS, T.handle, Kc.handle, Vc.handle, max_len, pos, n, nh, nkv, qo.handle))
+    q = _head_norm_rope(ref.matmul(wq, qd, H, xn), qn, table, pos, nh)
+    k = _head_norm_rope(ref.matmul(wk, kvd, H, xn), kn, table, pos, nkv).reshape(n, nkv, hd)
+    v = ref.matmul(wv, kvd, H, xn).reshape(n, nkv, hd)
+    got = hip.read(qo)
+    assert rel_error(got, q) <= 1e-3
+    assert_close(got, q, rel=1e-4, abs_=5e-5, what=f"q {shape} n={n}")
+    dk = hip.read(Kc).reshape(nkv, max_len, hd)[:, pos:pos + n].transpose(1, 0, 2)
+    dv = hip.read(Vc).reshape(nkv, max_len, hd)[:, pos:pos + n].transpose(1, 0, 2)
+    assert rel_error(dk, k) <= 1e-3 and rel_error(dv, v) <= 1e-3
+    assert_close(dk, k, rel=1e-4, abs_=5e-5, what="keys")
+    assert_close(dv, v, rel=1e-4, abs_=5e-5, what="values")
+
+
+@pytest.mark.parametrize("shape,n", [("0.6b", 100), ("0.6b", 512), ("4b", 100)])
+def test_gemm_silu(hip, tlib, shape, n):
+    H, _, _, I = SHAPES[shape]
+    wg, Wg = weight(hip, I, H, 7, "gate")
+    wu, Wu = weight(hip, I, H, 7, "up")
+    xn = np.random.default_rng(n + I).standard_normal(n * H).astype(np.float32)
+    XN, ho = buf(hip, xn), hip.alloc(n * I)
+    check(tlib.th_test_gemm_silu(hip.handle, XN.handle, Wg.handle, Wu.handle, n, ho.handle))
+    g, u = ref.matmul(wg, I, H, xn), ref.matmul(wu, I, H, xn)
+    exp = ref.silu_mul(g, u)
+    got = hip.read(ho)
+    assert rel_error(got, exp) <= 1e-3
+    # The kernel multiplies x kept as bf16 hi + lo (error <= 2^-17 |x_i|
+    # each, independent): gate and up are off by at most 6 standard
+    # deviations of that sum, eg and eu; h by |silu(g)| eu + |silu'(g) u| eg,
+    # plus its own hi + lo rounding (2^-16 |h|).
+    g, u = g.astype(np.float64), u.astype(np.float64)
+    eg, eu = split_sigma(wg, I, H, xn), split_sigma(wu, I, H, xn)
+    sg = 1.0 / (1.0 + np.exp(-g))
+    bound = np.abs(g * sg) * eu + np.abs(sg * (1 + g * (1 - sg)) * u) * eg + 2.0 ** -16 * np.abs(exp) + 1e-6
+    err = np.abs(got.astype(np.float64) - exp)
+    assert np.all(err <= bound), f"silu(gate) * up {shape} n={n}: worst {np.max(err / bound):.2f} of the bound"
+
+
+@pytest.mark.parametrize("dim,rows,n_parts", [(1024, 100, 0), (1024, 100, 1), (1024, 64, 3), (2560, 40, 2)])
+def test_add_rmsnorm_parts(hip, tlib, dim, rows, n_parts):
+    g, G = gains(hip, dim, 8, "g")
+    rng = np.random.default_rng(dim + rows + n_parts)
+    x = rng.standard_normal(rows * dim).astype(np.float32)
+    parts = rng.standard_normal(n_parts * rows * dim).astype(np.float32)
+    X, XN = buf(hip, x), hip.alloc(rows * dim)
+    P = buf(hip, parts) if n_parts else None
+    check(tlib.th_test_add_rmsnorm_parts(hip.handle, X.handle, h(P), n_parts, G.handle, EPS, XN.handle))
+    xs = x.copy()
+    if n_parts:
+        # The partials are summed in order, then added (one rounding each).
+        s = parts.reshape(n_parts, -1)[0].copy()
+        for p in range(1, n_parts):
+            s = ref.add(s, parts.reshape(n_parts, -1)[p])
+        xs = ref.add(xs, s)
+    exp = ref.rmsnorm(xs, g, EPS)
+    assert_close(hip.read(X), xs, rel=1e-6, abs_=1e-6, what="x + partials")
+    got = hip.read(XN)
+    assert rel_error(got, exp) <= 1e-3
+    assert_close(got, exp, rel=2e-5, abs_=1e-6, what="rmsnorm as hi + lo")

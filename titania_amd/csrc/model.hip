@@ -259,15 +259,16 @@ int ensure_fused_state(th_state *s) {
                   {&s->s_o, H}, {&s->s_h, I}};
         for (auto &b : sb) TH_HIP(hipMalloc(b.p, b.n * sizeof(float)));
         TH_HIP(hipMalloc(&s->s_part, (size_t)th::step_logits_partials((int)c.vocab_size) * sizeof(uint64_t)));
-        // Zeroed: epoch 0 precedes every epoch a step uses.
+        // Zeroed: epoch 0 precedes every epoch a step uses. Cleared on the
+        // device's stream, which is non-blocking: a null-stream hipMemset
+        // would not be ordered before the step kernels.
         const int chunks = std::max(
             th::step_qkv_attn_chunks(s->max_len, s->kv_dtype == TH_KV_BF16, (int)c.num_attention_heads), 1);
         const size_t words = th::step_qkv_attn_words((int)qd, (int)kvd, (int)c.num_attention_heads, chunks);
         TH_HIP(hipMalloc(&s->s_words, words * sizeof(unsigned long long)));
-        TH_HIP(hipMemset(s->s_words, 0, words * sizeof(unsigned long long)));
+        TH_HIP(hipMemsetAsync(s->s_words, 0, words * sizeof(unsigned long long), m->dev->stream));
         TH_HIP(hipMalloc(&s->s_err, sizeof(unsigned)));
-        TH_HIP(hipMemset(s->s_err, 0, sizeof(unsigned)));
-
+        TH_HIP(hipMemsetAsync(s->s_err, 0, sizeof(unsigned), m->dev->stream));
     }
     return TH_OK;
 }

@@ -1,0 +1,271 @@
+// Test-only entry points (include/titania_hip_test.h): each runs one fused
+// kernel of the decode step or the prefill on caller buffers, so that tests
+// can hold every fused kernel to the per-kernel bar against the oracle's
+// composition of the reference's primitives. The product path (the Device
+// entry points, th_forward, th_decode) never calls them. They allocate the
+// small device state a kernel needs (step state, exchange words, bf16 hi/lo
+// operands) and free it before returning.
+#include <cstring>
+#include <vector>
+
+#include "../../include/titania_hip_test.h"
+#include "common.h"
+#include "fused.h"
+#include "gemm.h"
+#include "step.h"
+
+namespace {
+
+using th::fail;
+
+// f32 out[i] = hi[i] + lo[i] (the split_bf16 terms of a GEMM operand).
+__global__ void hl_to_f32_kernel(const uint16_t *hi, const uint16_t *lo, size_t n, float *out) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = th::bf16_to_f32(hi[i]) + th::bf16_to_f32(lo[i]);
+}
+
+// Device memory freed when the holder goes out of scope, zeroed on the
+// device's stream (non-blocking, so a null-stream hipMemset would not be
+// ordered before the kernels that use it).
+struct DevMem {
+    void *p = nullptr;
+    ~DevMem() {
+        if (p) (void)hipFree(p);
+    }
+    int alloc(size_t bytes, hipStream_t s) {
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            p = nullptr;
+            return fail(TH_ERR_NOMEM, "test entry: %zu bytes of device memory", bytes);
+        }
+        if (hipMemsetAsync(p, 0, bytes, s) != hipSuccess) return fail(TH_ERR_HIP, "test entry: hipMemsetAsync failed");
+        return TH_OK;
+    }
+};
+
+int rows_of(const th_weight *w) { return w->ndim == 2 ? (int)w->shape[0] : 0; }
+int cols_of(const th_weight *w) { return w->ndim == 2 ? (int)w->shape[1] : 0; }
+
+}  // namespace
+
+extern "C" {
+
+int th_test_step_qkv(th_device *dev, const th_weight *wq, const th_weight *wk, const th_weight *wv,
+                     const th_buffer *x, const th_buffer *y, const th_weight *gain, float eps, th_buffer *x_out,
+                     th_buffer *qkv_out) {
+    TH_REQUIRE(dev && wq && wk && wv && x && gain && x_out && qkv_out, "th_test_step_qkv: null argument");
+    const int H = cols_of(wq), q_rows = rows_of(wq), kv_rows = rows_of(wk);
+    TH_REQUIRE(H > 0 && cols_of(wk) == H && cols_of(wv) == H && rows_of(wv) == kv_rows, "shapes disagree");
+    TH_REQUIRE(x->len == (size_t)H && (!y || y->len == (size_t)H) && x_out->len == (size_t)H &&
+                   gain->numel == (size_t)H && qkv_out->len == (size_t)(q_rows + 2 * kv_rows),
+               "buffer lengths disagree with the weights");
+    th::StepQkvArgs q{};
+    q.wq = wq->ptr;
+    q.wk = wk->ptr;
+    q.wv = wv->ptr;
+    q.q_rows = q_rows;
+    q.kv_rows = kv_rows;
+    q.hidden = H;
+    q.x_prev = x->ptr;
+    q.y_prev = y ? y->ptr : nullptr;
+    q.gain = gain->ptr;
+    q.eps = eps;
+    q.x_out = x_out->ptr;
+    q.qkv = qkv_out->ptr;
+    TH_HIP(th::launch_step_qkv(dev->stream, q));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_test_step_gate_up(th_device *dev, const th_weight *gate, const th_weight *up, const th_buffer *x1,
+                         const th_buffer *o, const th_weight *gain, float eps, th_buffer *x_out, th_buffer *h) {
+    TH_REQUIRE(dev && gate && up && x1 && o && gain && x_out && h, "th_test_step_gate_up: null argument");
+    const int I = rows_of(gate), H = cols_of(gate);
+    TH_REQUIRE(I > 0 && rows_of(up) == I && cols_of(up) == H && x1->len == (size_t)H && o->len == (size_t)H &&
+                   x_out->len == (size_t)H && gain->numel == (size_t)H && h->len == (size_t)I,
+               "buffer lengths disagree with the weights");
+    TH_HIP(th::launch_step_gate_up(dev->stream, gate->ptr, up->ptr, I, H, x1->ptr, o->ptr, gain->ptr, eps,
+                                   x_out->ptr, h->ptr));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_test_step_gemv(th_device *dev, const th_weight *w, const th_buffer *x, th_buffer *out) {
+    TH_REQUIRE(dev && w && x && out, "th_test_step_gemv: null argument");
+    const int rows = rows_of(w), cols = cols_of(w);
+    TH_REQUIRE(rows > 0 && x->len == (size_t)cols && out->len == (size_t)rows,
+               "buffer lengths disagree with the weight");
+    TH_HIP(th::launch_step_gemv(dev->stream, w->ptr, rows, cols, x->ptr, out->ptr));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_test_step_logits(th_device *dev, const th_weight *w, const th_buffer *x, const th_buffer *y,
+                        const th_weight *gain, float eps, th_buffer *logits, uint32_t *token) {
+    TH_REQUIRE(dev && w && x && gain && logits && token, "th_test_step_logits: null argument");
+    const int V = rows_of(w), H = cols_of(w);
+    TH_REQUIRE(V > 0 && x->len == (size_t)H && (!y || y->len == (size_t)H) && gain->numel == (size_t)H &&
+                   logits->len == (size_t)V,
+               "buffer lengths disagree with the weight");
+    DevMem part, st;
+    TRY(part.alloc((size_t)th::step_logits_partials(V) * sizeof(uint64_t), dev->stream));
+    TRY(st.alloc(sizeof(th::StepState), dev->stream));
+    int np = 0;
+    TH_HIP(th::launch_step_logits(dev->stream, w->ptr, V, H, x->ptr, y ? y->ptr : nullptr, gain->ptr, eps,
+                                  logits->ptr, static_cast<uint64_t *>(part.p), &np));
+    TH_HIP(th::launch_pick_partials(dev->stream, static_cast<uint64_t *>(part.p), (size_t)np,
+                                    static_cast<th::StepState *>(st.p), 0));
+    th::StepState host{};
+    TH_HIP(hipMemcpyAsync(&host, st.p, sizeof host, hipMemcpyDeviceToHost, dev->stream));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    *token = host.token;
+    return TH_OK;
+}
+
+int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_weight *wk, const th_weight *wv,
+                          const th_buffer *x, const th_buffer *y, const th_weight *gain, const th_weight *q_norm,
+                          const th_weight *k_norm, float eps, const th_buffer *rope, th_buffer *k_cache,
+                          th_buffer *v_cache, size_t max_len, size_t pos, size_t n_heads, size_t n_kv_heads,
+                          th_buffer *x_out, th_buffer *att_out) {
+    TH_REQUIRE(dev && wq && wk && wv && x && gain && rope && k_cache && v_cache && x_out && att_out,
+               "th_test_step_qkv_attn: null argument");
+    const int H = cols_of(wq);
+    const size_t hd = 128, qd = n_heads * hd, kvd = n_kv_heads * hd;
+    TH_REQUIRE(n_kv_heads > 0 && n_heads % n_kv_heads == 0 && (size_t)rows_of(wq) == qd &&
+                   (size_t)rows_of(wk) == kvd && (size_t)rows_of(wv) == kvd && cols_of(wk) == H &&
+                   cols_of(wv) == H,
+               "weights are not [n_heads * 128, hidden] and [n_kv_heads * 128, hidden] x 2");
+    TH_REQUIRE(x->len == (size_t)H && (!y || y->len == (size_t)H) && x_out->len == (size_t)H &&
+                   gain->numel == (size_t)H && att_out->len == qd,
+               "buffer lengths disagree with the weights");
+    TH_REQUIRE((!q_norm || q_norm->numel == hd) && (!k_norm || k_norm->numel == hd), "q/k norms hold 128 gains");
+    TH_REQUIRE(pos < max_len && rope->len >= max_len * hd, "the rope table holds max_len positions");
+    // The attention blocks read whole 64-row passes: the caches extend
+    // kStepKvTailRows rows of head_dim past the last head.
+    const size_t need = n_kv_heads * max_len * hd + (size_t)th::kStepKvTailRows * hd;
+    TH_REQUIRE(k_cache->len >= need && v_cache->len >= need, "caches need %zu floats (the tail included)", need);
+    const int chunks = th::step_qkv_attn_chunks(max_len, 0, (int)n_heads);
+    TH_REQUIRE(chunks > 0 && th::step_qkv_attn_supported(H, (int)n_heads, (int)n_kv_heads),
+               "the fused launch does not take this shape or context");
+    DevMem st, words, err;
+    TRY(st.alloc(sizeof(th::StepState), dev->stream));
+    const size_t nw = th::step_qkv_attn_words((int)qd, (int)kvd, (int)n_heads, chunks);
+    TRY(words.alloc(nw * sizeof(unsigned long long), dev->stream));
+    TRY(err.alloc(sizeof(unsigned), dev->stream));
+    th::StepState host{};
+    host.pos = (long long)pos;
+    TH_HIP(hipMemcpyAsync(st.p, &host, sizeof host, hipMemcpyHostToDevice, dev->stream));
+    th::StepQkvAttnArgs f{};
+    f.qkv.wq = wq->ptr;
+    f.qkv.wk = wk->ptr;
+    f.qkv.wv = wv->ptr;
+    f.qkv.q_rows = (int)qd;
+    f.qkv.kv_rows = (int)kvd;
+    f.qkv.hidden = H;
+    f.qkv.x_prev = x->ptr;
+    f.qkv.y_prev = y ? y->ptr : nullptr;
+    f.qkv.gain = gain->ptr;
+    f.qkv.eps = eps;
+    f.qkv.x_out = x_out->ptr;
+    f.at.q_norm = q_norm ? q_norm->ptr : nullptr;
+    f.at.k_norm = k_norm ? k_norm->ptr : nullptr;
+    f.at.rope = rope->ptr;
+    f.at.k_cache = k_cache->ptr;
+    f.at.v_cache = v_cache->ptr;
+    f.at.head_stride = (long long)(max_len * hd);
+    f.at.pos = &static_cast<th::StepState *>(st.p)->pos;
+    f.at.n_heads = (int)n_heads;
+    f.at.n_kv_heads = (int)n_kv_heads;
+    f.at.nsplit = 1;
+    f.at.kv_bf16 = 0;
+    f.at.eps = eps;
+    f.at.out = att_out->ptr;
+    f.words = static_cast<unsigned long long *>(words.p);
+    f.err = static_cast<unsigned *>(err.p);
+    f.st = static_cast<th::StepState *>(st.p);
+    f.layer = 0;
+    f.chunks = chunks;
+    TH_HIP(th::launch_step_qkv_attn(dev->stream, f));
+    unsigned failures = 0;
+    TH_HIP(hipMemcpyAsync(&failures, err.p, sizeof failures, hipMemcpyDeviceToHost, dev->stream));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    TH_REQUIRE(failures == 0, "%u attention blocks gave up waiting for their q/k/v", failures);
+    return TH_OK;
+}
+
+int th_test_gemm_qkv(th_device *dev, const th_buffer *xn, const th_weight *wq, const th_weight *wk,
+                     const th_weight *wv, const th_weight *q_norm, const th_weight *k_norm, float eps,
+                     const th_buffer *rope, th_buffer *k_cache, th_buffer *v_cache, size_t max_len, size_t pos,
+                     size_t n, size_t n_heads, size_t n_kv_heads, th_buffer *q_out) {
+    TH_REQUIRE(dev && xn && wq && wk && wv && rope && k_cache && v_cache && q_out, "th_test_gemm_qkv: null argument");
+    const size_t H = (size_t)cols_of(wq), hd = 128, qd = n_heads * hd, kvd = n_kv_heads * hd;
+    TH_REQUIRE(n > 0 && n_kv_heads > 0 && (size_t)rows_of(wq) == qd && (size_t)rows_of(wk) == kvd &&
+                   (size_t)rows_of(wv) == kvd && (size_t)cols_of(wk) == H && (size_t)cols_of(wv) == H,
+               "weights are not [n_heads * 128, hidden] and [n_kv_heads * 128, hidden] x 2");
+    TH_REQUIRE(xn->len == n * H && q_out->len == n * qd, "buffer lengths disagree with n and the weights");
+    TH_REQUIRE(pos + n <= max_len && rope->len >= max_len * hd, "positions past max_len or the rope table");
+    TH_REQUIRE(k_cache->len >= n_kv_heads * max_len * hd && v_cache->len >= n_kv_heads * max_len * hd,
+               "caches hold [n_kv_heads][max_len][128]");
+    TH_REQUIRE(th::gemm_qkv_fused(n, qd, kvd, H, hd), "the fused q/k/v GEMM does not take this shape");
+    DevMem split;
+    TRY(split.alloc(2 * n * H * sizeof(uint16_t), dev->stream));
+    uint16_t *hi = static_cast<uint16_t *>(split.p), *lo = hi + n * H;
+    TH_HIP(th::launch_gemm_split(dev->stream, xn->ptr, n, H, hi, lo));
+    th::QkvPostArgs qa{};
+    qa.q = q_out->ptr;
+    qa.q_norm = q_norm ? q_norm->ptr : nullptr;
+    qa.k_norm = k_norm ? k_norm->ptr : nullptr;
+    qa.rope = rope->ptr;
+    qa.k_cache = k_cache->ptr;
+    qa.v_cache = v_cache->ptr;
+    qa.head_stride = (long long)(max_len * hd);
+    qa.pos_stride = (long long)hd;
+    qa.pos = (long long)pos;
+    qa.n = (int)n;
+    qa.n_heads = (int)n_heads;
+    qa.n_kv_heads = (int)n_kv_heads;
+    qa.head_dim = (int)hd;
+    qa.kv_bf16 = 0;
+    qa.eps = eps;
+    TH_HIP(th::launch_gemm_qkv(dev->stream, hi, lo, H, wq->ptr, wk->ptr, wv->ptr, qa));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_test_gemm_silu(th_device *dev, const th_buffer *xn, const th_weight *gate, const th_weight *up, size_t n,
+                      th_buffer *h_out) {
+    TH_REQUIRE(dev && xn && gate && up && h_out, "th_test_gemm_silu: null argument");
+    const size_t I = (size_t)rows_of(gate), H = (size_t)cols_of(gate);
+    TH_REQUIRE(n > 0 && I > 0 && (size_t)rows_of(up) == I && (size_t)cols_of(up) == H && I % 64 == 0,
+               "gate and up are not [inter, hidden] with inter a multiple of 64");
+    TH_REQUIRE(xn->len == n * H && h_out->len == n * I, "buffer lengths disagree with n and the weights");
+    DevMem split, hsplit;
+    TRY(split.alloc(2 * n * H * sizeof(uint16_t), dev->stream));
+    TRY(hsplit.alloc(2 * n * I * sizeof(uint16_t), dev->stream));
+    uint16_t *hi = static_cast<uint16_t *>(split.p), *lo = hi + n * H;
+    uint16_t *hh = static_cast<uint16_t *>(hsplit.p), *hl = hh + n * I;
+    TH_HIP(th::launch_gemm_split(dev->stream, xn->ptr, n, H, hi, lo));
+    TH_HIP(th::launch_gemm_silu(dev->stream, hi, lo, n, H, gate->ptr, up->ptr, I, hh, hl));
+    hl_to_f32_kernel<<<256, 256, 0, dev->stream>>>(hh, hl, n * I, h_out->ptr);
+    TH_HIP(hipGetLastError());
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_test_add_rmsnorm_parts(th_device *dev, th_buffer *x, const th_buffer *parts, size_t n_parts,
+                              const th_weight *gain, float eps, th_buffer *xn) {
+    TH_REQUIRE(dev && x && gain && xn && (parts || n_parts == 0), "th_test_add_rmsnorm_parts: null argument");
+    const size_t dim = gain->numel, rows = dim ? x->len / dim : 0;
+    TH_REQUIRE(dim > 0 && rows * dim == x->len && xn->len == x->len, "x and xn hold whole rows of the gains");
+    TH_REQUIRE(!n_parts || parts->len == n_parts * x->len, "parts hold n_parts copies of x's length");
+    DevMem split;
+    TRY(split.alloc(2 * x->len * sizeof(uint16_t), dev->stream));
+    uint16_t *hi = static_cast<uint16_t *>(split.p), *lo = hi + x->len;
+    TH_HIP(th::launch_add_rmsnorm_parts(dev->stream, x->ptr, n_parts ? parts->ptr : nullptr, (int)n_parts, x->len,
+                                        nullptr, hi, lo, rows, gain->ptr, dim, eps));
+    hl_to_f32_kernel<<<256, 256, 0, dev->stream>>>(hi, lo, x->len, xn->ptr);
+    TH_HIP(hipGetLastError());
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+}  // extern "C"
