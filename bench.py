@@ -10,14 +10,20 @@ position 16, after `--warmup` untimed steps; weights, caches and the prompt's
 keys and values are resident in HBM before it starts.
 
 Prints one JSON line (the benchmark contract) with the roofline of the decode
-step and the CPU oracle's throughput on the same workload.
+step and the CPU oracle's throughput on the same workload. Inside the same
+line, `long_context_4b` reports the Qwen3-4B-shaped workload at the
+reference's precision: an 8192-token prompt in f32 KV caches, then 256 greedy
+decode steps (with its own roofline, the 8192-token prefill on the matrix
+cores, and the CPU oracle at that context).
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import platform
 import subprocess
 import sys
 import time
@@ -39,6 +45,18 @@ def kv_bytes_per_token(c, ctx_from: int, steps: int, kv_elem: int) -> float:
     read = c.num_hidden_layers * 2 * avg_ctx * kvd * kv_elem
     write = c.num_hidden_layers * 2 * kvd * kv_elem
     return read + write
+
+
+def cpu_model_name() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the baseline's record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(cfg, weights, prompt, steps: int, repeats: int) -> dict:
@@ -67,9 +85,50 @@ def cpu_baseline(cfg, weights, prompt, steps: int, repeats: int) -> dict:
         "value": rates[len(rates) // 2],
         "unit": "tokens/s",
         "cores": cores,
+        "cpu": cpu_model_name(),
         "kind": "port",
         "sample": f"{steps} greedy decode steps after the {len(prompt)}-token prompt, median of {repeats} runs",
         "tokens": tokens,
+    }
+
+
+def cpu_baseline_at_context(cfg, weights, ctx: int, steps: int, first_token: int) -> dict:
+    """The CPU oracle's greedy decode tokens/s at positions ctx, ctx + 1, ...
+    over f32 caches holding ctx earlier positions. A prefill of ctx tokens is
+    out of reach on the CPU, so the caches' earlier rows are filled with
+    seeded N(0, 1) values instead (the oracle's time does not depend on
+    them; rows left as untouched zero pages would read faster than real
+    ones). One untimed step first, then `steps` timed ones."""
+    from oracle import ref
+
+    cores = min(os.cpu_count() or 1, 16)
+    ref.set_threads(cores)
+    model = ref.RefModel(cfg, weights)
+    st = model.state(ctx + steps + 1)
+    kvd = cfg.num_key_value_heads * cfg.head_dim()
+    rng = np.random.default_rng(ctx)
+    rows = rng.standard_normal((ctx, kvd)).astype(np.float32)
+    for layer in range(cfg.num_hidden_layers):
+        for get in (ref.lib().ref_state_k_cache, ref.lib().ref_state_v_cache):
+            cache = np.ctypeslib.as_array(ctypes.cast(get(st.handle, layer), ctypes.POINTER(ctypes.c_float)),
+                                          shape=(st.max_len, kvd))
+            cache[:ctx] = rows
+    tok = int(first_token)
+    logits = model.forward(st, [tok], ctx)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok = ref.argmax(logits)
+        logits = model.forward(st, [tok], ctx + 1 + i)
+    rate = steps / (time.perf_counter() - t0)
+    del st
+    return {
+        "value": rate,
+        "unit": "tokens/s",
+        "cores": cores,
+        "cpu": cpu_model_name(),
+        "kind": "port",
+        "sample": f"{steps} greedy decode steps at positions {ctx + 1}-{ctx + steps} over f32 caches of {ctx} "
+                  "earlier positions (seeded values in place of a prefill), after one untimed step",
     }
 
 
@@ -256,18 +315,80 @@ def long_context_decode(dev, model, cfg, kv: int, kv_elem: int, steps: int, seed
     return rows
 
 
+LONG_CONTEXT = 8192
+
+
+def long_context_4b(dev, seed: int, steps: int, warmup: int, cpu_steps: int) -> dict:
+    """The Qwen3-4B-shaped workload (36 layers, hidden 2560, 32 Q / 8 KV heads,
+    MLP 9728, vocab 151936, tied embeddings) at the reference's precision, f32
+    KV caches: an 8192-token uniform-random prompt prefilled into the caches,
+    then `steps` greedy decode steps, timed with HIP events on the device
+    stream (weights, caches and the prompt's keys and values resident before
+    the timed region). Also the 8192-token prefill alone on the matrix cores,
+    and the CPU oracle's decode rate at the same context (bounded sample)."""
+    from titania_amd import QWEN3_4B, TH_KV_F32, TH_PATH_FUSED, synth
+    from titania_amd.model import Model, State
+
+    cfg, ctx = QWEN3_4B, LONG_CONTEXT
+    weights = synth.weights(cfg, seed=seed)
+    prompt = synth.prompt(ctx, cfg.vocab_size, seed=seed + 2)
+    model = Model(dev, cfg, weights)
+    state = State(model, ctx + max(steps, warmup, 1), TH_KV_F32)
+    model.forward(state, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    if warmup:
+        model.decode(state, ctx, warmup)
+    model.forward(state, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    dev.synchronize()
+    dev.timer_begin()
+    t0 = time.perf_counter()
+    tokens = model.decode(state, ctx, steps)
+    wall = time.perf_counter() - t0
+    gpu_ms = dev.timer_end()
+    state.close()
+    nbytes = cfg.weight_bytes_per_token() + kv_bytes_per_token(cfg, ctx, steps, 4) + 4 * cfg.vocab_size
+    achieved = nbytes / (gpu_ms / 1000.0 / steps) / 1e9
+    traffic, traffic_source = measured_traffic("qwen3-4b", "f32", ctx)
+    out = {
+        "metric": "batch-1 decode tokens/s (Qwen3-4B shape, 8192-token prompt in the KV cache)",
+        "value": steps / wall,
+        "unit": "tokens/s",
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": wall * 1000.0 / steps,
+        "dtype": "bf16 weights; f32 activations, accumulation and KV cache",
+        "config": {"workload": f"qwen3-4b greedy decode after an {ctx}-token prompt, {steps} steps, batch 1, "
+                               "f32 KV cache", "model": "qwen3-4b", "prompt": ctx, "seq_len": ctx + steps},
+        "roofline": {"bound": "hbm", "kernel": "decode step (one token's kernels; HIP graphs of eight steps "
+                                               "replayed)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic, "traffic_source": traffic_source, "bytes_per_step": nbytes,
+                     "gpu_ms_per_step": gpu_ms / steps},
+        "prefill": prefill_bench(dev, model, cfg, ctx, TH_KV_F32, seed),
+    }
+    model.close()
+    if cpu_steps:
+        out["cpu_baseline"] = cpu_baseline_at_context(cfg, weights, ctx, cpu_steps, int(tokens[-1]))
+    return out
+
+
 TRAFFIC_FILE = ROOT / "profiles" / "decode_traffic.json"
 
 
-def measured_traffic(model: str, kv: str, mode: str):
+def measured_traffic(model: str, kv: str, prompt: int):
     """HBM bytes per decode step (read + write) measured with hardware
-    counters for this workload, if a measurement is on file; else None."""
+    counters for this workload (model, KV cache type, prompt length), and
+    where they come from (the commands, the source revision and the launch
+    mode of that measurement), if a measurement is on file; else (None, None)."""
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
     except (OSError, ValueError):
-        return None
-    entry = data.get(f"{model}/{kv}")
-    return None if entry is None else entry.get("traffic_bytes_per_step")
+        return None, None
+    entry = data.get(f"{model}/{kv}/{prompt}")
+    if entry is None:
+        return None, None
+    source = {k: entry[k] for k in ("revision", "mode", "commands") if k in entry}
+    source["file"] = str(TRAFFIC_FILE.relative_to(ROOT))
+    return entry.get("traffic_bytes_per_step"), source
 
 
 def _counter_rows(directory: str):
@@ -325,6 +446,11 @@ def main() -> int:
     ap.add_argument("--model", choices=["qwen3-0.6b", "qwen3-4b"], default="qwen3-0.6b")
     ap.add_argument("--prefill", type=int, default=512,
                     help="also time a prefill of this many random prompt tokens (0: skip)")
+    ap.add_argument("--long-steps", type=int, default=256,
+                    help="greedy decode steps of the Qwen3-4B-shaped workload after an 8192-token prompt with f32 "
+                         "KV caches, reported inside the line as long_context_4b (0: skip it)")
+    ap.add_argument("--long-cpu-steps", type=int, default=4,
+                    help="CPU-oracle decode steps timed at that context")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -408,7 +534,7 @@ def main() -> int:
     kernel = {
         "eager": "decode step (one token's kernels launched one by one)",
     }.get(mode, "decode step (one token's kernels; HIP graphs of eight steps replayed)")
-    traffic = measured_traffic(args.model, args.kv, mode)
+    traffic, traffic_source = (None, None) if args.max_len else measured_traffic(args.model, args.kv, args.prompt)
 
     out = {
         "metric": "batch-1 decode tokens/s (Qwen3-0.6B shape) + % of HBM GB/s roofline",
@@ -421,7 +547,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": f"bf16 weights; f32 activations, accumulation and {args.kv} KV cache",
         "data": "synthetic (seeded N(0,0.02) bf16 weights, gains 1, uniform-random prompt)",
         "config": {
             "workload": f"{args.model} greedy decode, {args.prompt}-token prompt, {K} steps, batch 1, "
@@ -439,6 +565,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "bytes_per_step": bytes_per_token,
             "gpu_ms_per_step": gpu_ms / K,
         },
@@ -450,9 +577,13 @@ def main() -> int:
         cb = cpu_baseline(cfg, weights, prompt, K, args.cpu_repeats)
         out["parity_tokens_match"] = [int(x) for x in tokens] == cb.pop("tokens")
         out["cpu_baseline"] = cb
-    print(json.dumps(out))
     state.close()
     model.close()
+    if args.long_steps:
+        del weights
+        out["long_context_4b"] = long_context_4b(dev, args.seed, args.long_steps, 8,
+                                                 0 if args.no_cpu else args.long_cpu_steps)
+    print(json.dumps(out))
     dev.close()
     return 0
 

@@ -300,9 +300,11 @@ def test_qwen4b_decode_8k_context(qwen4b):
 @pytest.mark.slow
 def test_qwen4b_bf16_cache_drift(qwen4b):
     """The bf16 KV cache at the same shape: how far its logits drift from the
-    f32 path (measured and printed; bounded loosely, since rounding every cached
-    key and value to 8 bits of mantissa over 36 layers and 8192 positions is
-    not within the 2e-2 bar that f32 caches meet)."""
+    f32 path. Rounding every cached key and value to 8 bits of mantissa over
+    36 layers and 8192 positions is not within the 2e-2 bar that f32 caches
+    meet, which is why f32 is the default cache. The drift measured on this
+    prompt is 0.045; the bound is twice that (the run is deterministic, so a
+    larger drift means a changed kernel)."""
     from titania_amd import QWEN3_4B
 
     prompt = synth.prompt(8192, QWEN3_4B.vocab_size, seed=42)
@@ -311,7 +313,7 @@ def test_qwen4b_bf16_cache_drift(qwen4b):
     lb = qwen4b.forward(b, prompt, 0, TH_PATH_FUSED)
     drift = float(np.max(np.abs(la - lb)))
     print(f"bf16 vs f32 KV cache, Qwen3-4B, 8192 positions: max |logit difference| = {drift:.4f}")
-    assert drift <= 0.25
+    assert drift <= 0.09
     a.close()
     b.close()
 
