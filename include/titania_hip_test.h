@@ -71,6 +71,15 @@ TH_API int th_test_gemm_silu(th_device *dev, const th_buffer *xn, const th_weigh
 TH_API int th_test_add_rmsnorm_parts(th_device *dev, th_buffer *x, const th_buffer *parts, size_t n_parts,
                                      const th_weight *gain, float eps, th_buffer *xn);
 
+/* Prefill attention (model.rs:121-124 for n tokens at pos .. pos + n - 1)
+ * over f32 caches of max_len positions, the q rows already normalized and
+ * rotated: planes = 0 runs the kernel that splits keys and values into bf16
+ * hi/lo in every block, planes = 1 the one that reads them from planes split
+ * once. out = [n][n_heads * 128] f32. */
+TH_API int th_test_attention_prefill(th_device *dev, const th_buffer *q, const th_buffer *k_cache,
+                                     const th_buffer *v_cache, size_t max_len, size_t pos, size_t n, size_t n_heads,
+                                     size_t n_kv_heads, int planes, th_buffer *out);
+
 #ifdef __cplusplus
 }
 #endif

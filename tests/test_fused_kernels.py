@@ -39,6 +39,7 @@ TEST_SIGNATURES = {
     "th_test_gemm_qkv": [_P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P],
     "th_test_gemm_silu": [_P, _P, _P, _P, _SZ, _P],
     "th_test_add_rmsnorm_parts": [_P, _P, _P, _SZ, _P, _F, _P],
+    "th_test_attention_prefill": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_int, _P],
 }
 EPS = 1e-6
 
@@ -305,3 +306,34 @@ def test_add_rmsnorm_parts(hip, tlib, dim, rows, n_parts):
     got = hip.read(XN)
     assert rel_error(got, exp) <= 1e-3
     assert_close(got, exp, rel=2e-5, abs_=1e-6, what="rmsnorm as hi + lo")
+
+
+@pytest.mark.parametrize("n,pos,H,KVH", [(512, 0, 16, 8), (100, 37, 16, 8), (1500, 600, 16, 8), (300, 20, 32, 8),
+                                         (64, 1000, 32, 8), (200, 5, 16, 2), (100, 3, 8, 8)])
+def test_attention_planes(hip, tlib, n, pos, H, KVH):
+    """Prefill attention through the bf16 planes (keys and values split once
+    per call) gives the per-block-split kernel's output bit for bit, and the
+    oracle's within the per-kernel bar. Cache rows past pos + n hold NaN: a
+    read of them would reach the output."""
+    hd, max_len = 128, pos + n + 70
+    rng = np.random.default_rng(n + pos + H)
+    q = rng.standard_normal(n * H * hd).astype(np.float32)
+    kc = np.full((KVH, max_len, hd), np.nan, np.float32)
+    vc = np.full((KVH, max_len, hd), np.nan, np.float32)
+    kc[:, :pos + n] = rng.standard_normal((KVH, pos + n, hd))
+    vc[:, :pos + n] = rng.standard_normal((KVH, pos + n, hd))
+    Q, K, V = buf(hip, q), buf(hip, kc), buf(hip, vc)
+    outs = []
+    for planes in (0, 1):
+        O = hip.alloc(n * H * hd)
+        check(tlib.th_test_attention_prefill(hip.handle, Q.handle, K.handle, V.handle, max_len, pos, n, H, KVH,
+                                             planes, O.handle))
+        outs.append(hip.read(O))
+    assert np.all(np.isfinite(outs[1]))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "planes differ from the split kernel"
+    if n * (pos + n) <= 600_000:
+        # The oracle's caches are position-major: [position][kv head][128].
+        exp = ref.attention(q, kc[:, :pos + n].transpose(1, 0, 2).copy(), vc[:, :pos + n].transpose(1, 0, 2).copy(),
+                            pos, H, hd, KVH)
+        assert rel_error(outs[1], exp) <= 1e-3
+        assert_close(outs[1], exp, rel=1e-4, abs_=2e-5, what=f"attention n={n} pos={pos} {H}/{KVH}")

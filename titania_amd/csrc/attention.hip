@@ -909,24 +909,37 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
         for (int s = 0; s < SETS; ++s)
 #pragma unroll
             for (int j = 0; j < KT / 16; ++j) st[s][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // Per 32-dimension step: the tile's four key fragments first (one
+        // base address, constant offsets), then each product term across the
+        // four independent accumulators, so that no MFMA waits on the one
+        // before it. Each accumulator still adds hi*hi, hi*lo, lo*hi in turn.
+        const uint4 *kbh = ksh + (li * KSB + 8 * lg) / 8;
+        const uint4 *kbl = ksl + (F32 ? (li * KSB + 8 * lg) / 8 : 0);
 #pragma unroll
-        for (int c = 0; c < HD / 32; ++c)
+        for (int c = 0; c < HD / 32; ++c) {
+            bf16x8_t kh[KT / 16], kl[F32 ? KT / 16 : 1];
 #pragma unroll
-            for (int j = 0; j < KT / 16; ++j) {
-                const int ko = ((16 * j + li) * KSB + 32 * c + 8 * lg) / 8;
-                const bf16x8_t kh = as_bf8(ksh[ko]);
+            for (int j = 0; j < KT / 16; ++j) kh[j] = as_bf8(kbh[(16 * j * KSB + 32 * c) / 8]);
+            if constexpr (F32)
 #pragma unroll
-                for (int s = 0; s < SETS; ++s) {
-                    st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, as_bf8(qh[s][c]), st[s][j], 0, 0, 0);
-                    st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, as_bf8(ql[s][c]), st[s][j], 0, 0, 0);
-                }
-                if constexpr (F32) {
-                    const bf16x8_t kl = as_bf8(ksl[ko]);
+                for (int j = 0; j < KT / 16; ++j) kl[j] = as_bf8(kbl[(16 * j * KSB + 32 * c) / 8]);
 #pragma unroll
-                    for (int s = 0; s < SETS; ++s)
-                        st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, as_bf8(qh[s][c]), st[s][j], 0, 0, 0);
-                }
-            }
+            for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                for (int j = 0; j < KT / 16; ++j)
+                    st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[j], as_bf8(qh[s][c]), st[s][j], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                for (int j = 0; j < KT / 16; ++j)
+                    st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[j], as_bf8(ql[s][c]), st[s][j], 0, 0, 0);
+            if constexpr (F32)
+#pragma unroll
+                for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                    for (int j = 0; j < KT / 16; ++j)
+                        st[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl[j], as_bf8(qh[s][c]), st[s][j], 0, 0, 0);
+        }
         // Causal mask and online softmax of the lane's row; p overwrites st.
 #pragma unroll
         for (int s = 0; s < SETS; ++s) {
@@ -944,8 +957,7 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
                     st[s][j][e] = v;
                     mx = fmaxf(mx, v);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = rows_max(mx);
             const float mn = fmaxf(m[s], mx);
             const float alpha = m[s] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[s] - mn);
             float sum = 0.f;
@@ -958,8 +970,7 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
                     st[s][j][e] = p;
                     sum += p;
                 }
-            sum += __shfl_xor(sum, 16);
-            sum += __shfl_xor(sum, 32);
+            sum = rows_sum(sum);
             l[s] = l[s] * alpha + sum;
             m[s] = mn;
 #pragma unroll
@@ -978,25 +989,346 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
                                     st[s][2 * sg + 1][2], st[s][2 * sg + 1][3]};
                 split8(f, ph[s], pl[s]);
             }
+            // Four dimension tiles at a time: their V^T fragments first, then
+            // each product term across the four accumulators.
+            const uint4 *vbh = vth + (li * VTS + 32 * sg + 8 * lg) / 8;
+            const uint4 *vbl = vtl + (F32 ? (li * VTS + 32 * sg + 8 * lg) / 8 : 0);
 #pragma unroll
-            for (int d = 0; d < HD / 16; ++d) {
-                const int vo = ((16 * d + li) * VTS + 32 * sg + 8 * lg) / 8;
-                const bf16x8_t vh = as_bf8(vth[vo]);
+            for (int d0 = 0; d0 < HD / 16; d0 += 4) {
+                bf16x8_t vh[4], vl[F32 ? 4 : 1];
 #pragma unroll
-                for (int s = 0; s < SETS; ++s) {
-                    o[s][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, as_bf8(ph[s]), o[s][d], 0, 0, 0);
-                    o[s][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, as_bf8(pl[s]), o[s][d], 0, 0, 0);
-                }
-                if constexpr (F32) {
-                    const bf16x8_t vl = as_bf8(vtl[vo]);
+                for (int i = 0; i < 4; ++i) vh[i] = as_bf8(vbh[(16 * (d0 + i) * VTS) / 8]);
+                if constexpr (F32)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) vl[i] = as_bf8(vbl[(16 * (d0 + i) * VTS) / 8]);
+#pragma unroll
+                for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[s][d0 + i] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh[i], as_bf8(ph[s]), o[s][d0 + i], 0, 0, 0);
+#pragma unroll
+                for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[s][d0 + i] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh[i], as_bf8(pl[s]), o[s][d0 + i], 0, 0, 0);
+                if constexpr (F32)
 #pragma unroll
                     for (int s = 0; s < SETS; ++s)
-                        o[s][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, as_bf8(ph[s]), o[s][d], 0, 0, 0);
-                }
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            o[s][d0 + i] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl[i], as_bf8(ph[s]), o[s][d0 + i], 0, 0, 0);
             }
         }
     }
     // o[s][d][e] is dimension 16 d + 4 lg + e of the lane's row.
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+        if (qloc[s] >= nq) continue;
+        const long long th = (long long)(t0 + qloc[s]) * a.n_heads + head[s];
+        if (a.nsplit == 1) {
+            const float inv = 1.f / l[s];
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d) {
+                const float4 v = make_float4(o[s][d][0] * inv, o[s][d][1] * inv, o[s][d][2] * inv, o[s][d][3] * inv);
+                const long long off = th * HD + 16 * d + 4 * lg;
+                if (a.out_hi) {
+                    uint2 h, w;
+                    split_bf16x4(v, h, w);
+                    *reinterpret_cast<uint2 *>(a.out_hi + off) = h;
+                    *reinterpret_cast<uint2 *>(a.out_lo + off) = w;
+                } else {
+                    *reinterpret_cast<float4 *>(a.out + off) = v;
+                }
+            }
+        } else {
+            const long long slot = th * a.nsplit + z;
+#pragma unroll
+            for (int d = 0; d < HD / 16; ++d)
+                *reinterpret_cast<float4 *>(a.part_acc + slot * HD + 16 * d + 4 * lg) =
+                    make_float4(o[s][d][0], o[s][d][1], o[s][d][2], o[s][d][3]);
+            if (lg == 0) {
+                a.part_ml[slot * 2] = m[s] * kLn2;
+                a.part_ml[slot * 2 + 1] = l[s];
+            }
+        }
+    }
+}
+
+// ---- prefill attention over bf16 planes of an f32 cache ----
+//
+// attn_gqa_kernel splits every f32 key and value into bf16 hi + lo in every
+// block that reads it: with a 2048-token chunk, each 64-key tile is split by
+// every token tile of its KV group, in VALU and registers, between two block
+// barriers per tile. Here a first kernel writes the split once per layer into
+// four bf16 planes: K hi / lo row-major [kv head][position][128], V^T hi / lo
+// dimension-major [kv head][128][position] with each 32-key slice's columns
+// in the P^T operand order of attn_gqa_kernel (column 8 g + i holds key
+// 4 g + i for i < 4 and 16 + 4 g + i - 4 otherwise). The attention blocks
+// then stage tiles with direct global -> LDS loads into a two-stage ring, one
+// block barrier per tile, the next tile in flight during this one's
+// products. The planes carry the same bf16 terms and the products run in the
+// same order, so the result is attn_gqa_kernel's, bit for bit.
+
+struct KvPlaneArgs {
+    const float *k, *v;           // the layer's caches: head g, position p at g head_stride + p pos_stride
+    long long head_stride, pos_stride;
+    uint16_t *kh, *kl, *vh, *vl;  // the planes, each n_kv_heads x 128 x plane_len bf16
+    long long plane_len;          // positions a plane holds per head (a multiple of 64)
+    long long valid;              // positions [0, valid) hold keys; later ones of a tile become zeros
+};
+
+// One block per (64-position tile, KV head).
+__global__ __launch_bounds__(256) void kv_planes_kernel(KvPlaneArgs a) {
+    constexpr int HD = 128;
+    __shared__ float vs[64][HD + 1];
+    const int g = blockIdx.y, tid = threadIdx.x;
+    const long long p0 = (long long)blockIdx.x * 64;
+    const float *kb = a.k + (long long)g * a.head_stride, *vb = a.v + (long long)g * a.head_stride;
+    // Keys: 64 rows x 16 chunks of 8 dimensions.
+    for (int u = tid; u < 64 * 16; u += 256) {
+        const int r = u >> 4, ch = u & 15;
+        const long long p = p0 + r;
+        float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (p < a.valid) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(kb + p * a.pos_stride + 8 * ch);
+            const float4 x1 = *reinterpret_cast<const float4 *>(kb + p * a.pos_stride + 8 * ch + 4);
+            f[0] = x0.x; f[1] = x0.y; f[2] = x0.z; f[3] = x0.w;
+            f[4] = x1.x; f[5] = x1.y; f[6] = x1.z; f[7] = x1.w;
+        }
+        uint4 h, l;
+        split8(f, h, l);
+        const long long o = ((long long)g * a.plane_len + p) * HD + 8 * ch;
+        *reinterpret_cast<uint4 *>(a.kh + o) = h;
+        *reinterpret_cast<uint4 *>(a.kl + o) = l;
+    }
+    // Values: the tile through LDS, then 128 dimensions x 8 column chunks.
+    for (int u = tid; u < 64 * (HD / 4); u += 256) {
+        const int r = u / (HD / 4), c4 = u % (HD / 4);
+        const long long p = p0 + r;
+        const float4 x =
+            p < a.valid ? *reinterpret_cast<const float4 *>(vb + p * a.pos_stride + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        vs[r][4 * c4] = x.x;
+        vs[r][4 * c4 + 1] = x.y;
+        vs[r][4 * c4 + 2] = x.z;
+        vs[r][4 * c4 + 3] = x.w;
+    }
+    __syncthreads();
+    for (int u = tid; u < HD * 8; u += 256) {
+        const int d = u >> 3, pc = u & 7, slice = pc >> 2, grp = pc & 3;
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = vs[32 * slice + (i < 4 ? 4 * grp + i : 16 + 4 * grp + i - 4)][d];
+        uint4 h, l;
+        split8(f, h, l);
+        const long long o = ((long long)g * HD + d) * a.plane_len + p0 + 8 * pc;
+        *reinterpret_cast<uint4 *>(a.vh + o) = h;
+        *reinterpret_cast<uint4 *>(a.vl + o) = l;
+    }
+}
+
+struct PlaneRefs {
+    const uint16_t *kh, *kl, *vh, *vl;
+    long long plane_len;
+};
+
+// attn_gqa_kernel<float> with its tiles staged from the planes. LDS: two
+// stages of four 16 KB tiles (K hi, K lo: 64 keys x 256 B; V^T hi, V^T lo:
+// 128 dimensions x 128 B), rows XOR-swizzled in 16-byte chunks so that a
+// fragment read's 16 rows land on distinct banks: K row r keeps logical
+// chunk c at c ^ (r & 15), V^T row r at c ^ ((r >> 1) & 7) (two 128-byte
+// rows share a bank line).
+__global__ __launch_bounds__(512, 1) void attn_planes_kernel(AttnKernelArgs a, PlaneRefs pl, int n) {
+    constexpr int NW = 8, NT = 64 * NW, SETS = kGqaRows / 16 / NW, RW = 16 * SETS;
+    constexpr int HD = 128, KT = kGqaKeys;
+    static_assert(KT == 64 && SETS >= 1, "64-key tiles");
+    constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
+    struct alignas(16) Stage {
+        uint4 kh[KT * 16], kl[KT * 16];  // [key][16 chunks]
+        uint4 vh[HD * 8], vl[HD * 8];    // [dimension][8 chunks]
+    };
+    __shared__ Stage ring[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
+    const int G = a.group, QT = kGqaRows / G;
+    const int g = blockIdx.y;
+    const int t0 = blockIdx.x * QT;
+    const int nq = n - t0 < QT ? n - t0 : QT;
+    const long long pos = a.pos;
+    int qloc[SETS], head[SETS];
+    uint4 qh[SETS][HD / 32], ql[SETS][HD / 32];
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+        const int r = RW * wave + 16 * s + li;
+        qloc[s] = r % QT;
+        head[s] = g * G + r / QT;
+        const float *qp = a.q + ((long long)(t0 + (qloc[s] < nq ? qloc[s] : 0)) * a.n_heads + head[s]) * HD + 8 * lg;
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c) {
+            float f[8];
+            const float4 x0 = *reinterpret_cast<const float4 *>(qp + 32 * c);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qp + 32 * c + 4);
+            f[0] = x0.x; f[1] = x0.y; f[2] = x0.z; f[3] = x0.w;
+            f[4] = x1.x; f[5] = x1.y; f[6] = x1.z; f[7] = x1.w;
+            if (qloc[s] >= nq)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = 0.f;
+            split8(f, qh[s][c], ql[s][c]);
+        }
+    }
+    const long long last = pos + t0 + nq - 1;
+    const int wq = QT >= RW ? (RW * wave) % QT + RW - 1 : QT - 1;
+    const long long wlast = pos + t0 + (wq < nq - 1 ? wq : nq - 1);
+    const long long ntiles = last / KT + 1, z = blockIdx.z;
+    const long long kt0 = z * ntiles / a.nsplit, kt1 = (z + 1) * ntiles / a.nsplit;
+    floatx4 o[SETS][HD / 16];
+    float m[SETS], l[SETS];
+#pragma unroll
+    for (int s = 0; s < SETS; ++s) {
+        m[s] = -INFINITY;
+        l[s] = 0.f;
+#pragma unroll
+        for (int d = 0; d < HD / 16; ++d) o[s][d] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float scale2 = a.scale * kLog2e;
+    const uint16_t *khg = pl.kh + (long long)g * pl.plane_len * HD, *klg = pl.kl + (long long)g * pl.plane_len * HD;
+    const uint16_t *vhg = pl.vh + (long long)g * HD * pl.plane_len, *vlg = pl.vl + (long long)g * HD * pl.plane_len;
+    // Each wave fills two 1 KB spans of each tile: K spans are 4 keys, V^T
+    // spans 8 dimensions. Eight loads a wave a stage.
+    auto issue = [&](Stage &st, long long c0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int span = 2 * wave + i, p = span * 64 + lane, row = p >> 4, pc = p & 15;
+            const long long off = (c0 + row) * HD + 8 * (pc ^ (row & 15));
+            dma16(khg + off, st.kh + span * 64);
+            dma16(klg + off, st.kl + span * 64);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int span = 2 * wave + i, p = span * 64 + lane, row = p >> 3, pc = p & 7;
+            const long long off = (long long)row * pl.plane_len + c0 + 8 * (pc ^ ((row >> 1) & 7));
+            dma16(vhg + off, st.vh + span * 64);
+            dma16(vlg + off, st.vl + span * 64);
+        }
+    };
+    const long long cend = kt1 * KT;
+    if (kt0 < kt1) issue(ring[0], kt0 * KT);
+    int sn = 0;
+    for (long long c0 = kt0 * KT; c0 < cend; c0 += KT, sn ^= 1) {
+        // This wave's loads of the tile are done; the barrier makes every
+        // wave's visible and frees the other stage (read during the last tile).
+        wait_vm<0>();
+        __syncthreads();
+        if (c0 + KT < cend) issue(ring[sn ^ 1], c0 + KT);
+        if (c0 > wlast) continue;  // every query of this wave precedes the tile
+        const Stage &st = ring[sn];
+        floatx4 sc[SETS][KT / 16];
+#pragma unroll
+        for (int s = 0; s < SETS; ++s)
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j) sc[s][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // S^T = K Q^T: key rows 16 j + li, logical chunk 4 c + lg.
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c) {
+            const int pcv = (4 * c + lg) ^ li;
+            bf16x8_t kh[KT / 16], kl[KT / 16];
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j) kh[j] = as_bf8(st.kh[(16 * j + li) * 16 + pcv]);
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j) kl[j] = as_bf8(st.kl[(16 * j + li) * 16 + pcv]);
+#pragma unroll
+            for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                for (int j = 0; j < KT / 16; ++j)
+                    sc[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[j], as_bf8(qh[s][c]), sc[s][j], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                for (int j = 0; j < KT / 16; ++j)
+                    sc[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[j], as_bf8(ql[s][c]), sc[s][j], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                for (int j = 0; j < KT / 16; ++j)
+                    sc[s][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl[j], as_bf8(qh[s][c]), sc[s][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < SETS; ++s) {
+            const long long qpos = pos + t0 + qloc[s];
+            const long long d = qpos - c0 - 4 * lg;
+            const int lim = qloc[s] >= nq ? -1 : d > KT ? KT : (int)d;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v = 16 * j + e <= lim ? sc[s][j][e] * scale2 : -INFINITY;
+                    sc[s][j][e] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = rows_max(mx);
+            const float mn = fmaxf(m[s], mx);
+            const float alpha = m[s] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[s] - mn);
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < KT / 16; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v = sc[s][j][e];
+                    const float p = v == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(v - mn);
+                    sc[s][j][e] = p;
+                    sum += p;
+                }
+            sum = rows_sum(sum);
+            l[s] = l[s] * alpha + sum;
+            m[s] = mn;
+#pragma unroll
+            for (int d2 = 0; d2 < HD / 16; ++d2)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[s][d2][e] *= alpha;
+        }
+        // O^T += V^T P^T: dimension rows 16 (d0 + i) + li, logical chunk 4 sg + lg.
+#pragma unroll
+        for (int sg = 0; sg < KT / 32; ++sg) {
+            uint4 ph[SETS], pq[SETS];
+#pragma unroll
+            for (int s = 0; s < SETS; ++s) {
+                const float f[8] = {sc[s][2 * sg][0],     sc[s][2 * sg][1],     sc[s][2 * sg][2],
+                                    sc[s][2 * sg][3],     sc[s][2 * sg + 1][0], sc[s][2 * sg + 1][1],
+                                    sc[s][2 * sg + 1][2], sc[s][2 * sg + 1][3]};
+                split8(f, ph[s], pq[s]);
+            }
+            const int pcv = (4 * sg + lg) ^ ((li >> 1) & 7);
+#pragma unroll
+            for (int d0 = 0; d0 < HD / 16; d0 += 4) {
+                bf16x8_t vh[4], vl[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vh[i] = as_bf8(st.vh[(16 * (d0 + i) + li) * 8 + pcv]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) vl[i] = as_bf8(st.vl[(16 * (d0 + i) + li) * 8 + pcv]);
+#pragma unroll
+                for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[s][d0 + i] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh[i], as_bf8(ph[s]), o[s][d0 + i], 0, 0, 0);
+#pragma unroll
+                for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[s][d0 + i] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh[i], as_bf8(pq[s]), o[s][d0 + i], 0, 0, 0);
+#pragma unroll
+                for (int s = 0; s < SETS; ++s)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        o[s][d0 + i] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl[i], as_bf8(ph[s]), o[s][d0 + i], 0, 0, 0);
+            }
+        }
+    }
 #pragma unroll
     for (int s = 0; s < SETS; ++s) {
         if (qloc[s] >= nq) continue;
@@ -1077,6 +1409,49 @@ hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, si
     case 256: return attn_launch<256>(s, k, n);
     default: return hipErrorInvalidValue;
     }
+}
+
+size_t attention_planes_bytes(size_t max_len, size_t n_kv_heads) {
+    return 4 * n_kv_heads * 128 * ((max_len + 63) / 64 * 64) * sizeof(uint16_t);
+}
+
+bool attention_planes_supported(const AttnKernelArgs &k, size_t n, size_t head_dim) {
+    return head_dim == 128 && n >= kAttnTileMin && !k.kv_bf16 && !k.pos_dev && k.group >= 1 && k.group <= 8 &&
+           8 % k.group == 0 && k.n_kv_heads * k.group == k.n_heads && k.pos_stride % 4 == 0 &&
+           k.head_stride % 4 == 0;
+}
+
+hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim, void *planes,
+                                   size_t planes_bytes, size_t max_len) {
+    if (n == 0) return hipSuccess;
+    if (!attention_planes_supported(k, n, head_dim) || !planes || k.pos < 0 || (size_t)k.pos + n > max_len ||
+        attention_planes_bytes(max_len, (size_t)k.n_kv_heads) > planes_bytes || (uintptr_t)planes % 16)
+        return hipErrorInvalidValue;
+    const long long plane_len = (long long)((max_len + 63) / 64 * 64);
+    const size_t plane = (size_t)k.n_kv_heads * 128 * (size_t)plane_len;
+    uint16_t *p0 = static_cast<uint16_t *>(planes);
+    KvPlaneArgs c{};
+    c.k = static_cast<const float *>(k.k);
+    c.v = static_cast<const float *>(k.v);
+    c.head_stride = k.head_stride;
+    c.pos_stride = k.pos_stride;
+    c.kh = p0;
+    c.kl = p0 + plane;
+    c.vh = p0 + 2 * plane;
+    c.vl = p0 + 3 * plane;
+    c.plane_len = plane_len;
+    c.valid = k.pos + (long long)n;
+    kv_planes_kernel<<<dim3((unsigned)((c.valid + 63) / 64), (unsigned)k.n_kv_heads), 256, 0, s>>>(c);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const PlaneRefs pr{c.kh, c.kl, c.vh, c.vl, plane_len};
+    const int qt = kGqaRows / k.group;
+    dim3 grid((unsigned)((n + qt - 1) / qt), (unsigned)k.n_kv_heads, (unsigned)k.nsplit);
+    attn_planes_kernel<<<grid, 512, 0, s>>>(k, pr, (int)n);
+    e = hipGetLastError();
+    if (e != hipSuccess || k.nsplit == 1) return e;
+    return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128, k.out_hi,
+                               k.out_lo);
 }
 
 }  // namespace th

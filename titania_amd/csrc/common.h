@@ -150,6 +150,15 @@ int attention_splits(size_t n, size_t n_heads, size_t n_kv_heads, size_t max_len
 // Scratch floats the partials of `nsplit` splits take (0 for one split).
 size_t attention_scratch(size_t n, size_t n_heads, size_t head_dim, int nsplit);
 hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim);
+// Prefill attention of an f32 cache through bf16 hi/lo planes of the keys and
+// values: launch_attention's result, bit for bit, with each key and value
+// split once per call instead of once per token tile. `planes` holds
+// attention_planes_bytes(max_len, n_kv_heads) bytes of scratch (max_len: the
+// positions the caches hold). Host positions only (no pos_dev).
+size_t attention_planes_bytes(size_t max_len, size_t n_kv_heads);
+bool attention_planes_supported(const AttnKernelArgs &k, size_t n, size_t head_dim);
+hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim, void *planes,
+                                   size_t planes_bytes, size_t max_len);
 // Merges attention partials of `heads` (token, head) pairs into out (f32) or,
 // when hi is set, into hi/lo as split_bf16 terms.
 hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,

@@ -112,6 +112,23 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// The maximum (sum) of v over lanes l, l ^ 16 and l ^ 32, l ^ 48: the four
+// 16-lane rows of a wave combined lane by lane, in every lane. gfx950's
+// permlane swaps exchange whole rows in the VALU (no LDS round trip); since
+// max and + commute, every lane gets the same (r0 op r1) op (r2 op r3).
+__device__ __forceinline__ float rows_max(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
@@ -143,6 +160,21 @@ __device__ __forceinline__ uint64_t argmax_pack(float f, uint32_t idx) {
 
 __device__ __forceinline__ uint32_t argmax_index(uint64_t packed) {
     return 0xffffffffu - (uint32_t)(packed & 0xffffffffu);
+}
+
+// One 16-byte direct global -> LDS load a lane (global_load_lds): lane l's
+// 16 bytes land at lds_wave_base + 16 l, so a wave fills one 1 KB span; the
+// LDS address must be the same in every lane of the wave.
+__device__ __forceinline__ void dma16(const void *src, uint4 *lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding): a
+// global_load_lds counts until its LDS write is done.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
 // model/cpu.rs:153: g / (1 + exp(-g)).

@@ -57,17 +57,6 @@ using Head = Tile<32, 128, 64, 3>;          // one attention head's 128 rows: 24
 template <int CH>
 __device__ __forceinline__ int swz(int row) { return (row >> 1) & (CH - 1); }
 
-__device__ __forceinline__ void dma16(const void *src, uint4 *lds_wave_base) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) leaving the other counters alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
 // The block barrier of the K loop. __syncthreads() would also wait for every
 // load still in flight (its workgroup fence covers the LDS writes of
 // global_load_lds, even with the fence narrowed to LDS), the later stages'

@@ -74,6 +74,8 @@ struct th_state {
     size_t kv_elem = 4;
     float *attn_part = nullptr;  // attention partials for the fused path
     size_t attn_part_floats = 0;
+    void *kv_planes = nullptr;  // a layer's keys and values as bf16 hi/lo planes (f32 caches, prefill)
+    size_t kv_planes_bytes = 0;
     uint64_t *argmax_part = nullptr;
     th::StepState *step = nullptr;  // device
     uint32_t *tokens_dev = nullptr;
@@ -247,6 +249,10 @@ int ensure_fused_state(th_state *s) {
             std::max(s->attn_part_floats, th::attention_scratch(n, (size_t)c.num_attention_heads, hd, ns));
     }
     if (s->attn_part_floats) TH_HIP(hipMalloc(&s->attn_part, s->attn_part_floats * sizeof(float)));
+    if (s->kv_dtype == TH_KV_F32 && s->fb >= th::kGemmMinTokens && hd == 128) {
+        s->kv_planes_bytes = th::attention_planes_bytes(s->max_len, (size_t)c.num_key_value_heads);
+        TH_HIP(hipMalloc(&s->kv_planes, s->kv_planes_bytes));
+    }
     TH_HIP(hipMalloc(&s->argmax_part, th::argmax_partials((size_t)c.vocab_size) * sizeof(uint64_t)));
     TH_HIP(hipMalloc(&s->step, sizeof(th::StepState)));
     s->step_fused = th::step_supported((int)H, (int)I, (int)c.num_attention_heads, (int)c.num_key_value_heads,
@@ -483,7 +489,10 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
             aa.out_hi = hi;
             aa.out_lo = lo;
         }
-        TH_HIP(th::launch_attention(st, aa, n, hd));
+        if (s->kv_planes && th::attention_planes_supported(aa, n, hd))
+            TH_HIP(th::launch_attention_planes(st, aa, n, hd, s->kv_planes, s->kv_planes_bytes, s->max_len));
+        else
+            TH_HIP(th::launch_attention(st, aa, n, hd));
 
         if (hl) {
             TRY(single_gemm(L.o->ptr, qd, ks_o, hi, lo));
@@ -752,7 +761,7 @@ void th_state_destroy(th_state *s) {
                     s->fgate,   s->fup,        s->fy,   s->kv,         s->attn_part,  s->argmax_part,
                     s->step,    s->tokens_dev, s->logits_dev, s->sx_a, s->sx_b, s->s_y, s->s_qkv,
                     s->s_att, s->s_o, s->s_h, s->s_part, s->s_words, s->s_err, s->fsplit, s->s_sample,
-                    s->s_cand};
+                    s->s_cand, s->kv_planes};
     for (void *p : ptrs) free_dev(p);
     delete s;
 }

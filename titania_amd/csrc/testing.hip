@@ -5,6 +5,7 @@
 // entry points, th_forward, th_decode) never calls them. They allocate the
 // small device state a kernel needs (step state, exchange words, bf16 hi/lo
 // operands) and free it before returning.
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -264,6 +265,49 @@ int th_test_add_rmsnorm_parts(th_device *dev, th_buffer *x, const th_buffer *par
                                         nullptr, hi, lo, rows, gain->ptr, dim, eps));
     hl_to_f32_kernel<<<256, 256, 0, dev->stream>>>(hi, lo, x->len, xn->ptr);
     TH_HIP(hipGetLastError());
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    return TH_OK;
+}
+
+int th_test_attention_prefill(th_device *dev, const th_buffer *q, const th_buffer *k_cache, const th_buffer *v_cache,
+                              size_t max_len, size_t pos, size_t n, size_t n_heads, size_t n_kv_heads, int planes,
+                              th_buffer *out) {
+    TH_REQUIRE(dev && q && k_cache && v_cache && out, "th_test_attention_prefill: null argument");
+    const size_t hd = 128;
+    TH_REQUIRE(n > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && pos + n <= max_len,
+               "heads must split into KV groups and the tokens fit the caches");
+    TH_REQUIRE(q->len == n * n_heads * hd && out->len == n * n_heads * hd, "q and out hold n x n_heads x 128");
+    TH_REQUIRE(k_cache->len >= n_kv_heads * max_len * hd && v_cache->len >= n_kv_heads * max_len * hd,
+               "caches hold [n_kv_heads][max_len][128]");
+    th::AttnKernelArgs a{};
+    a.out = out->ptr;
+    a.q = q->ptr;
+    a.k = k_cache->ptr;
+    a.v = v_cache->ptr;
+    a.n_heads = (int)n_heads;
+    a.n_kv_heads = (int)n_kv_heads;
+    a.group = (int)(n_heads / n_kv_heads);
+    a.pos = (long long)pos;
+    a.pos_stride = (long long)hd;
+    a.head_stride = (long long)(max_len * hd);
+    a.nsplit = th::attention_splits(n, n_heads, n_kv_heads, pos + n, hd);
+    a.kv_bf16 = 0;
+    a.scale = 1.0f / sqrtf((float)hd);
+    DevMem part, pl;
+    const size_t pf = th::attention_scratch(n, n_heads, hd, a.nsplit);
+    if (pf) {
+        TRY(part.alloc(pf * sizeof(float), dev->stream));
+        a.part_acc = static_cast<float *>(part.p);
+        a.part_ml = a.part_acc + n * n_heads * (size_t)a.nsplit * hd;
+    }
+    if (planes) {
+        TH_REQUIRE(th::attention_planes_supported(a, n, hd), "the planes kernel does not take this shape");
+        const size_t bytes = th::attention_planes_bytes(max_len, n_kv_heads);
+        TRY(pl.alloc(bytes, dev->stream));
+        TH_HIP(th::launch_attention_planes(dev->stream, a, n, hd, pl.p, bytes, max_len));
+    } else {
+        TH_HIP(th::launch_attention(dev->stream, a, n, hd));
+    }
     TH_HIP(hipStreamSynchronize(dev->stream));
     return TH_OK;
 }
