@@ -127,6 +127,28 @@ __device__ __forceinline__ bf16x8 frag(const uint4 *tile, int row, int lc) {
     return __builtin_bit_cast(bf16x8, tile[row * CH + (lc ^ swz<CH>(row))]);
 }
 
+// The (column tile, row tile) of this block. Blocks are dealt to the 8 XCDs
+// in turn (linear block id mod 8), and the blocks that one XCD runs at once
+// share its L2. In launch order, 32 consecutive blocks would otherwise take
+// 32 different weight tiles of one row of tokens, so every weight chunk would
+// miss in L2. Here each XCD takes a contiguous range of tiles, ordered in
+// panels of PANEL row tiles (down the panel, then across): the blocks an XCD
+// runs together cover a few weight tiles and a few token tiles, and share
+// both. The map is a bijection whatever the XCD count; only the speed assumes it.
+template <int PANEL>
+__device__ __forceinline__ void tile_of_block(int &tx, int &ty) {
+    const int gx = (int)gridDim.x, gy = (int)gridDim.y, nt = gx * gy;
+    const int lin = (int)blockIdx.x + (int)blockIdx.y * gx;
+    constexpr int kXcds = 8;
+    const int xcd = lin % kXcds, i = lin / kXcds, q = nt / kXcds, r = nt % kXcds;
+    const int t = xcd * q + (xcd < r ? xcd : r) + i;  // this XCD's range starts at xcd q + min(xcd, r)
+    const int ph = gy < PANEL ? gy : PANEL;           // rows of a full panel
+    const int panel = t / (ph * gx), w = t % (ph * gx);
+    const int rows = gy - panel * ph < ph ? gy - panel * ph : ph;  // rows of this (maybe last) panel
+    tx = w / rows;
+    ty = panel * ph + w % rows;
+}
+
 // The matrix that the row tile r0 of the concatenation falls in: its weights
 // from its local row, output, row count and local row. Selected without
 // indexing the argument arrays by a run-time value, which would copy them to
@@ -166,7 +188,7 @@ struct HeadTile {
 };
 
 template <class T, int EPI = kStoreTile, typename KV = float>
-__device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict__ hi,
+__device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__restrict__ hi,
                                           const uint16_t *__restrict__ lo, int n, int cols,
                                           float *__restrict__ part, int ksplit, PairTile pt = {},
                                           HeadTile ht = {}) {
@@ -174,7 +196,7 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
     constexpr int FM = T::FM, FN = T::FN, kStages = T::kStages;
     __shared__ typename T::Stage ring[kStages];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * T::BM;
+    const int t0 = ty * T::BM;
     const int rl = sg.local;
     const int wm = (wave / T::WGN) * (T::BM / T::WGM), wn = (wave % T::WGN) * (T::BN / T::WGN);
     const int fr = lane & 15, fq = lane >> 4;  // fragment row, quarter of the K slice
@@ -316,13 +338,17 @@ __device__ __forceinline__ void gemm_tile(SegTile sg, const uint16_t *__restrict
 __global__ __launch_bounds__(Small::NT, 2) void gemm_kernel(Segs sg, const uint16_t *__restrict__ hi,
                                                         const uint16_t *__restrict__ lo, int n, int cols,
                                                         float *__restrict__ part, int ksplit) {
-    gemm_tile<Small>(seg_tile(sg, blockIdx.x * Small::BN), hi, lo, n, cols, part, ksplit);
+    int tx, ty;
+    tile_of_block<8>(tx, ty);
+    gemm_tile<Small>(ty, seg_tile(sg, tx * Small::BN), hi, lo, n, cols, part, ksplit);
 }
 
 __global__ __launch_bounds__(Large::NT, 1) void gemm_large_kernel(Segs sg, const uint16_t *__restrict__ hi,
                                                               const uint16_t *__restrict__ lo, int n, int cols,
                                                               float *__restrict__ part, int ksplit) {
-    gemm_tile<Large>(seg_tile(sg, blockIdx.x * Large::BN), hi, lo, n, cols, part, ksplit);
+    int tx, ty;
+    tile_of_block<4>(tx, ty);
+    gemm_tile<Large>(ty, seg_tile(sg, tx * Large::BN), hi, lo, n, cols, part, ksplit);
 }
 
 // gate and up in one launch, block x taking rows [x BN/2, (x + 1) BN/2) of
@@ -332,8 +358,10 @@ __global__ __launch_bounds__(T::NT, T::NT == 256 ? 2 : 1) void gemm_silu_kernel(
     const uint16_t *__restrict__ gate, const uint16_t *__restrict__ up, const uint16_t *__restrict__ hi,
     const uint16_t *__restrict__ lo, int n, int cols, int inter, uint16_t *__restrict__ h_hi,
     uint16_t *__restrict__ h_lo) {
-    const PairTile pt{gate, up, h_hi, h_lo, inter, (int)blockIdx.x * (T::BN / 2)};
-    gemm_tile<T, kSiluPairs>(SegTile{}, hi, lo, n, cols, nullptr, 1, pt);
+    int tx, ty;
+    tile_of_block<T::NT == 256 ? 8 : 4>(tx, ty);
+    const PairTile pt{gate, up, h_hi, h_lo, inter, tx * (T::BN / 2)};
+    gemm_tile<T, kSiluPairs>(ty, SegTile{}, hi, lo, n, cols, nullptr, 1, pt);
 }
 
 // q, k and v in one launch, block x taking attention head x of the
@@ -346,12 +374,14 @@ __global__ __launch_bounds__(Head::NT, 2) void gemm_qkv_kernel(const uint16_t *_
                                                                const uint16_t *__restrict__ hi,
                                                                const uint16_t *__restrict__ lo, int n, int cols,
                                                                QkvPostArgs a) {
-    const int h = blockIdx.x, nq = a.n_heads, nkv = a.n_kv_heads;
+    int h, ty;
+    tile_of_block<8>(h, ty);
+    const int nq = a.n_heads, nkv = a.n_kv_heads;
     const int role = h < nq ? 0 : h < nq + nkv ? 1 : 2;
     const int head = role == 0 ? h : role == 1 ? h - nq : h - nq - nkv;
     const uint16_t *w = (role == 0 ? wq : role == 1 ? wk : wv) + (size_t)head * 128 * cols;
     SegTile sg{w, nullptr, 128, 0};
-    gemm_tile<Head, kQkvHead, KV>(sg, hi, lo, n, cols, nullptr, 1, PairTile{}, HeadTile{&a, role, head});
+    gemm_tile<Head, kQkvHead, KV>(ty, sg, hi, lo, n, cols, nullptr, 1, PairTile{}, HeadTile{&a, role, head});
 }
 
 // split_bf16 of 4 elements a thread.
