@@ -1129,6 +1129,10 @@ __global__ __launch_bounds__(256) void kv_planes_kernel(KvPlaneArgs a) {
     }
 }
 
+// Waves of an attn_planes_kernel block (each 128 / 16 / kPlaneWaves sets of
+// 16 rows).
+constexpr int kPlaneWaves = 8;
+
 struct PlaneRefs {
     const uint16_t *kh, *kl, *vh, *vl;
     long long plane_len;
@@ -1140,8 +1144,10 @@ struct PlaneRefs {
 // fragment read's 16 rows land on distinct banks: K row r keeps logical
 // chunk c at c ^ (r & 15), V^T row r at c ^ ((r >> 1) & 7) (two 128-byte
 // rows share a bank line).
-__global__ __launch_bounds__(512, 1) void attn_planes_kernel(AttnKernelArgs a, PlaneRefs pl, int n) {
-    constexpr int NW = 8, NT = 64 * NW, SETS = kGqaRows / 16 / NW, RW = 16 * SETS;
+template <int NW>
+__global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs a, PlaneRefs pl, int n) {
+    constexpr int NT = 64 * NW, SETS = kGqaRows / 16 / NW, RW = 16 * SETS;
+    constexpr int SPW = 16 / NW;  // 1 KB spans a wave fills of each 16 KB tile
     constexpr int HD = 128, KT = kGqaKeys;
     static_assert(KT == 64 && SETS >= 1, "64-key tiles");
     constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
@@ -1195,19 +1201,19 @@ __global__ __launch_bounds__(512, 1) void attn_planes_kernel(AttnKernelArgs a, P
     const float scale2 = a.scale * kLog2e;
     const uint16_t *khg = pl.kh + (long long)g * pl.plane_len * HD, *klg = pl.kl + (long long)g * pl.plane_len * HD;
     const uint16_t *vhg = pl.vh + (long long)g * HD * pl.plane_len, *vlg = pl.vl + (long long)g * HD * pl.plane_len;
-    // Each wave fills two 1 KB spans of each tile: K spans are 4 keys, V^T
-    // spans 8 dimensions. Eight loads a wave a stage.
+    // Each wave fills SPW 1 KB spans of each tile: K spans are 4 keys, V^T
+    // spans 8 dimensions.
     auto issue = [&](Stage &st, long long c0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int span = 2 * wave + i, p = span * 64 + lane, row = p >> 4, pc = p & 15;
+        for (int i = 0; i < SPW; ++i) {
+            const int span = SPW * wave + i, p = span * 64 + lane, row = p >> 4, pc = p & 15;
             const long long off = (c0 + row) * HD + 8 * (pc ^ (row & 15));
             dma16(khg + off, st.kh + span * 64);
             dma16(klg + off, st.kl + span * 64);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int span = 2 * wave + i, p = span * 64 + lane, row = p >> 3, pc = p & 7;
+        for (int i = 0; i < SPW; ++i) {
+            const int span = SPW * wave + i, p = span * 64 + lane, row = p >> 3, pc = p & 7;
             const long long off = (long long)row * pl.plane_len + c0 + 8 * (pc ^ ((row >> 1) & 7));
             dma16(vhg + off, st.vh + span * 64);
             dma16(vlg + off, st.vl + span * 64);
@@ -1447,7 +1453,7 @@ hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_
     const PlaneRefs pr{c.kh, c.kl, c.vh, c.vl, plane_len};
     const int qt = kGqaRows / k.group;
     dim3 grid((unsigned)((n + qt - 1) / qt), (unsigned)k.n_kv_heads, (unsigned)k.nsplit);
-    attn_planes_kernel<<<grid, 512, 0, s>>>(k, pr, (int)n);
+    attn_planes_kernel<kPlaneWaves><<<grid, 64 * kPlaneWaves, 0, s>>>(k, pr, (int)n);
     e = hipGetLastError();
     if (e != hipSuccess || k.nsplit == 1) return e;
     return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128, k.out_hi,
