@@ -78,6 +78,15 @@ def test_qwen06_prefill512_greedy128(hip):
     check_workload(hip, QWEN3_0_6B, seed=4, n_prompt=512, steps=128, what="qwen3-0.6b 512+128")
 
 
+def test_qwen06_two_chunk_prefill(hip):
+    """Two layers of the Qwen3-0.6B shape, a 2600-token prompt: two fused
+    prefill chunks, the second at positions 2048.. (its attention reads the
+    first chunk's keys and values through the planes), then 8 greedy steps on
+    the split attention path (2608 positions: more than the fused launch's
+    32 chunks a head)."""
+    check_workload(hip, QWEN3_0_6B.with_layers(2), seed=12, n_prompt=2600, steps=8, what="qwen3-0.6b x2 2600+8")
+
+
 def test_qwen4b_shape_reduced_depth(hip):
     """Three layers of the Qwen3-4B shape, a 600-token prompt, 32 greedy steps."""
     check_workload(hip, QWEN3_4B.with_layers(3), seed=9, n_prompt=600, steps=32, what="qwen3-4b x3 600+32")
