@@ -415,16 +415,19 @@ bool gemm_supported(size_t rows, size_t cols) {
 
 namespace {
 
-// A launch takes the large tile when it has at least three large tiles a CU
+// A launch takes the large tile when it has at least two large tiles a CU
 // (and every matrix's rows are whole large tiles). Fewer leave the last round
 // of one-block-a-CU tiles partly empty, and the small tile, two blocks a CU
 // over four times the grid, finishes first (measured on the Qwen3 prefill
-// shapes: 2048 tokens x 19456 x 2560 607 against 703 us, 512 tokens x 19456 x
-// 2560 203 against 180 us). A single matrix with one to three large tiles a
-// CU and a deep K range (at least 96 steps) takes the large tile with K split
-// in two (2048 tokens x 2560 x 9728: 311 against 346 us; with 64 steps,
-// 2560 x 4096, the small tile stays ahead).
-constexpr size_t kLargeMinTiles = 768;
+// shapes: 512 tokens x 19456 x 2560 203 against 180 us). With the XCD-aware
+// tile order, two large tiles a CU already pay: a 2048-token Qwen3-0.6B
+// prefill (its q/k/v GEMM, 512 large tiles) 9.26 -> 8.93 ms with the
+// threshold at 512 rather than 768 tiles. A single matrix with one to three
+// large tiles a CU and a deep K range (at least 96 steps) takes the large
+// tile with K split in two (2048 tokens x 2560 x 9728: 311 against 346 us;
+// with 64 steps, 2560 x 4096, the small tile stays ahead).
+constexpr size_t kLargeMinTiles = 512;
+constexpr size_t kLargeSplitMinTiles = 256;
 
 struct Plan {
     bool large;
@@ -435,7 +438,7 @@ Plan gemm_plan(size_t n, size_t rows, size_t cols, int n_outs, bool rows_large) 
     const size_t nk = cols / BK;
     const size_t lt = rows_large ? (rows / Large::BN) * ((n + Large::BM - 1) / Large::BM) : 0;
     if (lt >= kLargeMinTiles) return {true, 1};
-    if (n_outs == 1 && lt >= kLargeMinTiles / 3 && nk >= 96) return {true, 2};
+    if (n_outs == 1 && lt >= kLargeSplitMinTiles && nk >= 96) return {true, 2};
     if (n_outs != 1) return {false, 1};
     // Small tiles: a single matrix with few row tiles (o, down) splits K so
     // that the launch still fills the chip, keeping at least 4 K steps a split.
