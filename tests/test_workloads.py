@@ -47,14 +47,20 @@ def oracle_greedy(r: ref.RefModel, prompt, steps: int, max_len: int):
     return first, np.array(toks, np.uint32), np.array(gaps), logits
 
 
-def check_workload(hip, cfg: Config, seed: int, n_prompt: int, steps: int, what: str):
+def check_workload(hip, cfg: Config, seed: int, n_prompt: int, steps: int, what: str, split: int = 0):
+    """The oracle against the fused forward of the prompt (in two calls, the
+    second at position `split`, when split > 0) and the captured decode."""
     w = synth.weights(cfg, seed=seed)
     r = ref.RefModel(cfg, w)
     prompt = synth.prompt(n_prompt, cfg.vocab_size, seed=seed + 1)
     first, rtoks, gaps, last = oracle_greedy(r, prompt, steps, n_prompt + steps)
     m = Model(hip, cfg, w)
     st = State(m, n_prompt + steps, TH_KV_F32)
-    got = m.forward(st, prompt, 0, TH_PATH_FUSED)
+    if split:
+        m.forward(st, prompt[:split], 0, TH_PATH_FUSED, want_logits=False)
+        got = m.forward(st, prompt[split:], split, TH_PATH_FUSED)
+    else:
+        got = m.forward(st, prompt, 0, TH_PATH_FUSED)
     toks, logits = m.decode(st, n_prompt, steps, keep_logits=True)
     st.close()
     m.close()
@@ -79,12 +85,13 @@ def test_qwen06_prefill512_greedy128(hip):
 
 
 def test_qwen06_two_chunk_prefill(hip):
-    """Two layers of the Qwen3-0.6B shape, a 2600-token prompt: two fused
-    prefill chunks, the second at positions 2048.. (its attention reads the
-    first chunk's keys and values through the planes), then 8 greedy steps on
+    """Two layers of the Qwen3-0.6B shape, a 2600-token prompt fed in two
+    forward calls, the second at positions 2048.. (its attention reads the
+    first call's keys and values through the planes), then 8 greedy steps on
     the split attention path (2608 positions: more than the fused launch's
     32 chunks a head)."""
-    check_workload(hip, QWEN3_0_6B.with_layers(2), seed=12, n_prompt=2600, steps=8, what="qwen3-0.6b x2 2600+8")
+    check_workload(hip, QWEN3_0_6B.with_layers(2), seed=12, n_prompt=2600, steps=8, what="qwen3-0.6b x2 2600+8",
+                   split=2048)
 
 
 def test_qwen4b_shape_reduced_depth(hip):
