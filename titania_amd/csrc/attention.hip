@@ -777,8 +777,11 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
     const int G = a.group, QT = kGqaRows / G;
-    const int g = blockIdx.y;
-    const int t0 = blockIdx.x * QT;
+    // Blocks in order of decreasing work (the last token tiles, which see
+    // the most keys, first), as in attn_planes_kernel.
+    const int gx = (int)gridDim.x, gy = (int)gridDim.y, lin = (int)blockIdx.x + (int)blockIdx.y * gx;
+    const int g = lin % gy;
+    const int t0 = (gx - 1 - lin / gy) * QT;
     const int nq = n - t0 < QT ? n - t0 : QT;
     const long long pos = a.pos_dev ? *a.pos_dev : a.pos;
     // Rows of set s: block row r = RW wave + 16 s + li is head g G + r / QT,
@@ -1162,8 +1165,13 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
     const int G = a.group, QT = kGqaRows / G;
-    const int g = blockIdx.y;
-    const int t0 = blockIdx.x * QT;
+    // Blocks in order of decreasing work: a token tile attends to every key
+    // up to its last query, so the last tiles have the most; launching them
+    // first (every KV group's last tile, then the one before, ...) keeps the
+    // lightest blocks for the end of the launch instead of the heaviest.
+    const int gx = (int)gridDim.x, gy = (int)gridDim.y, lin = (int)blockIdx.x + (int)blockIdx.y * gx;
+    const int g = lin % gy;
+    const int t0 = (gx - 1 - lin / gy) * QT;
     const int nq = n - t0 < QT ? n - t0 : QT;
     const long long pos = a.pos;
     int qloc[SETS], head[SETS];
