@@ -25,7 +25,7 @@ from oracle import ref
 from titania_amd import Tensor
 from titania_amd._lib import LIB_PATH, check
 from titania_amd.synth import bf16_to_f32, f32_to_bf16, normal_bf16
-from util import assert_close, rel_error
+from util import assert_close, attention_f64, rel_error
 
 pytestmark = pytest.mark.gpu
 
@@ -309,12 +309,15 @@ def test_add_rmsnorm_parts(hip, tlib, dim, rows, n_parts):
 
 
 @pytest.mark.parametrize("n,pos,H,KVH", [(512, 0, 16, 8), (100, 37, 16, 8), (1500, 600, 16, 8), (300, 20, 32, 8),
-                                         (64, 1000, 32, 8), (200, 5, 16, 2), (100, 3, 8, 8)])
+                                         (64, 1000, 32, 8), (200, 5, 16, 2), (100, 3, 8, 8), (2048, 0, 32, 8),
+                                         (2100, 150, 32, 8), (4096, 0, 16, 8)])
 def test_attention_planes(hip, tlib, n, pos, H, KVH):
     """Prefill attention through the bf16 planes (keys and values split once
     per call) gives the per-block-split kernel's output bit for bit, and the
-    oracle's within the per-kernel bar. Cache rows past pos + n hold NaN: a
-    read of them would reach the output."""
+    oracle's within the per-kernel bar (exact float64 attention past the
+    oracle's sizes). The last three shapes take the planes kernel's 256-row
+    blocks. Cache rows past pos + n hold NaN: a read of them would reach the
+    output."""
     hd, max_len = 128, pos + n + 70
     rng = np.random.default_rng(n + pos + H)
     q = rng.standard_normal(n * H * hd).astype(np.float32)
@@ -337,3 +340,7 @@ def test_attention_planes(hip, tlib, n, pos, H, KVH):
                             pos, H, hd, KVH)
         assert rel_error(outs[1], exp) <= 1e-3
         assert_close(outs[1], exp, rel=1e-4, abs_=2e-5, what=f"attention n={n} pos={pos} {H}/{KVH}")
+    else:
+        exp = attention_f64(q, kc, vc, pos, H, KVH)
+        assert rel_error(outs[1], exp) <= 1e-3
+        assert_close(outs[1], exp, rel=1e-4, abs_=2e-5, what=f"attention n={n} pos={pos} {H}/{KVH} (float64)")

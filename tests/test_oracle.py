@@ -24,7 +24,7 @@ import torch
 from oracle import ref
 from titania_amd import synth
 from titania_amd.config import Config
-from util import load_fixture
+from util import attention_f64, load_fixture
 
 
 rng = np.random.default_rng(1234)
@@ -215,6 +215,22 @@ def test_attention_float64(pos, n, heads, kv):
     got = ref.attention(q, k, v, pos, heads, hd, kv)
     exp = attention_float64(q, k, v, pos, heads, hd, kv)
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("pos,n,heads,kv", [(0, 5, 4, 2), (7, 9, 16, 8), (3, 4, 8, 1)])
+def test_attention_f64_helper(pos, n, heads, kv):
+    """The vectorised float64 attention the GPU tests use past the oracle's
+    sizes (head-major caches with rows past the context) agrees with the
+    oracle and with the per-row float64 loop above."""
+    hd = 128
+    q = rng.standard_normal(n * heads * hd).astype(np.float32)
+    kc = rng.standard_normal((kv, pos + n + 3, hd)).astype(np.float32)
+    vc = rng.standard_normal((kv, pos + n + 3, hd)).astype(np.float32)
+    got = attention_f64(q, kc, vc, pos, heads, kv)
+    kp = kc[:, :pos + n].transpose(1, 0, 2).copy()
+    vp = vc[:, :pos + n].transpose(1, 0, 2).copy()
+    np.testing.assert_allclose(got, attention_float64(q, kp, vp, pos, heads, hd, kv), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(ref.attention(q, kp, vp, pos, heads, hd, kv), got, rtol=1e-5, atol=2e-6)
 
 
 def test_attention_single_position_is_v():

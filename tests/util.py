@@ -64,3 +64,21 @@ def load_fixture(name: str):
     f = np.load(GOLDEN / f"hf_qwen3_{name}.npz")
     meta = json.loads(str(f["meta"]))
     return Config(**meta["config"]), meta, f["tokens"], f["logits"]
+
+
+def attention_f64(q, kc, vc, pos, H, KVH):
+    """Causal GQA attention in float64 (model/cpu.rs:113-149 in exact
+    arithmetic): q [n][H][128], caches [KVH][positions][128]."""
+    hd = 128
+    n, G = q.size // (H * hd), H // KVH
+    qh = q.reshape(n, H, hd).astype(np.float64)
+    out = np.empty((n, H, hd))
+    mask = np.arange(pos + n)[None, :] > (pos + np.arange(n))[:, None]
+    for h in range(H):
+        k = kc[h // G, :pos + n].astype(np.float64)
+        v = vc[h // G, :pos + n].astype(np.float64)
+        s = qh[:, h] @ k.T / np.sqrt(hd)
+        s[mask] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p @ v) / p.sum(axis=1, keepdims=True)
+    return out.reshape(-1)

@@ -1135,9 +1135,19 @@ __global__ __launch_bounds__(256) void kv_planes_kernel(KvPlaneArgs a) {
     }
 }
 
-// Waves of an attn_planes_kernel block (each 128 / 16 / kPlaneWaves sets of
-// 16 rows).
-constexpr int kPlaneWaves = 8;
+// Waves of an attn_planes_kernel block (each ROWS / 16 / kPlaneWaves sets of
+// 16 (token, head) rows). Two sets a wave halve the LDS reads per product
+// (every wave reads the whole tile) and double the products per staged
+// tile, at 246 VGPRs, still two waves a SIMD: 4B-shape 8192-token prefill
+// 175.9 -> 168.1 ms, Qwen3-0.6B 8192 tokens 39.7 -> 36.6 ms. With half the
+// blocks they are slower where blocks are few (0.6B, 512 tokens: 3.05 ->
+// 3.22 ms), so they run only once the launch has a block per CU unsplit.
+constexpr int kPlaneWaves = 8, kPlaneRowsWide = 256;
+
+static bool plane_rows_wide(size_t n, int group, int n_kv_heads) {
+    const size_t qt = (size_t)(kPlaneRowsWide / group);
+    return (n + qt - 1) / qt * (size_t)n_kv_heads >= 256;
+}
 
 struct PlaneRefs {
     const uint16_t *kh, *kl, *vh, *vl;
@@ -1150,9 +1160,9 @@ struct PlaneRefs {
 // fragment read's 16 rows land on distinct banks: K row r keeps logical
 // chunk c at c ^ (r & 15), V^T row r at c ^ ((r >> 1) & 7) (two 128-byte
 // rows share a bank line).
-template <int NW>
+template <int NW, int ROWS>
 __global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs a, PlaneRefs pl, int n) {
-    constexpr int NT = 64 * NW, SETS = kGqaRows / 16 / NW, RW = 16 * SETS;
+    constexpr int NT = 64 * NW, SETS = ROWS / 16 / NW, RW = 16 * SETS;
     constexpr int SPW = 16 / NW;  // 1 KB spans a wave fills of each 16 KB tile
     constexpr int HD = 128, KT = kGqaKeys;
     static_assert(KT == 64 && SETS >= 1, "64-key tiles");
@@ -1164,7 +1174,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs 
     __shared__ Stage ring[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int G = a.group, QT = kGqaRows / G;
+    const int G = a.group, QT = ROWS / G;
     // Blocks in order of decreasing work: a token tile attends to every key
     // up to its last query, so the last tiles have the most; launching them
     // first (every KV group's last tile, then the one before, ...) keeps the
@@ -1462,9 +1472,15 @@ hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const PlaneRefs pr{c.kh, c.kl, c.vh, c.vl, plane_len};
-    const int qt = kGqaRows / k.group;
+    // Rows a block: the wide form only unsplit, so that every row sees the
+    // key tiles (and the products) of the 128-row form and attn_gqa_kernel.
+    const bool wide = k.nsplit == 1 && plane_rows_wide(n, k.group, k.n_kv_heads);
+    const int qt = (wide ? kPlaneRowsWide : kGqaRows) / k.group;
     dim3 grid((unsigned)((n + qt - 1) / qt), (unsigned)k.n_kv_heads, (unsigned)k.nsplit);
-    attn_planes_kernel<kPlaneWaves><<<grid, 64 * kPlaneWaves, 0, s>>>(k, pr, (int)n);
+    if (wide)
+        attn_planes_kernel<kPlaneWaves, kPlaneRowsWide><<<grid, 64 * kPlaneWaves, 0, s>>>(k, pr, (int)n);
+    else
+        attn_planes_kernel<kPlaneWaves, kGqaRows><<<grid, 64 * kPlaneWaves, 0, s>>>(k, pr, (int)n);
     e = hipGetLastError();
     if (e != hipSuccess || k.nsplit == 1) return e;
     return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128, k.out_hi,
