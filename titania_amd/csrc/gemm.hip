@@ -37,9 +37,13 @@ constexpr int BK = 64;                    // K range multiple every launch needs
 // A block tile of BM tokens x BN weight rows, its WGM x WGN waves each a
 // BM/WGM x BN/WGN part, K staged BK columns at a time through `STAGES` LDS
 // stages.
-template <int BM_, int BN_, int BK_, int STAGES_, int WGM_ = 2, int WGN_ = 2>
+template <int BM_, int BN_, int BK_, int STAGES_, int WGM_ = 2, int WGN_ = 2, bool REG_PAIRS_ = false>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, kStages = STAGES_;
+    // Paired (gate/up) tiles: the weight tile interleaves 16-row groups of
+    // gate and up, so that a wave holds both halves of its outputs and the
+    // SiLU epilogue runs in registers (otherwise they meet in LDS).
+    static constexpr bool REG_PAIRS = REG_PAIRS_;
     static constexpr int WGM = WGM_, WGN = WGN_, NT = 64 * WGM * WGN;  // waves: WGM down x WGN across
     static constexpr int CH = BK / 8;  // 16-byte chunks per tile row (bf16)
     static constexpr int TA = BM * CH, TB = BN * CH;     // 16-byte chunks per tile
@@ -53,9 +57,16 @@ struct Tile {
 using Small = Tile<64, 64, 64, 3>;    // 24 KB a stage: two blocks a CU
 using Large = Tile<128, 128, 64, 3, 4, 2>;  // 48 KB a stage: one block a CU, eight waves of 32 x 64
 using Head = Tile<32, 128, 64, 3>;          // one attention head's 128 rows: 24 KB a stage, two blocks a CU
+// 48 KB a stage of 32 K columns: one block a CU, eight waves of 64 x 128. A
+// wave reads 16 fragments from LDS per 64 products, against 8 per 16 in the
+// 32 x 64 waves of the large tile.
+using Huge = Tile<256, 256, 32, 3, 4, 2, true>;
 
+// The XOR swizzle of a row's 16-byte chunks: a fragment read takes one chunk
+// of 16 consecutive rows, and the 64 banks span 256 bytes, 16 / CH rows of
+// CH chunks; rows that share a bank span differ in the swizzle.
 template <int CH>
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & (CH - 1); }
+__device__ __forceinline__ int swz(int row) { return (row / (16 / CH)) & (CH - 1); }
 
 // The block barrier of the K loop. __syncthreads() would also wait for every
 // load still in flight (its workgroup fence covers the LDS writes of
@@ -82,14 +93,16 @@ struct Segs {
 
 // Queues the loads of K step k0 into stage st: each wave fills whole 1 KB
 // spans (64 lanes x 16 B) of the stage. Weight rows [0, BN/2) of the tile
-// come from wa, the rest from wb. Token rows past n read row n - 1
-// (their results are never stored).
-template <class T>
+// come from wa, the rest from wb (with IL, 16-row groups alternate between
+// them). Token rows past n read row n - 1 (their results are never stored).
+template <class T, bool IL = false>
 __device__ __forceinline__ void issue_step(typename T::Stage &st, const uint16_t *hi, const uint16_t *lo,
                                            const uint16_t *wa, const uint16_t *wb, int t0, int n, int cols,
                                            int k0) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     auto w_row = [&](int row) {
+        if constexpr (IL)  // 16-row groups alternate between wa and wb
+            return ((row >> 4) & 1 ? wb : wa) + (size_t)((row >> 5) * 16 + (row & 15)) * cols;
         return row < T::BN / 2 ? wa + (size_t)row * cols : wb + (size_t)(row - T::BN / 2) * cols;
     };
     if constexpr (T::TA == T::TB) {
@@ -193,6 +206,7 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
                                           float *__restrict__ part, int ksplit, PairTile pt = {},
                                           HeadTile ht = {}) {
     constexpr bool PAIRED = EPI == kSiluPairs;
+    constexpr bool IL = PAIRED && T::REG_PAIRS;
     constexpr int FM = T::FM, FN = T::FN, kStages = T::kStages;
     __shared__ typename T::Stage ring[kStages];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -218,7 +232,7 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
 
 #pragma unroll
     for (int s = 0; s < kStages - 1; ++s)
-        if (s < nk) issue_step<T>(ring[s], hi, lo, wa, wb, t0, n, cols, s * T::BK);
+        if (s < nk) issue_step<T, IL>(ring[s], hi, lo, wa, wb, t0, n, cols, s * T::BK);
 
     for (int k = 0; k < nk; ++k) {
         // This wave's loads of step k are done once at most the later steps'
@@ -228,8 +242,8 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
         else wait_vm<0>();
         stage_barrier();
         if (k + kStages - 1 < nk)
-            issue_step<T>(ring[(k + kStages - 1) % kStages], hi, lo, wa, wb, t0, n, cols,
-                          (k + kStages - 1) * T::BK);
+            issue_step<T, IL>(ring[(k + kStages - 1) % kStages], hi, lo, wa, wb, t0, n, cols,
+                              (k + kStages - 1) * T::BK);
         const typename T::Stage &st = ring[k % kStages];
 #pragma unroll
         for (int ks = 0; ks < T::BK / 32; ++ks) {
@@ -252,7 +266,26 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
         }
     }
     // D[4 (l / 16) + i][l % 16]: token rows, weight-row columns.
-    if constexpr (PAIRED) {
+    if constexpr (IL) {
+        // Fragments 2p and 2p + 1 of a wave hold gate and up of the same 16
+        // outputs: h = silu(g) * u straight from the accumulators.
+        static_assert(FN % 2 == 0 && (T::BN / T::WGN) % 32 == 0, "whole gate/up fragment pairs a wave");
+#pragma unroll
+        for (int m = 0; m < FM; ++m)
+#pragma unroll
+            for (int p = 0; p < FN / 2; ++p)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = t0 + wm + m * 16 + fq * 4 + i;
+                    if (t >= n) continue;
+                    uint16_t h, l;
+                    split_bf16(silu(acc[m][2 * p][i]) * acc[m][2 * p + 1][i], h, l);
+                    const size_t o = (size_t)t * pt.inter + pt.r0 + wn / 2 + p * 16 + fr;
+                    pt.h_hi[o] = h;
+                    pt.h_lo[o] = l;
+                }
+        return;
+    } else if constexpr (PAIRED) {
         // gate and up of a row sit in different waves: through LDS (the ring
         // is free once every wave has left the K loop), then h = silu(g) * u
         // as hi/lo terms, four outputs a thread.
@@ -351,6 +384,13 @@ __global__ __launch_bounds__(Large::NT, 1) void gemm_large_kernel(Segs sg, const
     gemm_tile<Large>(ty, seg_tile(sg, tx * Large::BN), hi, lo, n, cols, part, ksplit);
 }
 
+__global__ __launch_bounds__(Huge::NT, 1) void gemm_huge_kernel(Segs sg, const uint16_t *__restrict__ hi,
+                                                            const uint16_t *__restrict__ lo, int n, int cols) {
+    int tx, ty;
+    tile_of_block<2>(tx, ty);
+    gemm_tile<Huge>(ty, seg_tile(sg, tx * Huge::BN), hi, lo, n, cols, nullptr, 1);
+}
+
 // gate and up in one launch, block x taking rows [x BN/2, (x + 1) BN/2) of
 // each, with the SiLU * up epilogue.
 template <class T>
@@ -359,7 +399,7 @@ __global__ __launch_bounds__(T::NT, T::NT == 256 ? 2 : 1) void gemm_silu_kernel(
     const uint16_t *__restrict__ lo, int n, int cols, int inter, uint16_t *__restrict__ h_hi,
     uint16_t *__restrict__ h_lo) {
     int tx, ty;
-    tile_of_block<T::NT == 256 ? 8 : 4>(tx, ty);
+    tile_of_block<T::NT == 256 ? 8 : T::BM == 256 ? 2 : 4>(tx, ty);
     const PairTile pt{gate, up, h_hi, h_lo, inter, tx * (T::BN / 2)};
     gemm_tile<T, kSiluPairs>(ty, SegTile{}, hi, lo, n, cols, nullptr, 1, pt);
 }
@@ -428,24 +468,29 @@ namespace {
 // with 64 steps, 2560 x 4096, the small tile stays ahead).
 constexpr size_t kLargeMinTiles = 512;
 constexpr size_t kLargeSplitMinTiles = 256;
+// The 256 x 256 tile from three tiles a CU.
+constexpr size_t kHugeMinTiles = 768;
 
 struct Plan {
-    bool large;
+    bool large, huge;
     int ksplit;
 };
 
-Plan gemm_plan(size_t n, size_t rows, size_t cols, int n_outs, bool rows_large) {
+// rows_large / rows_huge: every matrix's rows are whole large / huge tiles.
+Plan gemm_plan(size_t n, size_t rows, size_t cols, int n_outs, bool rows_large, bool rows_huge) {
     const size_t nk = cols / BK;
+    const size_t ht = rows_huge ? (rows / Huge::BN) * ((n + Huge::BM - 1) / Huge::BM) : 0;
+    if (ht >= kHugeMinTiles) return {true, true, 1};
     const size_t lt = rows_large ? (rows / Large::BN) * ((n + Large::BM - 1) / Large::BM) : 0;
-    if (lt >= kLargeMinTiles) return {true, 1};
-    if (n_outs == 1 && lt >= kLargeSplitMinTiles && nk >= 96) return {true, 2};
-    if (n_outs != 1) return {false, 1};
+    if (lt >= kLargeMinTiles) return {true, false, 1};
+    if (n_outs == 1 && lt >= kLargeSplitMinTiles && nk >= 96) return {true, false, 2};
+    if (n_outs != 1) return {false, false, 1};
     // Small tiles: a single matrix with few row tiles (o, down) splits K so
     // that the launch still fills the chip, keeping at least 4 K steps a split.
     const size_t tiles = (rows / Small::BN) * ((n + Small::BM - 1) / Small::BM);
     int ksplit = 1;
     while (ksplit < kGemmMaxSplitK && tiles * ksplit < 512 && (size_t)ksplit * 2 * 4 <= nk) ksplit *= 2;
-    return {false, ksplit};
+    return {false, false, ksplit};
 }
 
 }  // namespace
@@ -465,7 +510,8 @@ hipError_t launch_gemm_split(hipStream_t s, const float *x, size_t n, size_t col
 }
 
 int gemm_ksplit(size_t n, size_t rows, size_t cols, int n_outs) {
-    return gemm_plan(n, rows, cols, n_outs, rows % Large::BN == 0).ksplit;
+    // Only a single matrix splits K: its rows are the whole concatenation.
+    return gemm_plan(n, rows, cols, n_outs, rows % Large::BN == 0, n_outs == 1 && rows % Huge::BN == 0).ksplit;
 }
 
 hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t n, size_t cols,
@@ -486,10 +532,16 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
     }
     sg.n = n_outs;
     if (total / Small::BN > 65535) return hipErrorInvalidValue;
-    bool rows_large = true;
-    for (int i = 0; i < n_outs; ++i) rows_large = rows_large && outs[i].rows % Large::BN == 0;
-    const Plan plan = gemm_plan(n, total, cols, n_outs, rows_large);
-    if (plan.large && plan.ksplit == ksplit) {
+    bool rows_large = true, rows_huge = true;
+    for (int i = 0; i < n_outs; ++i) {
+        rows_large = rows_large && outs[i].rows % Large::BN == 0;
+        rows_huge = rows_huge && outs[i].rows % Huge::BN == 0;
+    }
+    const Plan plan = gemm_plan(n, total, cols, n_outs, rows_large, rows_huge);
+    if (plan.huge && ksplit == 1) {
+        dim3 grid((unsigned)(total / Huge::BN), (unsigned)((n + Huge::BM - 1) / Huge::BM));
+        gemm_huge_kernel<<<grid, Huge::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols);
+    } else if (plan.large && !plan.huge && plan.ksplit == ksplit) {
         dim3 grid((unsigned)(total / Large::BN), (unsigned)((n + Large::BM - 1) / Large::BM), (unsigned)ksplit);
         gemm_large_kernel<<<grid, Large::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
     } else {
@@ -506,8 +558,12 @@ hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *l
         n > ((size_t)1 << 24) || (n + Small::BM - 1) / Small::BM > 65535 || inter % (Large::BN / 2) ||
         ((uintptr_t)h_hi | (uintptr_t)h_lo) % 8)
         return hipErrorInvalidValue;
-    const Plan plan = gemm_plan(n, 2 * inter, cols, 2, true);
-    if (plan.large) {
+    const Plan plan = gemm_plan(n, 2 * inter, cols, 2, true, inter % (Huge::BN / 2) == 0);
+    if (plan.huge) {
+        dim3 grid((unsigned)(inter / (Huge::BN / 2)), (unsigned)((n + Huge::BM - 1) / Huge::BM));
+        gemm_silu_kernel<Huge><<<grid, Huge::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
+                                                          h_lo);
+    } else if (plan.large) {
         dim3 grid((unsigned)(inter / (Large::BN / 2)), (unsigned)((n + Large::BM - 1) / Large::BM));
         gemm_silu_kernel<Large><<<grid, Large::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
                                                            h_lo);
@@ -521,7 +577,7 @@ hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *l
 
 bool gemm_qkv_fused(size_t n, size_t q_rows, size_t kv_rows, size_t cols, size_t head_dim) {
     return head_dim == 128 && q_rows % 128 == 0 && kv_rows % 128 == 0 && cols % BK == 0 &&
-           !gemm_plan(n, q_rows + 2 * kv_rows, cols, 3, true).large;
+           !gemm_plan(n, q_rows + 2 * kv_rows, cols, 3, true, false).large;
 }
 
 hipError_t launch_gemm_qkv(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t cols, const uint16_t *wq,
