@@ -53,11 +53,18 @@ TH_API int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_w
 /* Prefill q/k/v GEMM on the matrix cores with the q/k norm + RoPE + KV
  * append epilogue, for n tokens at pos .. pos + n - 1: q_out = the rotated,
  * normalized q rows; k and v go to the caches (model.rs:108-120). xn holds
- * the normalized input rows. */
+ * the normalized input rows. With `planes` (or NULL), the epilogue also
+ * writes the prefill attention's bf16 planes of the new keys and values into
+ * it, as bf16 pairs in its floats: K hi, K lo [n_kv_heads][L][128], V^T hi,
+ * V^T lo [n_kv_heads][128][L] (L = max_len rounded up to 64; each 32-key
+ * slice of a V^T row holds key 4 g + i at column 8 g + i and key
+ * 16 + 4 g + i at column 8 g + 4 + i, g, i < 4); other positions are left
+ * as they were. */
 TH_API int th_test_gemm_qkv(th_device *dev, const th_buffer *xn, const th_weight *wq, const th_weight *wk,
                             const th_weight *wv, const th_weight *q_norm, const th_weight *k_norm, float eps,
                             const th_buffer *rope, th_buffer *k_cache, th_buffer *v_cache, size_t max_len,
-                            size_t pos, size_t n, size_t n_heads, size_t n_kv_heads, th_buffer *q_out);
+                            size_t pos, size_t n, size_t n_heads, size_t n_kv_heads, th_buffer *q_out,
+                            th_buffer *planes);
 
 /* Prefill gate/up GEMM with the SiLU epilogue: h = silu(xn . gate) *
  * (xn . up) for n rows (model.rs:137-140), as the f32 sum of the bf16 hi/lo

@@ -36,7 +36,7 @@ TEST_SIGNATURES = {
     "th_test_step_gemv": [_P, _P, _P, _P],
     "th_test_step_logits": [_P, _P, _P, _P, _P, _F, _P, C.POINTER(C.c_uint32)],
     "th_test_step_qkv_attn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P],
-    "th_test_gemm_qkv": [_P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P],
+    "th_test_gemm_qkv": [_P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P],
     "th_test_gemm_silu": [_P, _P, _P, _P, _SZ, _P],
     "th_test_add_rmsnorm_parts": [_P, _P, _P, _SZ, _P, _F, _P],
     "th_test_attention_prefill": [_P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, C.c_int, _P],
@@ -232,7 +232,7 @@ def test_step_qkv_attn(hip, tlib, shape, pos):
     assert np.array_equal(dk[:, :pos], kc[:, :pos]), "earlier keys untouched"
 
 
-@pytest.mark.parametrize("shape,n,pos", [("0.6b", 100, 0), ("0.6b", 512, 37), ("4b", 100, 20)])
+@pytest.mark.parametrize("shape,n,pos", [("0.6b", 100, 0), ("0.6b", 512, 37), ("0.6b", 512, 64), ("4b", 100, 20)])
 def test_gemm_qkv(hip, tlib, shape, n, pos):
     H, nh, nkv, _ = SHAPES[shape]
     hd, qd, kvd = 128, nh * 128, nkv * 128
@@ -246,8 +246,14 @@ def test_gemm_qkv(hip, tlib, shape, n, pos):
     table = ref.rope_table(max_len, hd, 1e6)
     Kc, Vc = hip.alloc(nkv * max_len * hd), hip.alloc(nkv * max_len * hd)
     XN, T, qo = buf(hip, xn), buf(hip, table), hip.alloc(n * qd)
+    # The planes, prefilled with bf16 NaN pairs that only the new positions may replace.
+    L = (max_len + 63) // 64 * 64
+    plane = nkv * 128 * L
+    sentinel = np.full(2 * plane, 0x7FC07FC0, np.uint32)
+    PL = buf(hip, sentinel.view(np.float32))
     check(tlib.th_test_gemm_qkv(hip.handle, XN.handle, Wq.handle, Wk.handle, Wv.handle, QN.handle, KN.handle,
-                                EPS, T.handle, Kc.handle, Vc.handle, max_len, pos, n, nh, nkv, qo.handle))
+                                EPS, T.handle, Kc.handle, Vc.handle, max_len, pos, n, nh, nkv, qo.handle,
+                                PL.handle))
     q = _head_norm_rope(ref.matmul(wq, qd, H, xn), qn, table, pos, nh)
     k = _head_norm_rope(ref.matmul(wk, kvd, H, xn), kn, table, pos, nkv).reshape(n, nkv, hd)
     v = ref.matmul(wv, kvd, H, xn).reshape(n, nkv, hd)
@@ -259,6 +265,41 @@ def test_gemm_qkv(hip, tlib, shape, n, pos):
     assert rel_error(dk, k) <= 1e-3 and rel_error(dv, v) <= 1e-3
     assert_close(dk, k, rel=1e-4, abs_=5e-5, what="keys")
     assert_close(dv, v, rel=1e-4, abs_=5e-5, what="values")
+    _check_planes(hip.read(PL).view(np.uint16), dk, dv, pos, n, nkv, L)
+
+
+def _check_planes(got, dk, dv, pos, n, nkv, L):
+    """The epilogue's planes are the bf16 hi/lo split of the cached keys and
+    values, bit for bit, at the new positions only: K rows at their
+    positions, V^T columns in the P^T operand order of the prefill attention
+    (a slice's column 8 g + i holds key 4 g + i for i < 4, else
+    16 + 4 g + i - 4)."""
+    hd = 128
+    plane = nkv * hd * L
+    kh, kl, vh, vl = (got[i * plane:(i + 1) * plane] for i in range(4))
+
+    def split(x):
+        h = f32_to_bf16(x)
+        return h, f32_to_bf16(x - bf16_to_f32(h))
+
+    key_of_col = [4 * g + i if i < 4 else 16 + 4 * g + i - 4 for g in range(4) for i in range(8)]
+    col_of_key = np.argsort(key_of_col)
+    assert sorted(key_of_col) == list(range(32))
+    want = np.full((4, plane), 0x7FC0, np.uint16)
+    k_hi, k_lo = split(dk)  # [n][nkv][hd]
+    v_hi, v_lo = split(dv)
+    p = np.arange(pos, pos + n)
+    cols = (p & ~31) + col_of_key[p & 31]
+    for g in range(nkv):
+        rows = (g * L + p)[:, None] * hd + np.arange(hd)[None, :]
+        want[0][rows] = k_hi[:, g]
+        want[1][rows] = k_lo[:, g]
+        vt = (g * hd + np.arange(hd))[None, :] * L + cols[:, None]
+        want[2][vt] = v_hi[:, g]
+        want[3][vt] = v_lo[:, g]
+    for i, (name, plane_got) in enumerate(zip(("K hi", "K lo", "V^T hi", "V^T lo"), (kh, kl, vh, vl))):
+        bad = np.flatnonzero(plane_got != want[i])
+        assert bad.size == 0, f"{name}: {bad.size} entries differ, first at {bad[:4]}"
 
 
 @pytest.mark.parametrize("H,I,n", [(1024, 3072, 100), (1024, 3072, 512), (2560, 9728, 100), (256, 3072, 8000)])

@@ -417,6 +417,16 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(float *__restric
     const long long th = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (th >= heads) return;
+    // The first kPre splits' partials are requested with the (max,
+    // denominator) pairs, so that the merge waits for one round trip.
+    constexpr int kPre = 8;
+    const float *pa = part_acc + th * nsplit * HD + lane * D;
+    float pre[kPre][D];
+#pragma unroll
+    for (int sp = 0; sp < kPre; ++sp)
+        if (sp < nsplit)
+#pragma unroll
+            for (int d = 0; d < D; ++d) pre[sp][d] = pa[(size_t)sp * HD + d];
     float ms = -INFINITY, ls = 0.f;
     if (lane < nsplit) {
         const float2 v = reinterpret_cast<const float2 *>(part_ml + th * nsplit * 2)[lane];
@@ -426,12 +436,18 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(float *__restric
     const float m = wave_max_dpp(ms);
     const float ws = ms != -INFINITY ? expf(ms - m) : 0.f;
     const float l = wave_sum_dpp(ls * ws);
-    const float *pa = part_acc + th * nsplit * HD + lane * D;
     float acc[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) acc[d] = 0.f;
-#pragma unroll 4
-    for (int sp = 0; sp < nsplit; ++sp) {
+#pragma unroll
+    for (int sp = 0; sp < kPre; ++sp) {
+        if (sp < nsplit) {
+            const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ws), sp));
+#pragma unroll
+            for (int d = 0; d < D; ++d) acc[d] += pre[sp][d] * w;
+        }
+    }
+    for (int sp = kPre; sp < nsplit; ++sp) {
         const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ws), sp));
 #pragma unroll
         for (int d = 0; d < D; ++d) acc[d] += pa[(size_t)sp * HD + d] * w;
@@ -1162,7 +1178,7 @@ struct PlaneRefs {
 // rows share a bank line).
 template <int NW, int ROWS>
 __global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs a, PlaneRefs pl, int n) {
-    constexpr int NT = 64 * NW, SETS = ROWS / 16 / NW, RW = 16 * SETS;
+    constexpr int SETS = ROWS / 16 / NW, RW = 16 * SETS;
     constexpr int SPW = 16 / NW;  // 1 KB spans a wave fills of each 16 KB tile
     constexpr int HD = 128, KT = kGqaKeys;
     static_assert(KT == 64 && SETS >= 1, "64-key tiles");
@@ -1448,30 +1464,49 @@ bool attention_planes_supported(const AttnKernelArgs &k, size_t n, size_t head_d
            k.head_stride % 4 == 0;
 }
 
-hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim, void *planes,
-                                   size_t planes_bytes, size_t max_len) {
-    if (n == 0) return hipSuccess;
-    if (!attention_planes_supported(k, n, head_dim) || !planes || k.pos < 0 || (size_t)k.pos + n > max_len ||
+PlanePtrs attention_planes_of(void *planes, size_t max_len, size_t n_kv_heads) {
+    const long long plane_len = (long long)((max_len + 63) / 64 * 64);
+    const size_t plane = n_kv_heads * 128 * (size_t)plane_len;
+    uint16_t *p0 = static_cast<uint16_t *>(planes);
+    return PlanePtrs{p0, p0 + plane, p0 + 2 * plane, p0 + 3 * plane, plane_len};
+}
+
+hipError_t launch_kv_planes(hipStream_t s, const AttnKernelArgs &k, size_t valid, void *planes, size_t planes_bytes,
+                            size_t max_len) {
+    if (valid == 0) return hipSuccess;
+    if (!planes || valid > max_len || k.kv_bf16 || k.pos_stride % 4 || k.head_stride % 4 ||
         attention_planes_bytes(max_len, (size_t)k.n_kv_heads) > planes_bytes || (uintptr_t)planes % 16)
         return hipErrorInvalidValue;
-    const long long plane_len = (long long)((max_len + 63) / 64 * 64);
-    const size_t plane = (size_t)k.n_kv_heads * 128 * (size_t)plane_len;
-    uint16_t *p0 = static_cast<uint16_t *>(planes);
+    const PlanePtrs pp = attention_planes_of(planes, max_len, (size_t)k.n_kv_heads);
     KvPlaneArgs c{};
     c.k = static_cast<const float *>(k.k);
     c.v = static_cast<const float *>(k.v);
     c.head_stride = k.head_stride;
     c.pos_stride = k.pos_stride;
-    c.kh = p0;
-    c.kl = p0 + plane;
-    c.vh = p0 + 2 * plane;
-    c.vl = p0 + 3 * plane;
-    c.plane_len = plane_len;
-    c.valid = k.pos + (long long)n;
+    c.kh = pp.kh;
+    c.kl = pp.kl;
+    c.vh = pp.vh;
+    c.vl = pp.vl;
+    c.plane_len = pp.plane_len;
+    c.valid = (long long)valid;
     kv_planes_kernel<<<dim3((unsigned)((c.valid + 63) / 64), (unsigned)k.n_kv_heads), 256, 0, s>>>(c);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const PlaneRefs pr{c.kh, c.kl, c.vh, c.vl, plane_len};
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim, void *planes,
+                                   size_t planes_bytes, size_t max_len, bool split_kv) {
+    if (n == 0) return hipSuccess;
+    if (!attention_planes_supported(k, n, head_dim) || !planes || k.pos < 0 || (size_t)k.pos + n > max_len ||
+        attention_planes_bytes(max_len, (size_t)k.n_kv_heads) > planes_bytes || (uintptr_t)planes % 16)
+        return hipErrorInvalidValue;
+    hipError_t e;
+    if (split_kv) {
+        e = launch_kv_planes(s, k, (size_t)k.pos + n, planes, planes_bytes, max_len);
+        if (e != hipSuccess) return e;
+    }
+    const PlanePtrs pp = attention_planes_of(planes, max_len, (size_t)k.n_kv_heads);
+    const long long plane_len = pp.plane_len;
+    const PlaneRefs pr{pp.kh, pp.kl, pp.vh, pp.vl, plane_len};
     // Rows a block: the wide form only unsplit, so that every row sees the
     // key tiles (and the products) of the 128-row form and attn_gqa_kernel.
     const bool wide = k.nsplit == 1 && plane_rows_wide(n, k.group, k.n_kv_heads);

@@ -157,8 +157,21 @@ hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, si
 // positions the caches hold). Host positions only (no pos_dev).
 size_t attention_planes_bytes(size_t max_len, size_t n_kv_heads);
 bool attention_planes_supported(const AttnKernelArgs &k, size_t n, size_t head_dim);
+// With split_kv false the planes already hold positions [0, pos + n): the
+// q/k/v GEMM's epilogue wrote the new keys and values (QkvPostArgs::kh ..),
+// and launch_kv_planes the earlier ones, before that GEMM.
 hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_t n, size_t head_dim, void *planes,
-                                   size_t planes_bytes, size_t max_len);
+                                   size_t planes_bytes, size_t max_len, bool split_kv = true);
+// The planes of positions [0, valid) from the caches of k (the 64-position
+// tile that holds `valid` gets zeros past it).
+hipError_t launch_kv_planes(hipStream_t s, const AttnKernelArgs &k, size_t valid, void *planes, size_t planes_bytes,
+                            size_t max_len);
+// The four planes inside `planes` for caches of max_len positions.
+struct PlanePtrs {
+    uint16_t *kh, *kl, *vh, *vl;
+    long long plane_len;
+};
+PlanePtrs attention_planes_of(void *planes, size_t max_len, size_t n_kv_heads);
 // Merges attention partials of `heads` (token, head) pairs into out (f32) or,
 // when hi is set, into hi/lo as split_bf16 terms.
 hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc, const float *part_ml, size_t heads,

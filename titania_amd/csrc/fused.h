@@ -25,9 +25,21 @@ struct QkvPostArgs {
     int n, n_heads, n_kv_heads, head_dim;
     int kv_bf16;
     float eps;
+    // When not null (f32 caches, head_dim 128): the prefill attention's bf16
+    // planes of the new keys and values, written beside the caches: K hi / lo
+    // [n_kv_heads][plane_len][128], V^T hi / lo [n_kv_heads][128][plane_len]
+    // with each 32-key slice in the order of vt_column.
+    uint16_t *kh, *kl, *vh, *vl;
+    long long plane_len;
 };
 
 hipError_t launch_qk_norm_rope_append(hipStream_t s, const QkvPostArgs &a);
+
+// The column of key k (0..31) within a 32-key slice of a V^T plane: the
+// slice's column 8 g + i holds key 4 g + i for i < 4 and 16 + 4 g + i - 4
+// otherwise (g < 4), the order in which the prefill attention's P^T operand
+// meets the keys.
+__host__ __device__ __forceinline__ int vt_column(int k) { return 8 * ((k & 15) >> 2) + ((k >> 4) << 2) + (k & 3); }
 
 // State of the on-device greedy loop, in device memory so that one captured
 // decode step can replay at every position.

@@ -331,6 +331,26 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
         __syncthreads();
         const QkvPostArgs &a = *ht.a;
         const long long pos0 = a.pos_dev ? *a.pos_dev : a.pos;
+        // A v head's V^T planes: a whole tile of 32 tokens that starts a
+        // 32-key slice writes its slice from LDS, 16 bytes a store; other
+        // tiles write each element at its column.
+        const bool vt_tile = ht.role == 2 && a.vh && ((pos0 + t0) & 31) == 0 && t0 + T::BM <= n;
+        if (vt_tile) {
+            static_assert(T::BM == 32, "a tile of one 32-key slice");
+            const long long c0 = pos0 + t0;
+            for (int e = tid; e < 128 * 4; e += T::NT) {
+                const int d = e >> 2, g = e & 3;
+                float f[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) f[i] = ep[(i < 4 ? 4 * g + i : 16 + 4 * g + i - 4) * EPS + d];
+                uint2 h0, l0, h1, l1;
+                split_bf16x4(make_float4(f[0], f[1], f[2], f[3]), h0, l0);
+                split_bf16x4(make_float4(f[4], f[5], f[6], f[7]), h1, l1);
+                const long long o = ((long long)ht.head * 128 + d) * a.plane_len + c0 + 8 * g;
+                *reinterpret_cast<uint4 *>(a.vh + o) = make_uint4(h0.x, h0.y, h1.x, h1.y);
+                *reinterpret_cast<uint4 *>(a.vl + o) = make_uint4(l0.x, l0.y, l1.x, l1.y);
+            }
+        }
         for (int tl = wave; tl < T::BM; tl += T::NT / 64) {
             const long long t = t0 + tl;
             if (t >= n) break;
@@ -340,6 +360,14 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
                 KV *vc = reinterpret_cast<KV *>(a.v_cache) + (long long)ht.head * a.head_stride + pos * a.pos_stride;
                 store_kv(vc + lane, av[0]);
                 store_kv(vc + lane + 64, bv[0]);
+                if (a.vh && !vt_tile) {
+                    // V^T planes: dimension-major rows, the key's column in its slice.
+                    const long long col = (pos & ~31LL) + vt_column((int)(pos & 31));
+                    const long long o0 = ((long long)ht.head * 128 + lane) * a.plane_len + col;
+                    const long long o1 = o0 + 64 * a.plane_len;
+                    split_bf16(av[0], a.vh[o0], a.vl[o0]);
+                    split_bf16(bv[0], a.vh[o1], a.vl[o1]);
+                }
                 continue;
             }
             norm_rope_pairs(av, bv, lane, 128, ht.role == 0 ? a.q_norm : a.k_norm, a.eps, a.rope + pos * 128);
@@ -351,6 +379,12 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
                 KV *kc = reinterpret_cast<KV *>(a.k_cache) + (long long)ht.head * a.head_stride + pos * a.pos_stride;
                 store_kv(kc + lane, av[0]);
                 store_kv(kc + lane + 64, bv[0]);
+                if (a.kh) {
+                    // K planes: row-major, the key's row at its position.
+                    const long long o = ((long long)ht.head * a.plane_len + pos) * 128 + lane;
+                    split_bf16(av[0], a.kh[o], a.kl[o]);
+                    split_bf16(bv[0], a.kh[o + 64], a.kl[o + 64]);
+                }
             }
         }
         return;

@@ -257,6 +257,10 @@ int ensure_fused_state(th_state *s) {
     if (s->kv_dtype == TH_KV_F32 && s->fb >= th::kGemmMinTokens && hd == 128) {
         s->kv_planes_bytes = th::attention_planes_bytes(s->max_len, (size_t)c.num_key_value_heads);
         TH_HIP(hipMalloc(&s->kv_planes, s->kv_planes_bytes));
+        // Zeroed: the attention reads whole 64-key tiles, and the keys of a
+        // tile past the context must be finite (they are masked); later
+        // writes are splits of finite cached values.
+        TH_HIP(hipMemsetAsync(s->kv_planes, 0, s->kv_planes_bytes, m->dev->stream));
     }
     TH_HIP(hipMalloc(&s->argmax_part, th::argmax_partials((size_t)c.vocab_size) * sizeof(uint64_t)));
     TH_HIP(hipMalloc(&s->step, sizeof(th::StepState)));
@@ -446,11 +450,49 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         qa.head_dim = (int)hd;
         qa.kv_bf16 = kv_bf16;
         qa.eps = eps;
+        th::AttnKernelArgs aa{};
+        aa.out = s->fatt;
+        aa.q = s->fq;
+        aa.k = qa.k_cache;
+        aa.v = qa.v_cache;
+        aa.n_heads = (int)nh;
+        aa.n_kv_heads = (int)nkv;
+        aa.group = (int)(nh / nkv);
+        aa.pos = (long long)pos;
+        aa.pos_dev = pos_dev;
+        aa.pos_stride = (long long)hd;
+        aa.head_stride = (long long)(s->max_len * hd);
+        aa.nsplit = nsplit;
+        aa.kv_bf16 = kv_bf16;
+        aa.scale = 1.0f / sqrtf((float)hd);
+        aa.part_acc = s->attn_part;
+        aa.part_ml = s->attn_part ? s->attn_part + n * nh * (size_t)nsplit * hd : nullptr;
+        if (hl) {
+            aa.out_hi = hi;
+            aa.out_lo = lo;
+        }
+        // The attention through bf16 planes of the keys and values (f32
+        // caches); the fused q/k/v GEMM writes the new positions' planes in
+        // its epilogue.
+        const bool use_planes = s->kv_planes && th::attention_planes_supported(aa, n, hd);
+        bool planes_written = false;
         // Residual add of the previous layer's MLP output, then the attention norm.
         if (hl) {
             TH_HIP(th::launch_add_rmsnorm_parts(st, s->fx, res, nres, res_stride, nullptr, hi, lo, n,
                                                 L.attn_norm->ptr, H, eps));
             if (th::gemm_qkv_fused(n, qd, nkv * hd, H, hd)) {
+                if (use_planes) {
+                    // Earlier positions from the caches first (its zeros past
+                    // them precede the epilogue's writes).
+                    TH_HIP(th::launch_kv_planes(st, aa, pos, s->kv_planes, s->kv_planes_bytes, s->max_len));
+                    const th::PlanePtrs pp = th::attention_planes_of(s->kv_planes, s->max_len, nkv);
+                    qa.kh = pp.kh;
+                    qa.kl = pp.kl;
+                    qa.vh = pp.vh;
+                    qa.vl = pp.vl;
+                    qa.plane_len = pp.plane_len;
+                    planes_written = true;
+                }
                 // q/k/v GEMM with the q/k norm + RoPE + KV append epilogue.
                 TH_HIP(th::launch_gemm_qkv(st, hi, lo, H, L.q->ptr, L.k->ptr, L.v->ptr, qa));
             } else {
@@ -473,29 +515,9 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
             TH_HIP(th::launch_qk_norm_rope_append(st, qa));
         }
 
-        th::AttnKernelArgs aa{};
-        aa.out = s->fatt;
-        aa.q = s->fq;
-        aa.k = qa.k_cache;
-        aa.v = qa.v_cache;
-        aa.n_heads = (int)nh;
-        aa.n_kv_heads = (int)nkv;
-        aa.group = (int)(nh / nkv);
-        aa.pos = (long long)pos;
-        aa.pos_dev = pos_dev;
-        aa.pos_stride = (long long)hd;
-        aa.head_stride = (long long)(s->max_len * hd);
-        aa.nsplit = nsplit;
-        aa.kv_bf16 = kv_bf16;
-        aa.scale = 1.0f / sqrtf((float)hd);
-        aa.part_acc = s->attn_part;
-        aa.part_ml = s->attn_part ? s->attn_part + n * nh * (size_t)nsplit * hd : nullptr;
-        if (hl) {
-            aa.out_hi = hi;
-            aa.out_lo = lo;
-        }
-        if (s->kv_planes && th::attention_planes_supported(aa, n, hd))
-            TH_HIP(th::launch_attention_planes(st, aa, n, hd, s->kv_planes, s->kv_planes_bytes, s->max_len));
+        if (use_planes)
+            TH_HIP(th::launch_attention_planes(st, aa, n, hd, s->kv_planes, s->kv_planes_bytes, s->max_len,
+                                               !planes_written));
         else
             TH_HIP(th::launch_attention(st, aa, n, hd));
 

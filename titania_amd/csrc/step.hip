@@ -392,9 +392,10 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
 // chunk of the cache that attends from those words. Blocks start in index order and the GEMV blocks never wait, so
 // the attention blocks' polls always end.
 // Rows a wave of the q/k/v GEMV blocks in qkv_attn_kernel (Qwen3-0.6B step:
-// 0.6114 ms with 2, 0.6094 with 4, 0.645 with 1; fewer GEMV blocks let the
-// attention blocks, which come after them, start sooner).
-constexpr int kQkvRowsPerWave = 4;
+// 0.6114 ms with 2, 0.6094 with 4, 0.645 with 1; with the branch-free P.V
+// loop, 0.5990 with 4 and 0.5975 with 5; fewer GEMV blocks let the attention
+// blocks, which come after them, start sooner).
+constexpr int kQkvRowsPerWave = 5;
 
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {

@@ -655,15 +655,18 @@ __device__ __forceinline__ void attend_wave4(const StepAttnArgs &a, int g, int h
     const float p = valid ? expf(s - m) : 0.f;  // m is finite when any row is valid
     const float l = wave_sum_dpp(sj == 0 ? p : 0.f);
     // P.V: dims 2 lane, 2 lane + 1; the row at pos is the new value. Rows
-    // past the context hold stale bits (NaN among them): skipped, not weighted
-    // by 0.
+    // past the context hold stale bits (NaN among them): their values are
+    // replaced by 0 (their weights are 0 already), so that the loop runs
+    // without branches; adding 0 * 0 leaves the sums as they were.
+    const float2 hv2 = reinterpret_cast<const float2 *>(hv)[lane];
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-        if (r0 + r >= len) break;  // uniform over the wave
         const float pr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), r * LPR));
         float2 v = VPair<KV>::get(vr[r]);
-        if (r0 + r == pos) v = make_float2(hv[2 * lane], hv[2 * lane + 1]);
+        const bool fr = r0 + r == pos, live = r0 + r < len;
+        v.x = fr ? hv2.x : (live ? v.x : 0.f);
+        v.y = fr ? hv2.y : (live ? v.y : 0.f);
         acc0 = fmaf(pr, v.x, acc0);
         acc1 = fmaf(pr, v.y, acc1);
     }

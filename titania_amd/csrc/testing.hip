@@ -196,7 +196,7 @@ int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_weight *
 int th_test_gemm_qkv(th_device *dev, const th_buffer *xn, const th_weight *wq, const th_weight *wk,
                      const th_weight *wv, const th_weight *q_norm, const th_weight *k_norm, float eps,
                      const th_buffer *rope, th_buffer *k_cache, th_buffer *v_cache, size_t max_len, size_t pos,
-                     size_t n, size_t n_heads, size_t n_kv_heads, th_buffer *q_out) {
+                     size_t n, size_t n_heads, size_t n_kv_heads, th_buffer *q_out, th_buffer *planes) {
     TH_REQUIRE(dev && xn && wq && wk && wv && rope && k_cache && v_cache && q_out, "th_test_gemm_qkv: null argument");
     const size_t H = (size_t)cols_of(wq), hd = 128, qd = n_heads * hd, kvd = n_kv_heads * hd;
     TH_REQUIRE(n > 0 && n_kv_heads > 0 && (size_t)rows_of(wq) == qd && (size_t)rows_of(wk) == kvd &&
@@ -227,6 +227,17 @@ int th_test_gemm_qkv(th_device *dev, const th_buffer *xn, const th_weight *wq, c
     qa.head_dim = (int)hd;
     qa.kv_bf16 = 0;
     qa.eps = eps;
+    if (planes) {
+        const size_t bytes = th::attention_planes_bytes(max_len, n_kv_heads);
+        TH_REQUIRE(planes->len * sizeof(float) >= bytes, "planes hold %zu bytes, %zu needed",
+                   planes->len * sizeof(float), bytes);
+        const th::PlanePtrs pp = th::attention_planes_of(planes->ptr, max_len, n_kv_heads);
+        qa.kh = pp.kh;
+        qa.kl = pp.kl;
+        qa.vh = pp.vh;
+        qa.vl = pp.vl;
+        qa.plane_len = pp.plane_len;
+    }
     TH_HIP(th::launch_gemm_qkv(dev->stream, hi, lo, H, wq->ptr, wk->ptr, wv->ptr, qa));
     TH_HIP(hipStreamSynchronize(dev->stream));
     return TH_OK;
