@@ -249,13 +249,15 @@ def test_qwen4b_prefill_gemm(hip, name, n):
     assert np.all(np.abs(got.astype(np.float64) - expected) <= 3e-5 * bound + 1e-6)
 
 
-@pytest.mark.parametrize("rows,cols,n", [(6144, 1024, 2000), (4096, 6144, 1024), (6144, 512, 8000)])
+@pytest.mark.parametrize("rows,cols,n", [(6144, 1024, 2000), (4096, 6144, 1024), (6144, 512, 8000),
+                                         (2560, 1024, 8000)])
 def test_large_tile_gemm(hip, rows, cols, n):
     """The 128 x 128 tile: a launch of 768 tiles with a ragged last token tile,
     and a single matrix of 256 tiles and 96 K steps, which splits K in two;
-    the 256 x 256 tile: 768 tiles, the last token tile ragged. Against a
-    float64 product: the relative error bar and an elementwise bound of a
-    few fp32 ulps of the row."""
+    the 256 x 256 tile: 768 tiles, the last token tile ragged, and a single
+    matrix of 320 tiles, which splits K in two (the Qwen3-4B o and down
+    projections at 8192 tokens). Against a float64 product: the relative
+    error bar and an elementwise bound of a few fp32 ulps of the row."""
     rng = np.random.default_rng(rows + cols + n)
     wbits = normal_bf16(rows * cols, 106, "large")
     x = rng.standard_normal(n * cols).astype(np.float32)

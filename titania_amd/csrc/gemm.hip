@@ -419,10 +419,11 @@ __global__ __launch_bounds__(Large::NT, 1) void gemm_large_kernel(Segs sg, const
 }
 
 __global__ __launch_bounds__(Huge::NT, 1) void gemm_huge_kernel(Segs sg, const uint16_t *__restrict__ hi,
-                                                            const uint16_t *__restrict__ lo, int n, int cols) {
+                                                            const uint16_t *__restrict__ lo, int n, int cols,
+                                                            float *__restrict__ part, int ksplit) {
     int tx, ty;
     tile_of_block<2>(tx, ty);
-    gemm_tile<Huge>(ty, seg_tile(sg, tx * Huge::BN), hi, lo, n, cols, nullptr, 1);
+    gemm_tile<Huge>(ty, seg_tile(sg, tx * Huge::BN), hi, lo, n, cols, part, ksplit);
 }
 
 // gate and up in one launch, block x taking rows [x BN/2, (x + 1) BN/2) of
@@ -502,8 +503,12 @@ namespace {
 // with 64 steps, 2560 x 4096, the small tile stays ahead).
 constexpr size_t kLargeMinTiles = 512;
 constexpr size_t kLargeSplitMinTiles = 256;
-// The 256 x 256 tile from three tiles a CU.
+// The 256 x 256 tile from three tiles a CU; a single matrix from one tile a
+// CU, with K split in two (the Qwen3-4B o and down projections at 8192
+// tokens, 320 tiles: 8192-token prefill 165.9 -> 160.6 ms against the
+// 128 x 128 tile, K split in three 160.8, in four 161.9).
 constexpr size_t kHugeMinTiles = 768;
+constexpr size_t kHugeSplitMinTiles = 256;
 
 struct Plan {
     bool large, huge;
@@ -515,6 +520,7 @@ Plan gemm_plan(size_t n, size_t rows, size_t cols, int n_outs, bool rows_large, 
     const size_t nk = cols / BK;
     const size_t ht = rows_huge ? (rows / Huge::BN) * ((n + Huge::BM - 1) / Huge::BM) : 0;
     if (ht >= kHugeMinTiles) return {true, true, 1};
+    if (n_outs == 1 && ht >= kHugeSplitMinTiles) return {true, true, 2};
     const size_t lt = rows_large ? (rows / Large::BN) * ((n + Large::BM - 1) / Large::BM) : 0;
     if (lt >= kLargeMinTiles) return {true, false, 1};
     if (n_outs == 1 && lt >= kLargeSplitMinTiles && nk >= 96) return {true, false, 2};
@@ -572,9 +578,9 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
         rows_huge = rows_huge && outs[i].rows % Huge::BN == 0;
     }
     const Plan plan = gemm_plan(n, total, cols, n_outs, rows_large, rows_huge);
-    if (plan.huge && ksplit == 1) {
-        dim3 grid((unsigned)(total / Huge::BN), (unsigned)((n + Huge::BM - 1) / Huge::BM));
-        gemm_huge_kernel<<<grid, Huge::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols);
+    if (plan.huge && plan.ksplit == ksplit) {
+        dim3 grid((unsigned)(total / Huge::BN), (unsigned)((n + Huge::BM - 1) / Huge::BM), (unsigned)ksplit);
+        gemm_huge_kernel<<<grid, Huge::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
     } else if (plan.large && !plan.huge && plan.ksplit == ksplit) {
         dim3 grid((unsigned)(total / Large::BN), (unsigned)((n + Large::BM - 1) / Large::BM), (unsigned)ksplit);
         gemm_large_kernel<<<grid, Large::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
