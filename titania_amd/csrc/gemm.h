@@ -64,6 +64,16 @@ struct QkvPostArgs;
 hipError_t launch_gemm_qkv(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t cols, const uint16_t *wq,
                            const uint16_t *wk, const uint16_t *wv, const QkvPostArgs &a);
 
+// Whether the q/k/v GEMM of n tokens at host position pos takes
+// launch_gemm_qkv_huge: head_dim 128, matrices of whole 256-row tiles, a
+// launch the 256 x 256 tile takes, pos a multiple of 32.
+bool gemm_qkv_huge_fused(size_t n, size_t q_rows, size_t kv_rows, size_t cols, size_t head_dim, long long pos);
+
+// launch_gemm_qkv on the 256 x 256 tile (a.pos_dev null): the same
+// post-processing, and with a.kh the planes of the new keys and values.
+hipError_t launch_gemm_qkv_huge(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t cols,
+                                const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, const QkvPostArgs &a);
+
 // Bytes of scratch launch_gemm_multi needs for n tokens of `cols` columns and
 // single-matrix outputs of up to `rows` rows (room for the split-K partials).
 size_t gemm_scratch_bytes(size_t n, size_t cols, size_t rows);

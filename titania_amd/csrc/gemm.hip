@@ -192,7 +192,7 @@ __device__ __forceinline__ SegTile seg_tile(const Segs &s, int r0) {
 // part[z][t][r]; the consumer sums the partials in z order.
 // Epilogues: store the tile (or its split-K partial), SiLU * up of paired
 // gate/up rows, or the q/k/v post-processing of one attention head.
-enum Epi { kStoreTile, kSiluPairs, kQkvHead };
+enum Epi { kStoreTile, kSiluPairs, kQkvHead, kQkvHeads };
 
 // The head of a q/k/v head tile: role 0 q, 1 k, 2 v; index within the role.
 struct HeadTile {
@@ -310,6 +310,116 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
             const size_t o = (size_t)(t0 + row) * pt.inter + pt.r0 + c;
             *reinterpret_cast<uint2 *>(pt.h_hi + o) = h;
             *reinterpret_cast<uint2 *>(pt.h_lo + o) = l;
+        }
+        return;
+    }
+    if constexpr (EPI == kQkvHeads) {
+        // Waves of 64 tokens x 128 rows: one attention head each, whose
+        // post-processing runs in registers. Lane (fq, fr) holds, for each of
+        // its 16 tokens m 16 + 4 fq + i, dimensions 16 q + fr (q < 8): the
+        // RMSNorm's sum of squares adds its 8 and then the 16 lanes of the
+        // token (an xor butterfly, which leaves the same sum in every lane),
+        // and the RoPE pairs (d, d + 64) are registers q and q + 4.
+        static_assert(T::BN / T::WGN == 128 && FN == 8, "one head of 128 dimensions a wave");
+        const QkvPostArgs &a = *ht.a;
+        const long long pos0 = a.pos_dev ? *a.pos_dev : a.pos;
+        const int head = ht.head + wn / 128;
+        if (ht.role < 2) {
+            const uint16_t *gain = ht.role == 0 ? a.q_norm : a.k_norm;
+            float gv[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) gv[q] = gain ? bf16_to_f32(gain[q * 16 + fr]) : 1.f;
+#pragma unroll
+            for (int m = 0; m < FM; ++m)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = t0 + wm + m * 16 + fq * 4 + i;
+                    const long long pos = pos0 + (t < n ? t : n - 1);
+                    float x[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) x[q] = acc[m][q][i];
+                    if (gain) {
+                        float ss = 0.f;
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) ss += x[q] * x[q];
+                        ss += __shfl_xor(ss, 1, 16);
+                        ss += __shfl_xor(ss, 2, 16);
+                        ss += __shfl_xor(ss, 4, 16);
+                        ss += __shfl_xor(ss, 8, 16);
+                        const float scale = 1.0f / sqrtf(ss / 128.f + a.eps);
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) x[q] = x[q] * (scale * gv[q]);
+                    }
+                    const float2 *ang = reinterpret_cast<const float2 *>(a.rope + pos * 128);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float2 cs = ang[q * 16 + fr];
+                        const float x0 = x[q] * cs.x - x[q + 4] * cs.y;
+                        const float x1 = x[q + 4] * cs.x + x[q] * cs.y;
+                        x[q] = x0;
+                        x[q + 4] = x1;
+                    }
+                    if (t >= n) continue;
+                    if (ht.role == 0) {
+                        float *dst = a.q + ((long long)t * a.n_heads + head) * 128;
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) dst[q * 16 + fr] = x[q];
+                    } else {
+                        KV *kc = reinterpret_cast<KV *>(a.k_cache) + (long long)head * a.head_stride +
+                                 pos * a.pos_stride;
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) store_kv(kc + q * 16 + fr, x[q]);
+                        if (a.kh) {
+                            const long long o = ((long long)head * a.plane_len + pos) * 128;
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) split_bf16(x[q], a.kh[o + q * 16 + fr], a.kl[o + q * 16 + fr]);
+                        }
+                    }
+                }
+            return;
+        }
+        // v heads: the cache rows, and the V^T planes from register pairs:
+        // tokens m 16 + 4 fq + i (m even) and (m + 1) 16 + 4 fq + i fill
+        // columns 8 fq .. 8 fq + 7 of the 32-key slice that starts at token
+        // m 16 (the slice order of vt_column), one 16-byte store each.
+#pragma unroll
+        for (int m = 0; m < FM; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = t0 + wm + m * 16 + fq * 4 + i;
+                if (t >= n) continue;
+                KV *vc = reinterpret_cast<KV *>(a.v_cache) + (long long)head * a.head_stride +
+                         (pos0 + t) * a.pos_stride;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) store_kv(vc + q * 16 + fr, acc[m][q][i]);
+            }
+        if (a.vh) {
+#pragma unroll
+            for (int m = 0; m < FM; m += 2) {
+                const int s0 = t0 + wm + m * 16;  // the slice's first token (pos0 + s0 is a multiple of 32)
+                if (s0 >= n) continue;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const long long o = ((long long)head * 128 + q * 16 + fr) * a.plane_len + pos0 + s0 + 8 * fq;
+                    if (s0 + 32 <= n) {
+                        uint2 h0, l0, h1, l1;
+                        split_bf16x4(make_float4(acc[m][q][0], acc[m][q][1], acc[m][q][2], acc[m][q][3]), h0, l0);
+                        split_bf16x4(
+                            make_float4(acc[m + 1][q][0], acc[m + 1][q][1], acc[m + 1][q][2], acc[m + 1][q][3]), h1,
+                            l1);
+                        *reinterpret_cast<uint4 *>(a.vh + o) = make_uint4(h0.x, h0.y, h1.x, h1.y);
+                        *reinterpret_cast<uint4 *>(a.vl + o) = make_uint4(l0.x, l0.y, l1.x, l1.y);
+                    } else {
+                        // The last slice, partly past the tokens: only their columns.
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int tm = j < 4 ? m : m + 1;
+                            if (t0 + wm + tm * 16 + fq * 4 + (j & 3) < n)
+                                split_bf16(acc[tm][q][j & 3], a.vh[o + j], a.vl[o + j]);
+                        }
+                    }
+                }
+            }
         }
         return;
     }
@@ -457,6 +567,26 @@ __global__ __launch_bounds__(Head::NT, 2) void gemm_qkv_kernel(const uint16_t *_
     const uint16_t *w = (role == 0 ? wq : role == 1 ? wk : wv) + (size_t)head * 128 * cols;
     SegTile sg{w, nullptr, 128, 0};
     gemm_tile<Head, kQkvHead, KV>(ty, sg, hi, lo, n, cols, nullptr, 1, PairTile{}, HeadTile{&a, role, head});
+}
+
+// q, k and v in one launch on the 256 x 256 tile, block x taking rows
+// [256 x, 256 x + 256) of the concatenation (two attention heads, one a
+// wave of 64 tokens x 128 rows), with the q/k/v post-processing epilogue.
+template <typename KV>
+__global__ __launch_bounds__(Huge::NT, 1) void gemm_qkv_huge_kernel(const uint16_t *__restrict__ wq,
+                                                                    const uint16_t *__restrict__ wk,
+                                                                    const uint16_t *__restrict__ wv,
+                                                                    const uint16_t *__restrict__ hi,
+                                                                    const uint16_t *__restrict__ lo, int n, int cols,
+                                                                    QkvPostArgs a) {
+    int tx, ty;
+    tile_of_block<2>(tx, ty);
+    const int qd = a.n_heads * 128, kvd = a.n_kv_heads * 128, r0 = tx * Huge::BN;
+    const int role = r0 < qd ? 0 : r0 < qd + kvd ? 1 : 2;
+    const int local = role == 0 ? r0 : role == 1 ? r0 - qd : r0 - qd - kvd;
+    const uint16_t *w = (role == 0 ? wq : role == 1 ? wk : wv) + (size_t)local * cols;
+    SegTile sg{w, nullptr, Huge::BN, 0};
+    gemm_tile<Huge, kQkvHeads, KV>(ty, sg, hi, lo, n, cols, nullptr, 1, PairTile{}, HeadTile{&a, role, local / 128});
 }
 
 // split_bf16 of 4 elements a thread.
@@ -612,6 +742,26 @@ hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *l
         gemm_silu_kernel<Small><<<grid, Small::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
                                                            h_lo);
     }
+    return hipGetLastError();
+}
+
+bool gemm_qkv_huge_fused(size_t n, size_t q_rows, size_t kv_rows, size_t cols, size_t head_dim, long long pos) {
+    const size_t rows = q_rows + 2 * kv_rows;
+    return head_dim == 128 && q_rows % Huge::BN == 0 && kv_rows % Huge::BN == 0 && gemm_supported(rows, cols) &&
+           pos % 32 == 0 && gemm_plan(n, rows, cols, 3, rows % Large::BN == 0, true).huge;
+}
+
+hipError_t launch_gemm_qkv_huge(hipStream_t s, const uint16_t *hi, const uint16_t *lo, size_t cols,
+                                const uint16_t *wq, const uint16_t *wk, const uint16_t *wv, const QkvPostArgs &a) {
+    const size_t n = (size_t)a.n, qd = (size_t)a.n_heads * 128, kvd = (size_t)a.n_kv_heads * 128;
+    if (a.n <= 0 || a.pos_dev || !hi || !lo || a.head_dim != 128 || !gemm_qkv_huge_fused(n, qd, kvd, cols, 128, a.pos) ||
+        (a.kh && (!a.kl || !a.vh || !a.vl || a.plane_len % 64 || a.pos + a.n > a.plane_len)))
+        return hipErrorInvalidValue;
+    dim3 grid((unsigned)((qd + 2 * kvd) / Huge::BN), (unsigned)((n + Huge::BM - 1) / Huge::BM));
+    if (a.kv_bf16)
+        gemm_qkv_huge_kernel<uint16_t><<<grid, Huge::NT, 0, s>>>(wq, wk, wv, hi, lo, (int)n, (int)cols, a);
+    else
+        gemm_qkv_huge_kernel<float><<<grid, Huge::NT, 0, s>>>(wq, wk, wv, hi, lo, (int)n, (int)cols, a);
     return hipGetLastError();
 }
 

@@ -480,21 +480,28 @@ int enqueue_fused(th_state *s, const uint32_t *tokens, size_t n, size_t pos, con
         if (hl) {
             TH_HIP(th::launch_add_rmsnorm_parts(st, s->fx, res, nres, res_stride, nullptr, hi, lo, n,
                                                 L.attn_norm->ptr, H, eps));
+            // The q/k/v GEMMs with the q/k norm + RoPE + KV append epilogue,
+            // which also writes the new positions' planes.
+            auto epilogue_planes = [&]() -> int {
+                if (!use_planes) return TH_OK;
+                // Earlier positions from the caches first (its zeros past
+                // them precede the epilogue's writes).
+                TH_HIP(th::launch_kv_planes(st, aa, pos, s->kv_planes, s->kv_planes_bytes, s->max_len));
+                const th::PlanePtrs pp = th::attention_planes_of(s->kv_planes, s->max_len, nkv);
+                qa.kh = pp.kh;
+                qa.kl = pp.kl;
+                qa.vh = pp.vh;
+                qa.vl = pp.vl;
+                qa.plane_len = pp.plane_len;
+                planes_written = true;
+                return TH_OK;
+            };
             if (th::gemm_qkv_fused(n, qd, nkv * hd, H, hd)) {
-                if (use_planes) {
-                    // Earlier positions from the caches first (its zeros past
-                    // them precede the epilogue's writes).
-                    TH_HIP(th::launch_kv_planes(st, aa, pos, s->kv_planes, s->kv_planes_bytes, s->max_len));
-                    const th::PlanePtrs pp = th::attention_planes_of(s->kv_planes, s->max_len, nkv);
-                    qa.kh = pp.kh;
-                    qa.kl = pp.kl;
-                    qa.vh = pp.vh;
-                    qa.vl = pp.vl;
-                    qa.plane_len = pp.plane_len;
-                    planes_written = true;
-                }
-                // q/k/v GEMM with the q/k norm + RoPE + KV append epilogue.
+                TRY(epilogue_planes());
                 TH_HIP(th::launch_gemm_qkv(st, hi, lo, H, L.q->ptr, L.k->ptr, L.v->ptr, qa));
+            } else if (!pos_dev && th::gemm_qkv_huge_fused(n, qd, nkv * hd, H, hd, (long long)pos)) {
+                TRY(epilogue_planes());
+                TH_HIP(th::launch_gemm_qkv_huge(st, hi, lo, H, L.q->ptr, L.k->ptr, L.v->ptr, qa));
             } else {
                 const th::GemmOut o[3] = {
                     {L.q->ptr, qd, s->fq}, {L.k->ptr, nkv * hd, s->fk}, {L.v->ptr, nkv * hd, s->fv}};

@@ -206,7 +206,9 @@ int th_test_gemm_qkv(th_device *dev, const th_buffer *xn, const th_weight *wq, c
     TH_REQUIRE(pos + n <= max_len && rope->len >= max_len * hd, "positions past max_len or the rope table");
     TH_REQUIRE(k_cache->len >= n_kv_heads * max_len * hd && v_cache->len >= n_kv_heads * max_len * hd,
                "caches hold [n_kv_heads][max_len][128]");
-    TH_REQUIRE(th::gemm_qkv_fused(n, qd, kvd, H, hd), "the fused q/k/v GEMM does not take this shape");
+    const bool head_tile = th::gemm_qkv_fused(n, qd, kvd, H, hd);
+    TH_REQUIRE(head_tile || th::gemm_qkv_huge_fused(n, qd, kvd, H, hd, (long long)pos),
+               "the fused q/k/v GEMM does not take this shape");
     DevMem split;
     TRY(split.alloc(2 * n * H * sizeof(uint16_t), dev->stream));
     uint16_t *hi = static_cast<uint16_t *>(split.p), *lo = hi + n * H;
@@ -238,7 +240,10 @@ int th_test_gemm_qkv(th_device *dev, const th_buffer *xn, const th_weight *wq, c
         qa.vl = pp.vl;
         qa.plane_len = pp.plane_len;
     }
-    TH_HIP(th::launch_gemm_qkv(dev->stream, hi, lo, H, wq->ptr, wk->ptr, wv->ptr, qa));
+    if (head_tile)
+        TH_HIP(th::launch_gemm_qkv(dev->stream, hi, lo, H, wq->ptr, wk->ptr, wv->ptr, qa));
+    else
+        TH_HIP(th::launch_gemm_qkv_huge(dev->stream, hi, lo, H, wq->ptr, wk->ptr, wv->ptr, qa));
     TH_HIP(hipStreamSynchronize(dev->stream));
     return TH_OK;
 }
