@@ -353,39 +353,76 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__
                                                                       const float *__restrict__ part_ml, int nsplit,
                                                                       int hd, uint16_t *__restrict__ hi,
                                                                       uint16_t *__restrict__ lo) {
+    constexpr int kPre = 16;  // accumulator rows a thread requests up front
     __shared__ float w[kMaxSplits];
     __shared__ float red[kCombineThreads / 64];
     __shared__ float acc_red[kCombineThreads];
     const long long th = blockIdx.x;  // token * n_heads + head
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *ml = part_ml + th * nsplit * 2;
+    // This block's dimensions [dlo, dlo + dw) (gridDim.y blocks share a
+    // head), in groups of splits: thread t takes dimension dlo + t % dw of
+    // the splits s = t / dw, + groups, ...
+    const int dw = hd / (int)gridDim.y, dlo = (int)blockIdx.y * dw;
+    const int groups = dw < kCombineThreads ? kCombineThreads / dw : 1;
+    // With one pass over the dimensions and at most kPre splits a thread
+    // (every launch of the decode step), the accumulator rows are requested
+    // with the statistics, so the merge waits for one memory round trip
+    // instead of three; the sums run in the same order either way (Qwen3-0.6B
+    // decode after a 4096-token prompt: 0.925 -> 0.903 ms a step).
+    const bool pre = dw <= kCombineThreads && nsplit <= kCombineThreads && nsplit <= kPre * groups;
+    float2 st = make_float2(-INFINITY, 0.f);
+    float pacc[kPre];
+    if (pre) {
+        if (tid < nsplit) st = reinterpret_cast<const float2 *>(ml)[tid];
+        const int dd = tid % dw, grp = tid / dw;
+        const float *pa = part_acc + th * nsplit * hd + dlo + dd;
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            const int s = grp + k * groups;
+            pacc[k] = grp < groups && s < nsplit ? pa[(size_t)s * hd] : 0.f;
+        }
+    }
     float m = -INFINITY;
-    for (int s = tid; s < nsplit; s += kCombineThreads) m = fmaxf(m, ml[2 * s]);
+    if (pre) m = st.x;
+    else
+        for (int s = tid; s < nsplit; s += kCombineThreads) m = fmaxf(m, ml[2 * s]);
     m = wave_max_dpp(m);
     if (lane == 0) red[wave] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float l = 0.f;
-    for (int s = tid; s < nsplit; s += kCombineThreads) {
-        const float ms = ml[2 * s];
-        const float ws = ms != -INFINITY ? expf(ms - m) : 0.f;
-        w[s] = ws;
-        l += ml[2 * s + 1] * ws;
+    if (pre) {
+        if (tid < nsplit) {
+            const float ws = st.x != -INFINITY ? expf(st.x - m) : 0.f;
+            w[tid] = ws;
+            l = st.y * ws;
+        }
+    } else {
+        for (int s = tid; s < nsplit; s += kCombineThreads) {
+            const float ms = ml[2 * s];
+            const float ws = ms != -INFINITY ? expf(ms - m) : 0.f;
+            w[s] = ws;
+            l += ml[2 * s + 1] * ws;
+        }
     }
     l = wave_sum_dpp(l);
     if (lane == 0) red[wave] = l;
     __syncthreads();
     l = ((red[0] + red[1]) + red[2]) + red[3];
-    // This block's dimensions [dlo, dlo + dw) (gridDim.y blocks share a
-    // head), in groups of splits: thread t takes dimension dlo + t % dw of
-    // the splits s = t / dw, + groups, ...
-    const int dw = hd / (int)gridDim.y, dlo = (int)blockIdx.y * dw;
-    const int groups = dw < kCombineThreads ? kCombineThreads / dw : 1;
     for (int d0 = 0; d0 < dw; d0 += kCombineThreads) {
         const int dd = d0 + tid % dw, grp = tid / dw, d = dlo + dd;
         float acc = 0.f;
-        if (dd < dw && grp < groups) {
+        if (pre) {
+            if (grp < groups) {
+#pragma unroll
+                for (int k = 0; k < kPre; ++k) {
+                    const int s = grp + k * groups;
+                    if (s < nsplit) acc += pacc[k] * w[s];
+                }
+            }
+        } else if (dd < dw && grp < groups) {
             const float *pa = part_acc + th * nsplit * hd + d;
 #pragma unroll 8
             for (int s = grp; s < nsplit; s += groups) acc += pa[(size_t)s * hd] * w[s];
