@@ -21,6 +21,16 @@ __device__ __forceinline__ void unpack8(const uint4 &w, float f[8]) {
     f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
 }
 
+// A 16-byte load with the non-temporal (streaming) cache policy: for weight
+// rows that a decode step reads once. On the Qwen3-0.6B decode step this took
+// 0.605 to 0.574 ms against plain loads (the same policy on the cached key
+// and value rows made the step slower).
+typedef unsigned int th_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
+    const th_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const th_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Round-to-nearest-even f32 -> bf16 bits (finite inputs; NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);

@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(float *__restrict__ out, cons
     for (size_t c = lane; c < chunks; c += 64) {
         uint4 wv[ROWS];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) wv[r] = wr[r][c];
+        for (int r = 0; r < ROWS; ++r) wv[r] = ld_nt(wr[r] + c);
         float xf[NT][8];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {

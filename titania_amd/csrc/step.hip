@@ -12,9 +12,9 @@
 // recompute the sum it needs.
 //
 // The GEMVs are HBM-bound: each block issues the 16-byte loads of all its
-// weight rows first (they do not depend on the activations), then builds the
-// normalized input in LDS while those loads are in flight, then reduces one
-// row per wave with DPP.
+// weight rows first (they do not depend on the activations; non-temporal, as
+// a step reads each weight once), then builds the normalized input in LDS
+// while those loads are in flight, then reduces one row per wave with DPP.
 #include <algorithm>
 
 #include "common.h"
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         const bool valid = EPI == kSiluPairs ? (r0 + r - (r & 1)) / 2 < half : row < a.n_rows;
         const uint4 *p = row_at(a.rows, valid ? row : 0, a.cols);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) w[r][c] = p[c * 64 + lane];
+        for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt(p + c * 64 + lane);
     }
     build_input<PRO == kNormSum, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out,
                                                                         red);
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
     for (int r = 0; r < RPW; ++r) {
         const uint4 *p = row_at(a.rows, r0 + r < a.n_rows ? r0 + r : 0, a.cols);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) w[r][c] = p[c * 64 + lane];
+        for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt(p + c * 64 + lane);
     }
     build_input<true, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out, red);
     float res[RPW];
