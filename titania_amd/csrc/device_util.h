@@ -21,13 +21,25 @@ __device__ __forceinline__ void unpack8(const uint4 &w, float f[8]) {
     f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
 }
 
-// A 16-byte load with the non-temporal (streaming) cache policy: for weight
+// 16-byte loads with the non-temporal (streaming) cache policy, for weight
 // rows that a decode step reads once. On the Qwen3-0.6B decode step this took
-// 0.605 to 0.574 ms against plain loads (the same policy on the cached key
-// and value rows made the step slower).
+// 0.605 to 0.570 ms against plain loads (the same policy on the cached key
+// and value rows made the step slower; the scope bits sc0 / sc1 changed
+// nothing beside it).
 typedef unsigned int th_u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
     const th_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const th_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+// The same through a buffer descriptor of a wave-uniform row base (the
+// address lives in scalar registers: 0.570 -> 0.567 ms on that step).
+// Element idx of the row, idx * 16 < 2^31.
+constexpr int kCachePolicyNt = 2;               // the instruction's nt bit
+constexpr unsigned kBufferRsrcWord3 = 0x00020000;  // raw 32-bit data, no swizzle
+__device__ __forceinline__ uint4 ld_nt_row(const uint4 *row, int idx) {
+    __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(row), 0, 0x7fffffff,
+                                                                 kBufferRsrcWord3);
+    const th_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, idx * 16, 0, kCachePolicyNt);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 

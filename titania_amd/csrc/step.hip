@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     __shared__ uint64_t red64[kWaves];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     constexpr int RPB = RPW * kWaves;
     const int r0 = blockIdx.x * RPB + wave * RPW;
     // For paired rows (gate j, up j), a wave takes j and j + half.
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         const bool valid = EPI == kSiluPairs ? (r0 + r - (r & 1)) / 2 < half : row < a.n_rows;
         const uint4 *p = row_at(a.rows, valid ? row : 0, a.cols);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt(p + c * 64 + lane);
+        for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt_row(p, c * 64 + lane);
     }
     build_input<PRO == kNormSum, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out,
                                                                         red);
@@ -413,14 +413,14 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
     }
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r0 = blockIdx.x * RPB + wave * RPW;
     uint4 w[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const uint4 *p = row_at(a.rows, r0 + r < a.n_rows ? r0 + r : 0, a.cols);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt(p + c * 64 + lane);
+        for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt_row(p, c * 64 + lane);
     }
     build_input<true, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out, red);
     float res[RPW];
