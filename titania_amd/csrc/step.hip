@@ -393,9 +393,9 @@ __global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a
 // the attention blocks' polls always end.
 // Rows a wave of the q/k/v GEMV blocks in qkv_attn_kernel (Qwen3-0.6B step:
 // 0.6114 ms with 2, 0.6094 with 4, 0.645 with 1; with the branch-free P.V
-// loop, 0.5990 with 4 and 0.5975 with 5; fewer GEMV blocks let the attention
-// blocks, which come after them, start sooner).
-constexpr int kQkvRowsPerWave = 5;
+// loop, 0.5990 with 4 and 0.5975 with 5; with non-temporal weight loads,
+// 0.5673 / 0.5651 / 0.5640 / 0.5693 ms with 2 / 3 / 4 / 5).
+constexpr int kQkvRowsPerWave = 4;
 
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
