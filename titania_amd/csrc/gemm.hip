@@ -49,6 +49,8 @@ struct Tile {
     static constexpr int TA = BM * CH, TB = BN * CH;     // 16-byte chunks per tile
     static constexpr int FM = BM / WGM / 16, FN = BN / WGN / 16;  // 16 x 16 fragments per wave
     static constexpr int DMA_PER_WAVE = (2 * TA + TB) / NT;
+    // issue_step deals whole 64-lane spans of each tile to the waves.
+    static_assert(TA % NT == 0 && TB % NT == 0, "every wave loads the same whole spans of each tile");
     struct alignas(16) Stage {
         uint4 hi[TA], lo[TA];  // [BM][CH] activation halves
         uint4 w[TB];           // [BN][CH] weights
