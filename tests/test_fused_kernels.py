@@ -10,7 +10,7 @@ q/k/v + attention launch (q/k norm, RoPE, KV append, chunked attention); the
 prefill's q/k/v GEMM (norm + RoPE + KV append epilogue), gate/up GEMM (SiLU
 epilogue) and residual-partials + RMSNorm kernel.
 
-Bar: the north star's per-kernel relative error <= 1e-3 (normwise), and an
+Bar: a per-kernel relative error <= 1e-3 (normwise), and an
 elementwise bound of a few fp32 rounding steps of each output's magnitude.
 """
 
