@@ -57,6 +57,12 @@ struct Tile {
     };
 };
 using Small = Tile<64, 64, 64, 3>;    // 24 KB a stage: two blocks a CU
+// The small tile with two stages (48 KB): three blocks a CU. For the gate/up
+// GEMM of launches with more small tiles than two a CU, where the rounds of
+// blocks matter more than the deeper ring (Qwen3-0.6B prefill, paired runs:
+// 512 tokens, 768 tiles, 2.89-2.94 -> 2.86-2.92 ms; 1024 tokens 4.88-4.90 ->
+// 4.81-4.82 ms).
+using Small2 = Tile<64, 64, 64, 2>;
 using Large = Tile<128, 128, 64, 3, 4, 2>;  // 48 KB a stage: one block a CU, eight waves of 32 x 64
 using Head = Tile<32, 128, 64, 3>;          // one attention head's 128 rows: 24 KB a stage, two blocks a CU
 // 48 KB a stage of 32 K columns: one block a CU, eight waves of 64 x 128. A
@@ -545,7 +551,7 @@ __global__ __launch_bounds__(Huge::NT, 1) void gemm_huge_kernel(Segs sg, const u
 // gate and up in one launch, block x taking rows [x BN/2, (x + 1) BN/2) of
 // each, with the SiLU * up epilogue.
 template <class T>
-__global__ __launch_bounds__(T::NT, T::NT == 256 ? 2 : 1) void gemm_silu_kernel(
+__global__ __launch_bounds__(T::NT, T::NT == 256 ? (T::kStages == 2 ? 3 : 2) : 1) void gemm_silu_kernel(
     const uint16_t *__restrict__ gate, const uint16_t *__restrict__ up, const uint16_t *__restrict__ hi,
     const uint16_t *__restrict__ lo, int n, int cols, int inter, uint16_t *__restrict__ h_hi,
     uint16_t *__restrict__ h_lo) {
@@ -644,6 +650,8 @@ constexpr size_t kLargeSplitMinTiles = 256;
 // tokens, 320 tiles: 8192-token prefill 165.9 -> 160.6 ms against the
 // 128 x 128 tile, K split in three 160.8, in four 161.9).
 constexpr size_t kHugeMinTiles = 768;
+// More small tiles than two a CU: the gate/up GEMM takes Small2.
+constexpr size_t kSmall2MinTiles = 512;
 constexpr size_t kHugeSplitMinTiles = 256;
 
 struct Plan {
@@ -745,8 +753,12 @@ hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *l
                                                            h_lo);
     } else {
         dim3 grid((unsigned)(inter / (Small::BN / 2)), (unsigned)((n + Small::BM - 1) / Small::BM));
-        gemm_silu_kernel<Small><<<grid, Small::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
-                                                           h_lo);
+        if ((size_t)grid.x * grid.y > kSmall2MinTiles)
+            gemm_silu_kernel<Small2><<<grid, Small2::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter,
+                                                                 h_hi, h_lo);
+        else
+            gemm_silu_kernel<Small><<<grid, Small::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter,
+                                                               h_hi, h_lo);
     }
     return hipGetLastError();
 }
