@@ -609,7 +609,8 @@ int claim_path(th_state *s, int path) {
 
 // Decode steps per replay of the multi-step graph: a replay boundary costs
 // the GPU ≈6 µs against ≈1.5 µs between kernels inside a graph (0.6B decode:
-// 0.619 -> 0.6145 ms a step with 4 steps a replay).
+// 0.619 -> 0.6145 ms a step with 4 steps a replay). Longer replays measured
+// slower: 0.562-0.563 ms a step with 8, 0.566-0.567 with 16, 0.571 with 32.
 constexpr size_t kGraphSteps = 8;
 
 // Captures `n_steps` decode steps (n = 1 each, position and token from
