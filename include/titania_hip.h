@@ -89,13 +89,14 @@ TH_API int th_rope(th_device *dev, th_buffer *x, const th_buffer *table, size_t 
 TH_API int th_attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
                  const th_buffer *v_cache, size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads);
 /* th_attention without any allocation: its split partials go to a fixed
- * 8 MiB array that the library holds on each GPU until the process ends, so
+ * 16 MiB array that the library holds on each GPU until the process ends, so
  * that callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc) can call it. No counterpart
  * in model/device.rs. Same arguments, checks and results as th_attention; a
- * call whose partials need more than 8 MiB (n * n_heads * splits *
- * (head_dim + 2) floats: e.g. one token of 64 heads at any context fits, a
- * 2048-token prompt does not) returns TH_ERR_INVALID. Every call on a GPU
+ * call whose partials need more than 16 MiB (n * n_heads * splits *
+ * (head_dim + 2) floats, at most 256 splits for one token: one token of up to
+ * 126 heads of head_dim 128 at any context fits, a 2048-token prompt of 32
+ * heads at 8192 positions does not) returns TH_ERR_INVALID. Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (two device handles of one GPU, two
  * threads) race. */
 TH_API int th_attention_noalloc(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache,
@@ -199,7 +200,13 @@ TH_API int th_model_config(const th_model *model, th_config *out);
 #define TH_KV_BF16 1 /* bf16 caches: half the bytes per position */
 
 /* model/model.rs:176-211 `State::new` for sequences of up to max_len tokens.
- * The caches are laid out per layer and per KV head: [layer][kv_head][max_len][head_dim]. */
+ * The caches are laid out per layer and per KV head: [layer][kv_head][max_len][head_dim].
+ * Besides the caches, the first forward or decode allocates buffers for
+ * prefill chunks of up to min(8192, max_len) tokens, kept for the state's
+ * life: 4 * (3 hidden + 2 q + 2 kv + 2 intermediate) bytes a token of
+ * activations plus the GEMM's split scratch, about 1.9 GB at the Qwen3-4B
+ * shape once max_len >= 8192 (0.25 GB at max_len 1024). Size max_len to the
+ * longest sequence the state will hold. */
 TH_API int th_state_create(th_model *model, size_t max_len, int kv_dtype, th_state **out);
 TH_API void th_state_destroy(th_state *state);
 

@@ -50,6 +50,22 @@ TH_API int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_w
                                  th_buffer *k_cache, th_buffer *v_cache, size_t max_len, size_t pos,
                                  size_t n_heads, size_t n_kv_heads, th_buffer *x_out, th_buffer *att_out);
 
+/* The decode step's split attention and its combine, the launches a step
+ * takes once its context outgrows the fused q/k/v + attention launch, for
+ * one token at `pos` (model.rs:111-124): qkv holds the raw q, k and v rows
+ * ([n_heads * 128][n_kv_heads * 128][n_kv_heads * 128]); q and k are
+ * RMSNorm'd per head (q_norm / k_norm may be NULL) and rotated, k and v
+ * appended to the caches at pos, and att = attention over positions
+ * 0..pos, in the splits the step uses for caches of max_len positions,
+ * merged by the combine kernel when there are several (*n_splits, if not
+ * NULL, receives their count). kv_bf16 = 1: the caches hold bf16 values, two
+ * to a float of the buffer. The caches extend 128 rows of 128 floats past
+ * the last head. */
+TH_API int th_test_step_attention(th_device *dev, const th_buffer *qkv, const th_weight *q_norm,
+                                  const th_weight *k_norm, float eps, const th_buffer *rope, th_buffer *k_cache,
+                                  th_buffer *v_cache, size_t max_len, size_t pos, size_t n_heads, size_t n_kv_heads,
+                                  int kv_bf16, th_buffer *att_out, int *n_splits);
+
 /* Prefill q/k/v GEMM on the matrix cores with the q/k norm + RoPE + KV
  * append epilogue, for n tokens at pos .. pos + n - 1: q_out = the rotated,
  * normalized q rows; k and v go to the caches (model.rs:108-120). xn holds

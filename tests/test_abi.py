@@ -55,7 +55,7 @@ def test_test_entry_points_exported_and_bound():
     import test_fused_kernels as fk
 
     header = cabi.header_signatures(cabi.TEST_HEADER)
-    assert len(header) == 9 and sorted(header) == sorted(fk.TEST_SIGNATURES)
+    assert len(header) == 10 and sorted(header) == sorted(fk.TEST_SIGNATURES)
     lib = C.CDLL(str(_lib.LIB_PATH))
     assert all(hasattr(lib, n) for n in header)
     bound = cabi.ctypes_signatures({n: (C.c_int, a) for n, a in fk.TEST_SIGNATURES.items()})

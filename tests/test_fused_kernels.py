@@ -6,7 +6,8 @@ entry points of include/titania_hip_test.h.
 Kernels: the decode step's q/k/v GEMV (residual add + RMSNorm prologue), its
 gate/up GEMV (SiLU epilogue), its plain GEMV (o, down; 19 chunks a lane at
 the 4B down shape), its output projection (argmax epilogue + pick), its fused
-q/k/v + attention launch (q/k norm, RoPE, KV append, chunked attention); the
+q/k/v + attention launch (q/k norm, RoPE, KV append, chunked attention), its
+split attention with the combine (the launches of long contexts); the
 prefill's q/k/v GEMM (norm + RoPE + KV append epilogue), gate/up GEMM (SiLU
 epilogue) and residual-partials + RMSNorm kernel.
 
@@ -36,6 +37,8 @@ TEST_SIGNATURES = {
     "th_test_step_gemv": [_P, _P, _P, _P],
     "th_test_step_logits": [_P, _P, _P, _P, _P, _F, _P, C.POINTER(C.c_uint32)],
     "th_test_step_qkv_attn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _P, _P],
+    "th_test_step_attention": [_P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, C.c_int, _P,
+                               C.POINTER(C.c_int)],
     "th_test_gemm_qkv": [_P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, _SZ, _P, _P],
     "th_test_gemm_silu": [_P, _P, _P, _P, _SZ, _P],
     "th_test_add_rmsnorm_parts": [_P, _P, _P, _SZ, _P, _F, _P],
@@ -233,6 +236,87 @@ def test_step_qkv_attn(hip, tlib, shape, pos):
     assert_close(dk[:, pos], kc[:, pos], rel=1e-4, abs_=1e-5, what="appended key")
     assert_close(dv[:, pos], vc[:, pos], rel=1e-4, abs_=1e-5, what="appended value")
     assert np.array_equal(dk[:, :pos], kc[:, :pos]), "earlier keys untouched"
+
+
+# (q heads, KV heads, context, max_len, bf16 cache): group sizes 1, 2, 4 and 8
+# (the LDS-staged kernel for 1 and 8, the register kernel for 2 and 4) at
+# contexts of one split (512 positions) to the 256-split cap (32768 f32
+# positions take 256 splits of 128), ragged last splits and empty ones.
+SPLIT_CASES = [
+    (8, 8, 2049, 2049, 0), (8, 8, 4096, 4200, 0), (8, 8, 2049, 2100, 1),
+    (16, 8, 500, 512, 0), (16, 8, 2049, 2049, 0), (16, 8, 4096, 4096, 0), (16, 8, 32768, 32768, 0),
+    (16, 8, 4096, 4160, 1), (16, 8, 32768, 32768, 1),
+    (32, 8, 1025, 1025, 0), (32, 8, 2049, 2080, 0), (32, 8, 8193, 8193, 0), (32, 8, 8448, 8448, 0),
+    (32, 8, 3000, 8448, 0), (32, 8, 8448, 8448, 1), (32, 8, 1025, 1100, 1),
+    (64, 8, 1025, 1025, 0), (64, 8, 8193, 8200, 0), (64, 8, 2049, 2049, 1),
+]
+
+
+@pytest.mark.parametrize("nh,nkv,ctx,max_len,kv_bf16", SPLIT_CASES)
+def test_step_attention_split(hip, tlib, nh, nkv, ctx, max_len, kv_bf16):
+    """The decode step's split attention + combine against per-head norms,
+    RoPE, the cache append and the oracle's attention over positions 0..pos
+    (pos = ctx - 1). With a bf16 cache the oracle attends over the bf16
+    values of the earlier rows and the f32 new key and value (the kernel
+    attends to the new row from registers and stores it rounded)."""
+    hd, qd, kvd = 128, nh * 128, nkv * 128
+    pos = ctx - 1
+    qn, QN = gains(hip, hd, 9, "qn")
+    kn, KN = gains(hip, hd, 9, "kn")
+    rng = np.random.default_rng(ctx + 7 * nh + kv_bf16)
+    qkv = rng.standard_normal(qd + 2 * kvd).astype(np.float32)
+    table = ref.rope_table(max_len, hd, 1e6)
+    kc = np.zeros((nkv, max_len, hd), np.float32)
+    vc = np.zeros((nkv, max_len, hd), np.float32)
+    kc[:, :pos] = rng.standard_normal((nkv, pos, hd))
+    vc[:, :pos] = rng.standard_normal((nkv, pos, hd))
+    tail = np.zeros(128 * hd, np.float32)
+    if kv_bf16:
+        # Two bf16 values a float; rows past pos hold NaN, which a read of
+        # them would carry to the output.
+        kb, vb = f32_to_bf16(kc), f32_to_bf16(vc)
+        kb[:, pos:], vb[:, pos:] = 0x7FC0, 0x7FC0
+        kc[:, :pos], vc[:, :pos] = bf16_to_f32(kb[:, :pos]), bf16_to_f32(vb[:, :pos])
+        dev_k = np.concatenate([kb.reshape(-1).view(np.float32), tail])
+        dev_v = np.concatenate([vb.reshape(-1).view(np.float32), tail])
+    else:
+        kn_ = np.full_like(kc, np.nan)
+        vn_ = np.full_like(vc, np.nan)
+        kn_[:, :pos], vn_[:, :pos] = kc[:, :pos], vc[:, :pos]
+        dev_k, dev_v = np.concatenate([kn_.reshape(-1), tail]), np.concatenate([vn_.reshape(-1), tail])
+    Kc, Vc = buf(hip, dev_k), buf(hip, dev_v)
+    QKV, T, att = buf(hip, qkv), buf(hip, table), hip.alloc(qd)
+    ns = C.c_int()
+    check(tlib.th_test_step_attention(hip.handle, QKV.handle, QN.handle, KN.handle, EPS, T.handle, Kc.handle,
+                                      Vc.handle, max_len, pos, nh, nkv, kv_bf16, att.handle, C.byref(ns)))
+    assert (ns.value > 1) == (max_len > 512), f"{ns.value} splits for {max_len} positions"
+    q = _head_norm_rope(qkv[:qd], qn, table, pos, nh)
+    k = _head_norm_rope(qkv[qd:qd + kvd], kn, table, pos, nkv)
+    v = qkv[qd + kvd:]
+    kc[:, pos], vc[:, pos] = k.reshape(nkv, hd), v.reshape(nkv, hd)
+    # The oracle's caches are position-major: [position][kv head][128].
+    exp = ref.attention(q, kc[:, :ctx].transpose(1, 0, 2).copy(), vc[:, :ctx].transpose(1, 0, 2).copy(),
+                        pos, nh, hd, nkv)
+    got = hip.read(att)
+    assert np.all(np.isfinite(got)), "a row past the context reached the output"
+    assert rel_error(got, exp) <= 1e-3
+    assert_close(got, exp, rel=1e-4, abs_=1e-5, what=f"split attention {nh}/{nkv} ctx {ctx} max_len {max_len}")
+    dk, dv = hip.read(Kc), hip.read(Vc)
+    if kv_bf16:
+        dk = dk[: nkv * max_len * hd // 2].view(np.uint16).reshape(nkv, max_len, hd)
+        dv = dv[: nkv * max_len * hd // 2].view(np.uint16).reshape(nkv, max_len, hd)
+        assert np.array_equal(dk[:, :pos], kb[:, :pos]), "earlier keys untouched"
+        # The appended row is the kernel's f32 key rounded to bf16: within
+        # one bf16 rounding of the oracle's.
+        assert_close(bf16_to_f32(dk[:, pos]), kc[:, pos], rel=2 ** -8, abs_=1e-5, what="appended key")
+        assert_close(bf16_to_f32(dv[:, pos]), vc[:, pos], rel=2 ** -8, abs_=1e-5, what="appended value")
+    else:
+        dk = dk[: nkv * max_len * hd].reshape(nkv, max_len, hd)
+        dv = dv[: nkv * max_len * hd].reshape(nkv, max_len, hd)
+        assert np.array_equal(dk[:, :pos], kc[:, :pos]), "earlier keys untouched"
+        assert_close(dk[:, pos], kc[:, pos], rel=1e-4, abs_=1e-5, what="appended key")
+        assert_close(dv[:, pos], vc[:, pos], rel=1e-4, abs_=1e-5, what="appended value")
+        assert np.all(np.isnan(dk[:, pos + 1:])), "rows past pos untouched"
 
 
 @pytest.mark.parametrize("shape,n,pos", [("0.6b", 100, 0), ("0.6b", 512, 37), ("0.6b", 512, 64), ("4b", 100, 20),

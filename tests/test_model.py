@@ -214,11 +214,13 @@ def tiny8(hip):
 
 @pytest.mark.parametrize("decode_mode", ["graph"], indirect=True)
 @pytest.mark.parametrize("prompt_len,steps,kv", [(9, 24, TH_KV_F32), (300, 16, TH_KV_F32), (300, 12, TH_KV_BF16),
-                                                 (700, 8, TH_KV_F32)])
+                                                 (700, 8, TH_KV_F32), (2100, 6, TH_KV_F32), (4200, 4, TH_KV_BF16)])
 def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
     """Decode with eight KV heads against the oracle: one attention chunk per
-    head, several chunks merged, and (700 positions) the split attention kernel
-    with its combine."""
+    head (9 positions), several chunks merged by each head's first (300 and
+    700 positions: 5 and 12 chunks of 64 f32 or 3 of 128 bf16 positions), and
+    past the fused launch's 32 chunks a head the split attention kernel with
+    its combine (2100 f32 positions: 33 splits of 64; 4200 bf16: 33 of 128)."""
     m, r = tiny8
     c = QWEN3_TINY8
     prompt = synth.prompt(prompt_len, c.vocab_size, seed=prompt_len + 1)

@@ -346,6 +346,66 @@ def test_generate_is_the_forward_loop():
 
 
 
+@pytest.mark.parametrize("t,k,p,seed", [(0.7, 20, 0.8, 42), (1.0, 300, 1.0, 7), (0.0, 20, 0.8, 3), (1.3, 5, 0.5, 0)])
+def test_generate_sampled_is_the_forward_loop(t, k, p, seed):
+    """ref_generate_sampled (the checker of the device's sampled decodes) is
+    the loop of RefModel.forward and Sampler.sample that chat.rs:149-178
+    runs: each token drawn from the previous forward's logits, then fed at
+    the next position; the generator ends in the loop's state."""
+    cfg = Config(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                 num_key_value_heads=2, vocab_size=300, head_dim_=64)
+    w = synth.weights(cfg, seed=5, random_gains=True)
+    prompt = synth.prompt(6, cfg.vocab_size, seed=5)
+    m = ref.RefModel(cfg, w)
+    a = ref.Sampler(t, k, p, seed)
+    toks = m.generate_sampled(m.state(32), prompt, 12, a)
+    b = ref.Sampler(t, k, p, seed)
+    st = m.state(32)
+    lg = m.forward(st, prompt, 0)
+    for i in range(12):
+        tok = b.sample(lg)
+        assert tok == toks[i], f"token {i}"
+        lg = m.forward(st, [tok], len(prompt) + i)
+    assert a.state == b.state
+    if t > 0:
+        assert len(set(toks.tolist())) > 1, "a sampled run that never varies pins little"
+
+
+def test_ref_chat_sampled_is_the_forward_loop():
+    """A sampled RefChat reply is the same loop, stopping at a stop token
+    without feeding it; its cache then holds exactly the fed tokens (the next
+    turn's logits equal a fresh forward over all of them)."""
+    cfg = Config(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                 num_key_value_heads=2, vocab_size=300, head_dim_=64)
+    w = synth.weights(cfg, seed=6, random_gains=True)
+    m = ref.RefModel(cfg, w)
+    prompt = synth.prompt(5, cfg.vocab_size, seed=6)
+    free = ref.Sampler(0.9, 30, 0.9, 11)
+    probe = m.generate_sampled(m.state(64), prompt, 20, free)
+    stop = [int(probe[9])]  # a token the unbounded run draws
+    chat = ref.RefChat(m, 64, ref.Sampler(0.9, 30, 0.9, 11))
+    end = [1, 2]
+    reply = chat.generate(prompt, stop, end, 40)
+    b = ref.Sampler(0.9, 30, 0.9, 11)
+    st = m.state(64)
+    lg = m.forward(st, prompt, 0)
+    fed = list(prompt)
+    want = []
+    while True:
+        tok = b.sample(lg)
+        want.append(tok)
+        if tok in stop:
+            break
+        lg = m.forward(st, [tok], len(fed))
+        fed.append(tok)
+    assert reply.tolist() == want and want[-1] == stop[0] and len(want) <= 10
+    assert chat.sampler.state == b.state
+    fed += end
+    assert chat.len == len(fed)
+    fresh = m.forward(m.state(64), fed, 0)
+    assert np.array_equal(chat.logits.view(np.uint32), fresh.view(np.uint32))
+
+
 # ---- sampling (model/sampler.rs) ----
 
 M64 = (1 << 64) - 1

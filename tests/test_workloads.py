@@ -99,6 +99,17 @@ def test_qwen4b_shape_reduced_depth(hip):
     check_workload(hip, QWEN3_4B.with_layers(3), seed=9, n_prompt=600, steps=32, what="qwen3-4b x3 600+32")
 
 
+def test_qwen4b_split_attention_decode(hip):
+    """Three layers of the Qwen3-4B shape, a 2600-token prompt fed as 2048 +
+    552 tokens, then 16 greedy steps. Past 1024 f32 positions at 32 q heads
+    the captured step leaves the fused q/k/v + attention launch for the
+    split attention (the register kernel with groups of 4 q heads, one split
+    per 64 positions: 41 splits) and its combine, the launches of the 8K
+    workload of this shape."""
+    check_workload(hip, QWEN3_4B.with_layers(3), seed=31, n_prompt=2600, steps=16, what="qwen3-4b x3 2600+16",
+                   split=2048)
+
+
 # Small models with 1, 4 and 8 query heads per KV head.
 GROUPS = {
     1: Config(hidden_size=512, intermediate_size=1536, num_hidden_layers=2, num_attention_heads=4,
@@ -111,10 +122,12 @@ GROUPS = {
 
 
 @pytest.mark.parametrize("group", sorted(GROUPS))
-@pytest.mark.parametrize("n_prompt,steps", [(9, 20), (200, 12)])
+@pytest.mark.parametrize("n_prompt,steps", [(9, 20), (200, 12), (1100, 6)])
 def test_group_sizes_greedy(hip, group, n_prompt, steps):
     """The captured decode step at 1, 4 and 8 query heads per KV head, f32
-    caches, against the oracle: logits within 1e-4, identical tokens."""
+    caches, against the oracle: logits within 1e-4, identical tokens. Groups
+    of 1 and 8 take the split attention kernel; at 1100 positions it runs 18
+    splits and the combine."""
     cfg = GROUPS[group]
     w = synth.weights(cfg, seed=20 + group, random_gains=True)
     r = ref.RefModel(cfg, w)

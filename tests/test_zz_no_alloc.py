@@ -37,8 +37,11 @@ def _call(fn, hip, out, q, k, v, pos, H, hd, KVH):
              C.c_void_p(v.handle), C.c_size_t(pos), C.c_size_t(H), C.c_size_t(hd), C.c_size_t(KVH)))
 
 
-@pytest.mark.parametrize("first,second", [((4096, 1, 16, 8), (1000, 1, 16, 8)), ((20000, 1, 32, 8), (600, 3, 8, 2))])
+@pytest.mark.parametrize("first,second", [((4096, 1, 16, 8), (1000, 1, 16, 8)), ((20000, 1, 32, 8), (600, 3, 8, 2)),
+                                          ((16400, 1, 64, 8), (9000, 1, 64, 8))])
 def test_noalloc_matches_attention(hip, first, second):
+    """The third pair: one token of 64 heads past 16384 positions, 256
+    splits (64 x 256 x 130 floats, 8.5 MB of partials)."""
     L = lib()
     for i, (ctx, n, H, KVH) in enumerate((first, second)):
         (kv, vv, q), (bk, bv, bq) = _case(hip, ctx, n, H, KVH, seed=ctx + i)

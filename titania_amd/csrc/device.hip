@@ -389,13 +389,13 @@ int th_rope(th_device *dev, th_buffer *x, const th_buffer *table, size_t pos, si
     return TH_OK;
 }
 
-// model/cpu.rs:113-149 / model/titania.rs:186-209
 }  // extern "C"
 
 namespace {
 
-// th_attention, with its split partials in the device's growable scratch, or
-// (fixed) in the no-alloc array, refusing calls whose partials outgrow it.
+// th_attention (model/cpu.rs:113-149 / model/titania.rs:186-209), with its
+// split partials in the device's growable scratch, or (fixed) in the no-alloc
+// array, refusing calls whose partials outgrow it.
 int attention(th_device *dev, th_buffer *out, const th_buffer *q, const th_buffer *k_cache, const th_buffer *v_cache,
               size_t pos, size_t n_heads, size_t head_dim, size_t n_kv_heads, bool fixed) {
     TH_REQUIRE(dev && out && q && k_cache && v_cache, "th_attention: null argument");

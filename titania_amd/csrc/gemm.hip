@@ -794,6 +794,11 @@ hipError_t launch_gemm_qkv(hipStream_t s, const uint16_t *hi, const uint16_t *lo
     if (!hi || !lo || !wq || !wk || !wv || a.head_dim != 128 || cols % BK || cols >= ((size_t)1 << 20) ||
         a.n_heads < 1 || a.n_kv_heads < 1 || (a.n + Head::BM - 1) / Head::BM > 65535)
         return hipErrorInvalidValue;
+    // The planes as launch_gemm_qkv_huge takes them (a position read on the
+    // device is the caller's to keep below plane_len).
+    if (a.kh && (!a.kl || !a.vh || !a.vl || a.kv_bf16 || a.plane_len % 64 ||
+                 (!a.pos_dev && (a.pos < 0 || a.pos + a.n > a.plane_len))))
+        return hipErrorInvalidValue;
     dim3 grid((unsigned)(a.n_heads + 2 * a.n_kv_heads), (unsigned)((a.n + Head::BM - 1) / Head::BM));
     if (a.kv_bf16)
         gemm_qkv_kernel<uint16_t><<<grid, Head::NT, 0, s>>>(wq, wk, wv, hi, lo, a.n, (int)cols, a);

@@ -10,7 +10,10 @@
 #include "common.h"
 
 namespace {
-constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+// Covers the partials of one token at any context for up to 126 heads of
+// head_dim 128 (63 of head_dim 256): a single-token call takes at most 256
+// splits of (head_dim + 2) floats a head.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 }
 
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];

@@ -193,6 +193,60 @@ int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_weight *
     return TH_OK;
 }
 
+int th_test_step_attention(th_device *dev, const th_buffer *qkv, const th_weight *q_norm, const th_weight *k_norm,
+                           float eps, const th_buffer *rope, th_buffer *k_cache, th_buffer *v_cache, size_t max_len,
+                           size_t pos, size_t n_heads, size_t n_kv_heads, int kv_bf16, th_buffer *att_out,
+                           int *n_splits) {
+    TH_REQUIRE(dev && qkv && rope && k_cache && v_cache && att_out, "th_test_step_attention: null argument");
+    const size_t hd = 128, qd = n_heads * hd, kvd = n_kv_heads * hd;
+    const size_t group = n_kv_heads ? n_heads / n_kv_heads : 0;
+    TH_REQUIRE(n_kv_heads > 0 && group * n_kv_heads == n_heads && (group == 1 || group == 2 || group == 4 || group == 8),
+               "the split attention takes KV groups of 1, 2, 4 or 8 q heads");
+    TH_REQUIRE(qkv->len == qd + 2 * kvd && att_out->len == qd, "qkv holds the raw q, k, v rows; att_out n_heads x 128");
+    TH_REQUIRE((!q_norm || q_norm->numel == hd) && (!k_norm || k_norm->numel == hd), "q/k norms hold 128 gains");
+    TH_REQUIRE(kv_bf16 == 0 || kv_bf16 == 1, "kv_bf16 is 0 or 1");
+    TH_REQUIRE(pos < max_len && rope->len >= max_len * hd, "the rope table holds max_len positions");
+    // A pass of cached rows may start up to a pass below max_len: the caches
+    // extend kStepKvTailRows rows of head_dim floats past the last head (bf16
+    // caches hold two values a float).
+    const size_t cache_floats = kv_bf16 ? (n_kv_heads * max_len * hd + 1) / 2 : n_kv_heads * max_len * hd;
+    const size_t need = cache_floats + (size_t)th::kStepKvTailRows * hd;
+    TH_REQUIRE(k_cache->len >= need && v_cache->len >= need, "caches need %zu floats (the tail included)", need);
+    const int nsplit = th::step_attention_splits(max_len, kv_bf16);
+    DevMem st, part;
+    TRY(st.alloc(sizeof(th::StepState), dev->stream));
+    th::StepState host{};
+    host.pos = (long long)pos;
+    TH_HIP(hipMemcpyAsync(st.p, &host, sizeof host, hipMemcpyHostToDevice, dev->stream));
+    th::StepAttnArgs a{};
+    a.qkv = qkv->ptr;
+    a.q_norm = q_norm ? q_norm->ptr : nullptr;
+    a.k_norm = k_norm ? k_norm->ptr : nullptr;
+    a.rope = rope->ptr;
+    a.k_cache = k_cache->ptr;
+    a.v_cache = v_cache->ptr;
+    a.head_stride = (long long)(max_len * hd);
+    a.pos = &static_cast<th::StepState *>(st.p)->pos;
+    a.n_heads = (int)n_heads;
+    a.n_kv_heads = (int)n_kv_heads;
+    a.nsplit = nsplit;
+    a.kv_bf16 = kv_bf16;
+    a.eps = eps;
+    a.out = att_out->ptr;
+    const size_t pf = th::attention_scratch(1, n_heads, hd, nsplit);
+    if (pf) {
+        TRY(part.alloc(pf * sizeof(float), dev->stream));
+        a.part_acc = static_cast<float *>(part.p);
+        a.part_ml = a.part_acc + n_heads * (size_t)nsplit * hd;
+    }
+    TH_HIP(th::launch_step_attention(dev->stream, a));
+    if (nsplit > 1)
+        TH_HIP(th::launch_attn_combine(dev->stream, att_out->ptr, a.part_acc, a.part_ml, n_heads, nsplit, (int)hd));
+    TH_HIP(hipStreamSynchronize(dev->stream));
+    if (n_splits) *n_splits = nsplit;
+    return TH_OK;
+}
+
 int th_test_gemm_qkv(th_device *dev, const th_buffer *xn, const th_weight *wq, const th_weight *wk,
                      const th_weight *wv, const th_weight *q_norm, const th_weight *k_norm, float eps,
                      const th_buffer *rope, th_buffer *k_cache, th_buffer *v_cache, size_t max_len, size_t pos,
