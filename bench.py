@@ -59,13 +59,23 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
+def cpu_threads() -> tuple[int, int]:
+    """(threads the CPU baseline uses, logical cores this process may run on):
+    every core of the affinity mask, as rayon's default takes every logical
+    core, unless OMP_NUM_THREADS sets the host's CPU share lower."""
+    visible = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(visible, int(share)) if share.isdigit() and int(share) > 0 else visible
+    return threads, visible
+
+
 def cpu_baseline(cfg, weights, prompt, steps: int, repeats: int) -> dict:
     """The CPU oracle (C restatement of the reference's Cpu device and forward
     pass) on the same weights and prompt: greedy decode tokens/s from position
     len(prompt), median of `repeats` runs."""
     from oracle import ref
 
-    cores = min(os.cpu_count() or 1, 16)
+    cores, visible = cpu_threads()
     ref.set_threads(cores)
     model = ref.RefModel(cfg, weights)
     rates, tokens = [], []
@@ -85,6 +95,7 @@ def cpu_baseline(cfg, weights, prompt, steps: int, repeats: int) -> dict:
         "value": rates[len(rates) // 2],
         "unit": "tokens/s",
         "cores": cores,
+        "cores_visible": visible,
         "cpu": cpu_model_name(),
         "kind": "port",
         "sample": f"{steps} greedy decode steps after the {len(prompt)}-token prompt, median of {repeats} runs",
@@ -101,7 +112,7 @@ def cpu_baseline_at_context(cfg, weights, ctx: int, steps: int, first_token: int
     ones). One untimed step first, then `steps` timed ones."""
     from oracle import ref
 
-    cores = min(os.cpu_count() or 1, 16)
+    cores, visible = cpu_threads()
     ref.set_threads(cores)
     model = ref.RefModel(cfg, weights)
     st = model.state(ctx + steps + 1)
@@ -125,11 +136,42 @@ def cpu_baseline_at_context(cfg, weights, ctx: int, steps: int, first_token: int
         "value": rate,
         "unit": "tokens/s",
         "cores": cores,
+        "cores_visible": visible,
         "cpu": cpu_model_name(),
         "kind": "port",
         "sample": f"{steps} greedy decode steps at positions {ctx + 1}-{ctx + steps} over f32 caches of {ctx} "
                   "earlier positions (seeded values in place of a prefill), after one untimed step",
     }
+
+
+def trait_path_decode(model, cfg, prompt, steps: int, paths: dict) -> dict:
+    """Greedy decode through the Device-trait paths, as `titania run --device
+    hip` would drive them: the prompt, then per step one forward of the
+    picked token with its logits read back and the argmax taken on the host
+    (model/chat.rs:149-178 at temperature 0 over Model::forward). OPS is the
+    reference's unpatched forward_batch (one trait primitive per call), TRAIT
+    the patched one (titania_amd/rust/patches: the fused trait-extension
+    methods). Wall-clock tokens/s over `steps` steps after 4 untimed ones."""
+    from titania_amd.model import State
+
+    out = {}
+    for name, path in paths.items():
+        st = State(model, len(prompt) + steps + 4)
+        logits = model.forward(st, prompt, 0, path)
+        toks = []
+        pos = len(prompt)
+        for i in range(steps + 4):
+            if i == 4:
+                t0 = time.perf_counter()
+            tok = int(np.argmax(logits))
+            toks.append(tok)
+            logits = model.forward(st, [tok], pos, path)
+            pos += 1
+        wall = time.perf_counter() - t0
+        st.close()
+        out[name] = {"value": steps / wall, "unit": "tokens/s", "ms_per_step": wall * 1000.0 / steps,
+                     "tokens": toks}
+    return out
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
@@ -451,6 +493,9 @@ def main() -> int:
                          "KV caches, reported inside the line as long_context_4b (0: skip it)")
     ap.add_argument("--long-cpu-steps", type=int, default=4,
                     help="CPU-oracle decode steps timed at that context")
+    ap.add_argument("--trait-steps", type=int, default=32,
+                    help="also time greedy decode through the Device-trait paths (ops, trait) for this many steps "
+                         "(0: skip)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -475,7 +520,8 @@ def main() -> int:
               "is not supported (no multi-GPU sharding is built).", file=sys.stderr)
         return 2
 
-    from titania_amd import QWEN3_0_6B, QWEN3_4B, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, Hip, synth
+    from titania_amd import (QWEN3_0_6B, QWEN3_4B, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, TH_PATH_TRAIT,
+                             Hip, synth)
     from titania_amd.model import Model, State
 
     cfg = QWEN3_0_6B if args.model == "qwen3-0.6b" else QWEN3_4B
@@ -573,6 +619,16 @@ def main() -> int:
     }
     if args.prefill:
         out["prefill"] = prefill_bench(dev, model, cfg, args.prefill, kv, args.seed)
+    if args.trait_steps and kv == TH_KV_F32:
+        tp = trait_path_decode(model, cfg, prompt, args.trait_steps, {"ops": TH_PATH_OPS, "trait": TH_PATH_TRAIT})
+        fused = [int(x) for x in tokens]
+        for v in tp.values():
+            n = min(len(fused), len(v["tokens"]))
+            v["tokens_match_fused"] = v.pop("tokens")[:n] == fused[:n]
+        tp["note"] = ("side figures, not the metric: the Device-trait paths with the logits read and the argmax "
+                      "taken on the host every step; ops = the reference's forward_batch over the hip device's "
+                      "primitives, trait = the patched forward_batch over its fused trait methods")
+        out["trait_paths"] = tp
     if not args.no_cpu:
         cb = cpu_baseline(cfg, weights, prompt, K, args.cpu_repeats)
         out["parity_tokens_match"] = [int(x) for x in tokens] == cb.pop("tokens")

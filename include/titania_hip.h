@@ -134,9 +134,31 @@ TH_API void th_graph_free(th_device *dev, th_graph *graph);
 /* ---- fused extensions (each equals its composition of trait methods) ---- */
 
 /* x += y, then xb = rmsnorm(x) with `weight` (the add, copy and rmsnorm of
- * model/model.rs:132-136). y may be NULL for copy + rmsnorm alone (model.rs:106-107). */
+ * model/model.rs:132-136). y may be NULL for copy + rmsnorm alone (model.rs:106-107),
+ * and may be xb itself (the residual add of a projection written to xb, then
+ * the norm into xb). Default methods `add_rmsnorm` / `copy_rmsnorm` of the
+ * trait extension (titania_amd/rust/patches/model-device.rs.patch). */
 TH_API int th_add_rmsnorm(th_device *dev, th_buffer *x, const th_buffer *y, th_buffer *xb, const th_weight *weight,
                    float eps);
+/* The attention block's input side for n = xb.len / hidden tokens at
+ * positions pos.. (model/model.rs:108-120 in one call): q, k, v = wq, wk, wv
+ * . xb; q and k RMSNorm'd per head by q_norm / k_norm (either may be NULL) and
+ * rotated with the rope table; k and v copied into the caches, laid out
+ * [position][n_kv_heads][head_dim] as th_attention reads them, at pos. Equals
+ * matmul x 3, rmsnorm x 2, rope x 2 and copy x 2 in that order within
+ * rounding; afterwards k and v hold the projections before the norm and
+ * rotation (nothing reads them after the copies). Default method
+ * `qkv_rope_append` of the trait extension. */
+TH_API int th_qkv_rope_append(th_device *dev, th_buffer *q, th_buffer *k, th_buffer *v, const th_weight *wq,
+                              const th_weight *wk, const th_weight *wv, const th_weight *q_norm,
+                              const th_weight *k_norm, const th_buffer *xb, const th_buffer *rope,
+                              th_buffer *k_cache, th_buffer *v_cache, size_t pos, size_t n_heads, size_t n_kv_heads,
+                              size_t head_dim, float eps);
+/* gate = silu(w_gate . xb) * (w_up . xb) (model/model.rs:137-139: matmul,
+ * matmul, silu_mul); `up` is scratch, its contents afterwards unspecified.
+ * Default method `gate_up_silu` of the trait extension. */
+TH_API int th_gate_up_silu(th_device *dev, th_buffer *gate, th_buffer *up, const th_weight *w_gate,
+                           const th_weight *w_up, const th_buffer *xb);
 /* Greedy choice (model/sampler.rs:21-33 at temperature 0): index of the largest
  * of the buffer's values under IEEE total order, lowest index on ties. */
 TH_API int th_argmax(th_device *dev, const th_buffer *logits, uint32_t *token);
@@ -212,6 +234,8 @@ TH_API void th_state_destroy(th_state *state);
 
 #define TH_PATH_OPS 0   /* one trait primitive per step, exactly as model.rs:103-148 calls them */
 #define TH_PATH_FUSED 1 /* fused kernels, same results within rounding */
+#define TH_PATH_TRAIT 2 /* the trait extension's methods in the order the patched forward_batch calls them
+                           (titania_amd/rust/patches/model-model.rs.patch), on the caches of TH_PATH_OPS */
 
 /* model/model.rs:83-91 `Model::forward`: runs n tokens, the first at position
  * pos, adds their keys and values to the caches and writes the logits of the

@@ -108,6 +108,73 @@ def test_rust_device_impl_covers_the_trait():
     assert called <= set(cabi.header_signatures()), called - set(cabi.header_signatures())
 
 
+# The trait extension (titania_amd/rust/patches/model-device.rs.patch): each
+# default method, and the header function hip.rs overrides it with.
+EXTENSION_METHODS = {"add_rmsnorm": "th_add_rmsnorm", "qkv_rope_append": "th_qkv_rope_append",
+                     "gate_up_silu": "th_gate_up_silu", "argmax": "th_argmax"}
+PATCHES = cabi.ROOT / "titania_amd" / "rust" / "patches"
+PATCHED_FILES = ["model/device.rs", "model/model.rs", "model/lib.rs", "model/Cargo.toml", "cli/opts.rs", "cli/run.rs"]
+
+
+def _added_lines(name: str) -> str:
+    text = (PATCHES / name).read_text()
+    return "\n".join(line[1:] for line in text.splitlines() if line.startswith("+") and not line.startswith("+++"))
+
+
+def test_rust_device_impl_overrides_the_extension():
+    """Every default method the trait-extension patch adds is overridden in
+    hip.rs through its fused header function, and the patched forward_batch
+    calls each of them."""
+    device = _added_lines("model-device.rs.patch")
+    model = _added_lines("model-model.rs.patch")
+    text = (cabi.ROOT / "titania_amd" / "rust" / "model" / "hip.rs").read_text()
+    impl = text[text.index("impl Device for Hip"):text.index("pub struct HipModel")]
+    header = cabi.header_signatures()
+    for m, fn in EXTENSION_METHODS.items():
+        assert re.search(rf"\bfn {m}\(", device), f"default method {m}"
+        body = impl[impl.index(f"fn {m}("):]
+        body = body[:body.index("\n    }\n")]
+        assert f"sys::{fn}(" in body, (m, fn)
+        assert fn in header
+        assert re.search(rf"\.{m}\(", model), f"forward_batch calls {m}"
+    assert len(re.findall(r"\bfn \w+\(", device)) == len(EXTENSION_METHODS)
+
+
+def test_patches_apply_to_the_reference(tmp_path):
+    """The reference-side patches apply cleanly to copies of the reference's
+    files (the reference itself is not touched) and give the `hip` device,
+    its CLI name and the extension calls."""
+    import shutil
+    import subprocess
+
+    ref_root = Path("/root/reference")
+    if not (ref_root / "model" / "device.rs").exists():
+        pytest.skip("the reference sources are not in this container")
+    for f in PATCHED_FILES:
+        (tmp_path / f).parent.mkdir(parents=True, exist_ok=True)
+        shutil.copy(ref_root / f, tmp_path / f)
+    for f in PATCHED_FILES:
+        patch = PATCHES / (f.replace("/", "-") + ".patch")
+        r = subprocess.run(["patch", "-p1", "--no-backup-if-mismatch", "-i", str(patch)], cwd=tmp_path,
+                           capture_output=True, text=True)
+        assert r.returncode == 0, (f, r.stdout, r.stderr)
+    opts = (tmp_path / "cli/opts.rs").read_text()
+    assert '"hip" => Ok(Device::Hip)' in opts
+    run = (tmp_path / "cli/run.rs").read_text()
+    assert "Device::Hip => serve(dir, Hip::new(0)" in run and run.count("Device::Hip =>") == 3
+    lib_rs = (tmp_path / "model/lib.rs").read_text()
+    assert "mod hip;" in lib_rs and "pub use hip::{Hip, HipModel};" in lib_rs
+    assert "titania-hip-sys" in (tmp_path / "model/Cargo.toml").read_text()
+    model = (tmp_path / "model/model.rs").read_text()
+    body = model[model.index("fn run_batch("):model.index("pub struct State")]
+    # The per-layer copies and norms now go through the extension.
+    assert "d.copy(&mut s.xb, 0, &s.x, 0" not in body
+    for m in EXTENSION_METHODS:
+        if m != "argmax":
+            assert f"d.{m}(" in body, m
+    assert "self.device.argmax(&state.logits)" in model
+
+
 def test_errors_without_gpu_are_reported():
     lib = _lib.lib()
     rc = lib.th_resize(None, None, 1)

@@ -396,6 +396,84 @@ def test_add_rmsnorm(hip):
     assert_close(hip.read(bxb), cxb, what="rmsnorm(x)")
 
 
+@pytest.mark.parametrize("n,pos,shape", [(1, 0, "0.6b"), (1, 37, "4b"), (3, 10, "0.6b"), (20, 5, "0.6b"),
+                                         (64, 100, "4b"), (5, 2, "tiny")])
+def test_qkv_rope_append(hip, n, pos, shape):
+    """th_qkv_rope_append (the trait extension's qkv_rope_append) against the
+    oracle's matmul x 3, q/k rmsnorm, rope x 2 and cache copies
+    (model.rs:108-120) into position-major caches: one token takes the
+    three-matrix GEMV, 3 the few-token GEMV, 20 and 64 the MFMA GEMM; the
+    tiny shape (head_dim 64, hidden 256) has no q/k norms."""
+    H, nh, nkv, hd, norms = {"0.6b": (1024, 16, 8, 128, True), "4b": (2560, 32, 8, 128, True),
+                             "tiny": (256, 4, 2, 64, False)}[shape]
+    qd, kvd, max_len, eps = nh * hd, nkv * hd, pos + n + 5, 1e-6
+    ws = [normal_bf16(r * H, 130 + i, "w", 0.05) for i, r in enumerate((qd, kvd, kvd))]
+    W = [hip.upload(Tensor((r, H), w)) for r, w in zip((qd, kvd, kvd), ws)]
+    gq = f32_to_bf16(1.0 + bf16_to_f32(normal_bf16(hd, 131, "gq", 0.1)))
+    gk = f32_to_bf16(1.0 + bf16_to_f32(normal_bf16(hd, 132, "gk", 0.1)))
+    QN, KN = (hip.upload(Tensor((hd,), gq)), hip.upload(Tensor((hd,), gk))) if norms else (None, None)
+    rng = np.random.default_rng(n + pos)
+    xb = rng.standard_normal(n * H).astype(np.float32)
+    kc = rng.standard_normal(max_len * kvd).astype(np.float32)
+    vc = rng.standard_normal(max_len * kvd).astype(np.float32)
+    table = ref.rope_table(max_len, hd, 1e6)
+    bufs = {}
+    for name, a in (("xb", xb), ("kc", kc), ("vc", vc), ("rope", table)):
+        bufs[name] = hip.alloc(a.size)
+        hip.write(bufs[name], a)
+    q, k, v = hip.alloc(n * qd), hip.alloc(n * kvd), hip.alloc(n * kvd)
+    hip.qkv_rope_append(q, k, v, W[0], W[1], W[2], QN, KN, bufs["xb"], bufs["rope"], bufs["kc"], bufs["vc"], pos,
+                        nh, nkv, hd, eps)
+    eq = ref.matmul(ws[0], qd, H, xb)
+    ek = ref.matmul(ws[1], kvd, H, xb)
+    ev = ref.matmul(ws[2], kvd, H, xb)
+    if norms:
+        eq, ek = ref.rmsnorm(eq, gq, eps), ref.rmsnorm(ek, gk, eps)
+    eq, ek = ref.rope(eq, table, pos, nh, hd), ref.rope(ek, table, pos, nkv, hd)
+    ekc = ref.copy(kc, pos * kvd, ek, 0, n * kvd)
+    evc = ref.copy(vc, pos * kvd, ev, 0, n * kvd)
+    for what, got, exp in (("q", hip.read(q), eq), ("k cache", hip.read(bufs["kc"]), ekc),
+                           ("v cache", hip.read(bufs["vc"]), evc)):
+        assert rel_error(got, exp) <= 1e-3, what
+        assert_close(got, exp, rel=1e-4, abs_=5e-5, what=f"{what} n={n} {shape}")
+    dk = hip.read(bufs["kc"])
+    assert np.array_equal(dk[:pos * kvd], kc[:pos * kvd]) and np.array_equal(dk[(pos + n) * kvd:],
+                                                                               kc[(pos + n) * kvd:])
+
+
+@pytest.mark.parametrize("n,H,I", [(1, 1024, 3072), (1, 2560, 9728), (4, 1024, 3072), (32, 1024, 3072),
+                                   (2, 256, 512)])
+def test_gate_up_silu(hip, n, H, I):
+    """th_gate_up_silu (the trait extension's gate_up_silu) against the
+    oracle's matmul x 2 + silu_mul (model.rs:137-139): one token takes the
+    GEMV with the SiLU epilogue, 32 the MFMA GEMM."""
+    wg, wu = normal_bf16(I * H, 140, "g", 0.05), normal_bf16(I * H, 141, "u", 0.05)
+    Wg, Wu = hip.upload(Tensor((I, H), wg)), hip.upload(Tensor((I, H), wu))
+    xb = np.random.default_rng(n + H).standard_normal(n * H).astype(np.float32)
+    bx, gate, up = hip.alloc(xb.size), hip.alloc(n * I), hip.alloc(n * I)
+    hip.write(bx, xb)
+    hip.gate_up_silu(gate, up, Wg, Wu, bx)
+    exp = ref.silu_mul(ref.matmul(wg, I, H, xb), ref.matmul(wu, I, H, xb))
+    got = hip.read(gate)
+    assert rel_error(got, exp) <= 1e-3
+    assert_close(got, exp, rel=1e-4, abs_=5e-5, what=f"gate_up_silu n={n}")
+
+
+def test_add_rmsnorm_in_place(hip):
+    """y may be xb itself (the trait extension's add_rmsnorm: the projection
+    in xb added into x, then x's norm into xb)."""
+    rows, dim = 5, 1024
+    g = f32_to_bf16(1.0 + bf16_to_f32(normal_bf16(dim, 121, "g", 0.1)))
+    x, y = numbers(rows * dim, 23), numbers(rows * dim, 24)
+    bx, bxb = hip.alloc(x.size), hip.alloc(y.size)
+    hip.write(bx, x)
+    hip.write(bxb, y)
+    hip.add_rmsnorm(bx, bxb, bxb, hip.upload(Tensor((dim,), g)), 1e-6)
+    cx = ref.add(x, y)
+    assert_close(hip.read(bx), cx, what="x += xb")
+    assert_close(hip.read(bxb), ref.rmsnorm(cx, g, 1e-6), what="xb = rmsnorm(x)")
+
+
 def test_argmax(hip):
     v = 151936
     x = bf16_to_f32(normal_bf16(v, 130, "logits"))

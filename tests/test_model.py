@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 
 from oracle import ref
-from titania_amd import QWEN3_0_6B, QWEN3_TINY, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, Sampler
+from titania_amd import (QWEN3_0_6B, QWEN3_TINY, TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, TH_PATH_TRAIT,
+                         Sampler)
 from titania_amd.config import Config
 from titania_amd import synth
 from titania_amd.model import Model, State
@@ -34,7 +35,7 @@ def tiny(hip):
     m.close()
 
 
-@pytest.mark.parametrize("path", [TH_PATH_OPS, TH_PATH_FUSED])
+@pytest.mark.parametrize("path", [TH_PATH_OPS, TH_PATH_FUSED, TH_PATH_TRAIT])
 def test_tiny_forward(tiny, path):
     m, r = tiny
     c = QWEN3_TINY
@@ -89,16 +90,21 @@ def test_tiny_decode_large_cache(tiny, kv):
 
 
 def test_paths_refuse_to_mix(tiny):
-    m, _ = tiny
+    m, r = tiny
     st = State(m, 32)
     m.forward(st, [1, 2, 3], 0, TH_PATH_OPS)
     with pytest.raises(Exception):
         m.forward(st, [4], 3, TH_PATH_FUSED)
+    # The trait path keeps the ops path's caches: it continues where that left off.
+    got = m.forward(st, [4], 3, TH_PATH_TRAIT)
+    rs = r.state(32)
+    r.forward(rs, [1, 2, 3], 0)
+    assert np.max(np.abs(got - r.forward(rs, [4], 3))) <= 1e-4
     st.close()
 
 
 @pytest.mark.parametrize("name", ["tied", "untied"])
-@pytest.mark.parametrize("path", [TH_PATH_OPS, TH_PATH_FUSED])
+@pytest.mark.parametrize("path", [TH_PATH_OPS, TH_PATH_FUSED, TH_PATH_TRAIT])
 def test_forward_matches_transformers(hip, name, path):
     """The device's logits at every position against transformers'
     Qwen3ForCausalLM (a fixture made with tests/golden/make_hf_qwen3.py), an
@@ -153,15 +159,24 @@ def test_qwen06_greedy(qwen06):
     st.close()
 
 
-def test_qwen06_ops_path_logits(qwen06):
-    """The trait-primitive path on the same model: prompt logits against the oracle."""
+@pytest.mark.parametrize("path", [TH_PATH_OPS, TH_PATH_TRAIT])
+def test_qwen06_ops_path_logits(qwen06, path):
+    """The trait-primitive path and the trait-extension path on the same
+    model: prompt logits (a 16-token batch and a 64 + 6 two-batch prompt)
+    against the oracle, then single-token steps with their greedy picks."""
     m, r = qwen06
-    prompt = synth.prompt(16, QWEN3_0_6B.vocab_size, seed=1)
-    st = State(m, 32)
-    got = m.forward(st, prompt, 0, TH_PATH_OPS)
-    exp = r.forward(r.state(32), prompt, 0)
-    assert float(np.max(np.abs(got - exp))) <= LOGIT_TOL
-    st.close()
+    for n_prompt in (16, 70):
+        prompt = synth.prompt(n_prompt, QWEN3_0_6B.vocab_size, seed=1)
+        st, rs = State(m, 96), r.state(96)
+        got = m.forward(st, prompt, 0, path)
+        exp = r.forward(rs, prompt, 0)
+        assert float(np.max(np.abs(got - exp))) <= 1e-3
+        for i in range(4):
+            tok = ref.argmax(exp)
+            got = m.forward(st, [tok], n_prompt + i, path)
+            exp = r.forward(rs, [tok], n_prompt + i)
+            assert float(np.max(np.abs(got - exp))) <= 1e-3, (n_prompt, i)
+        st.close()
 
 
 @pytest.fixture

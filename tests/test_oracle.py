@@ -406,6 +406,79 @@ def test_ref_chat_sampled_is_the_forward_loop():
     assert np.array_equal(chat.logits.view(np.uint32), fresh.view(np.uint32))
 
 
+def _patched_forward(cfg, w, tokens, pos, kc, vc, max_len):
+    """run_batch of titania_amd/rust/patches/model-model.rs.patch with the
+    default methods of model-device.rs.patch, on the oracle's restatements of
+    the cpu.rs primitives (one batch of at most 64 tokens): add_rmsnorm =
+    add (when set), copy, rmsnorm; qkv_rope_append = matmul x 3, the q/k
+    norms, rope x 2, copy x 2; gate_up_silu = matmul x 2, silu_mul."""
+    H, hd, I, V = cfg.hidden_size, cfg.head_dim(), cfg.intermediate_size, cfg.vocab_size
+    nh, nkv, eps = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.rms_norm_eps
+    qd, kvd, n = nh * hd, nkv * hd, len(tokens)
+    table = ref.rope_table(max_len, hd, cfg.rope_theta)
+
+    def t(name):
+        return w[name].data
+
+    def add_rmsnorm(x, xb, add, gain):
+        if add:
+            x = ref.add(x, xb)
+        xb = ref.copy(xb, 0, x, 0, n * H)
+        return x, ref.rmsnorm(xb, gain, eps)
+
+    x = ref.embed(t("model.embed_tokens.weight"), H, tokens)
+    xb = np.zeros(n * H, np.float32)
+    for i in range(cfg.num_hidden_layers):
+        p = f"model.layers.{i}"
+        x, xb = add_rmsnorm(x, xb, i > 0, t(f"{p}.input_layernorm.weight"))
+        q = ref.matmul(t(f"{p}.self_attn.q_proj.weight"), qd, H, xb)
+        k = ref.matmul(t(f"{p}.self_attn.k_proj.weight"), kvd, H, xb)
+        v = ref.matmul(t(f"{p}.self_attn.v_proj.weight"), kvd, H, xb)
+        if f"{p}.self_attn.q_norm.weight" in w:
+            q = ref.rmsnorm(q, t(f"{p}.self_attn.q_norm.weight"), eps)
+        if f"{p}.self_attn.k_norm.weight" in w:
+            k = ref.rmsnorm(k, t(f"{p}.self_attn.k_norm.weight"), eps)
+        q = ref.rope(q, table, pos, nh, hd)
+        k = ref.rope(k, table, pos, nkv, hd)
+        kc[i] = ref.copy(kc[i], pos * kvd, k, 0, n * kvd)
+        vc[i] = ref.copy(vc[i], pos * kvd, v, 0, n * kvd)
+        att = ref.attention(q, kc[i], vc[i], pos, nh, hd, nkv)
+        xb = ref.matmul(t(f"{p}.self_attn.o_proj.weight"), H, qd, att)
+        x, xb = add_rmsnorm(x, xb, True, t(f"{p}.post_attention_layernorm.weight"))
+        g = ref.matmul(t(f"{p}.mlp.gate_proj.weight"), I, H, xb)
+        u = ref.matmul(t(f"{p}.mlp.up_proj.weight"), I, H, xb)
+        g = ref.silu_mul(g, u)
+        xb = ref.matmul(t(f"{p}.mlp.down_proj.weight"), H, I, g)
+    if cfg.num_hidden_layers:
+        x = ref.add(x, xb)
+    last = ref.rmsnorm(ref.copy(np.zeros(H, np.float32), 0, x, (n - 1) * H, H), t("model.norm.weight"), eps)
+    head = "model.embed_tokens.weight" if cfg.tie_word_embeddings else "lm_head.weight"
+    return ref.matmul(t(head), V, H, last)
+
+
+@pytest.mark.parametrize("kv_heads,tied", [(2, True), (4, False)])
+def test_patched_forward_batch_is_bit_identical(kv_heads, tied):
+    """The trait-extension patch keeps the reference device's results bit for
+    bit: its forward_batch with the default methods gives exactly the logits
+    of the original op order (the oracle's forward), for a prompt and then
+    two single-token steps at later positions."""
+    cfg = Config(hidden_size=256, intermediate_size=512, num_hidden_layers=3, num_attention_heads=4,
+                 num_key_value_heads=kv_heads, vocab_size=300, head_dim_=64, tie_word_embeddings=tied)
+    w = synth.weights(cfg, seed=13, random_gains=True)
+    m = ref.RefModel(cfg, w)
+    max_len = 40
+    st = m.state(max_len)
+    kvd = kv_heads * 64
+    kc = [np.zeros(max_len * kvd, np.float32) for _ in range(cfg.num_hidden_layers)]
+    vc = [np.zeros(max_len * kvd, np.float32) for _ in range(cfg.num_hidden_layers)]
+    prompt = synth.prompt(23, cfg.vocab_size, seed=13)
+    calls = [(list(prompt), 0), ([7], 23), ([201], 24)]
+    for toks, pos in calls:
+        want = m.forward(st, toks, pos)
+        got = _patched_forward(cfg, w, toks, pos, kc, vc, max_len)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"tokens at {pos}"
+
+
 # ---- sampling (model/sampler.rs) ----
 
 M64 = (1 << 64) - 1

@@ -15,7 +15,7 @@ SYNTH_PATH = PKG / "libtitania_synth.so"
 
 TH_OK, TH_ERR_INVALID, TH_ERR_HIP, TH_ERR_NOMEM = 0, 1, 2, 3
 TH_KV_F32, TH_KV_BF16 = 0, 1
-TH_PATH_OPS, TH_PATH_FUSED = 0, 1
+TH_PATH_OPS, TH_PATH_FUSED, TH_PATH_TRAIT = 0, 1, 2
 
 
 class HipError(RuntimeError):
@@ -80,6 +80,8 @@ SIGNATURES: dict[str, tuple] = {
     "th_attention_noalloc": (_I, [_P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ]),
     "th_silu_mul": (_I, [_P, _P, _P]),
     "th_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, C.c_float]),
+    "th_qkv_rope_append": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _SZ, _SZ, _SZ, C.c_float]),
+    "th_gate_up_silu": (_I, [_P, _P, _P, _P, _P, _P]),
     "th_argmax": (_I, [_P, _P, C.POINTER(C.c_uint32)]),
     "th_sample": (_I, [_P, _P, C.c_float, _SZ, C.c_float, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)]),
     "th_model_create": (_I, [_P, C.POINTER(ThConfig), C.POINTER(_P), _SZ, C.POINTER(_P)]),

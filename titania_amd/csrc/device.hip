@@ -11,6 +11,7 @@
 #include "common.h"
 #include "gemm.h"
 #include "sample.h"
+#include "step.h"
 
 namespace {
 thread_local std::string g_error;
@@ -356,7 +357,12 @@ int th_matmul(th_device *dev, th_buffer *out, const th_weight *w, const th_buffe
     TH_REQUIRE(out->ptr != x->ptr || n == 0, "matmul cannot write its input");
     if (n >= th::kGemmMinTokens && th::gemm_supported(rows, cols))
         TH_NOT_CAPTURING(dev, "a matmul of 16 or more tokens (stream-ordered scratch)");
-    TH_HIP(th::launch_matmul(dev->stream, out->ptr, w->ptr, rows, cols, x->ptr, n));
+    // One token: the decode step's GEMV (every row's loads in flight before
+    // the input is read) where it takes the row length.
+    if (n == 1 && th::step_gemv_supported((int)cols) && rows < ((size_t)1 << 30))
+        TH_HIP(th::launch_step_gemv(dev->stream, w->ptr, (int)rows, (int)cols, x->ptr, out->ptr));
+    else
+        TH_HIP(th::launch_matmul(dev->stream, out->ptr, w->ptr, rows, cols, x->ptr, n));
     return TH_OK;
 }
 
@@ -473,9 +479,101 @@ int th_add_rmsnorm(th_device *dev, th_buffer *x, const th_buffer *y, th_buffer *
     TH_REQUIRE(dim > 0, "an rmsnorm weight has elements");
     TH_REQUIRE(xb->len == x->len, "xb holds %zu activations, x %zu", xb->len, x->len);
     TH_REQUIRE(!y || y->len >= x->len, "y holds %zu activations, x %zu", y ? y->len : 0, x->len);
-    TH_REQUIRE(!y || (y->ptr != x->ptr && y->ptr != xb->ptr), "y must not alias x or xb");
+    // y may be xb: each row of y is read before that row of xb is written.
+    TH_REQUIRE(!y || y->ptr != x->ptr, "y must not alias x");
     TH_HIP(th::launch_add_rmsnorm(dev->stream, x->ptr, y ? y->ptr : nullptr, xb->ptr, x->len / dim, w->ptr, dim,
                                   eps));
+    return TH_OK;
+}
+
+int th_qkv_rope_append(th_device *dev, th_buffer *q, th_buffer *k, th_buffer *v, const th_weight *wq,
+                       const th_weight *wk, const th_weight *wv, const th_weight *q_norm, const th_weight *k_norm,
+                       const th_buffer *xb, const th_buffer *rope, th_buffer *k_cache, th_buffer *v_cache, size_t pos,
+                       size_t n_heads, size_t n_kv_heads, size_t head_dim, float eps) {
+    TH_REQUIRE(dev && q && k && v && wq && wk && wv && xb && rope && k_cache && v_cache,
+               "th_qkv_rope_append: null argument");
+    TH_REQUIRE(n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 512,
+               "heads of an even head_dim of at most 512");
+    const size_t qd = n_heads * head_dim, kvd = n_kv_heads * head_dim;
+    TH_REQUIRE(wq->ndim == 2 && wk->ndim == 2 && wv->ndim == 2 && wq->shape[0] == qd && wk->shape[0] == kvd &&
+                   wv->shape[0] == kvd && wq->shape[1] > 0 && wk->shape[1] == wq->shape[1] &&
+                   wv->shape[1] == wq->shape[1],
+               "weights are not [n_heads * head_dim, hidden] and [n_kv_heads * head_dim, hidden] x 2");
+    const size_t H = wq->shape[1], n = xb->len / H;
+    TH_REQUIRE(n > 0 && xb->len == n * H, "xb holds %zu activations, not whole rows of %zu", xb->len, H);
+    TH_REQUIRE(q->len == n * qd && k->len == n * kvd && v->len == n * kvd,
+               "q, k and v hold %zu tokens of n_heads and n_kv_heads heads", n);
+    TH_REQUIRE(q->ptr != xb->ptr && k->ptr != xb->ptr && v->ptr != xb->ptr, "q, k and v cannot be xb");
+    TH_REQUIRE((!q_norm || q_norm->numel == head_dim) && (!k_norm || k_norm->numel == head_dim),
+               "q/k norms hold head_dim gains");
+    TH_REQUIRE((pos + n) * head_dim <= rope->len, "position %zu is past the end of the table", pos + n - 1);
+    TH_REQUIRE((pos + n) * kvd <= k_cache->len && (pos + n) * kvd <= v_cache->len,
+               "tokens past the end of the caches");
+    // The projections (model.rs:108-110): one GEMV launch for all three rows
+    // sets at one token, one matrix-core GEMM from 16 tokens.
+    if (n == 1 && th::step_gemv_supported((int)H)) {
+        const uint16_t *w[3] = {wq->ptr, wk->ptr, wv->ptr};
+        const int rows[3] = {(int)qd, (int)kvd, (int)kvd};
+        float *const out[3] = {q->ptr, k->ptr, v->ptr};
+        TH_HIP(th::launch_step_gemv3(dev->stream, w, rows, (int)H, xb->ptr, out));
+    } else if (n >= th::kGemmMinTokens && th::gemm_supported(qd, H) && th::gemm_supported(kvd, H)) {
+        TH_NOT_CAPTURING(dev, "a projection of 16 or more tokens (stream-ordered scratch)");
+        const th::GemmOut o[3] = {{wq->ptr, qd, q->ptr}, {wk->ptr, kvd, k->ptr}, {wv->ptr, kvd, v->ptr}};
+        TH_HIP(th::launch_gemm_outs(dev->stream, xb->ptr, n, H, o, 3));
+    } else {
+        if (n >= th::kGemmMinTokens) TH_NOT_CAPTURING(dev, "a projection of 16 or more tokens (stream-ordered scratch)");
+        TH_HIP(th::launch_matmul(dev->stream, q->ptr, wq->ptr, qd, H, xb->ptr, n));
+        TH_HIP(th::launch_matmul(dev->stream, k->ptr, wk->ptr, kvd, H, xb->ptr, n));
+        TH_HIP(th::launch_matmul(dev->stream, v->ptr, wv->ptr, kvd, H, xb->ptr, n));
+    }
+    // The q/k norms, the rotations and the appends (model.rs:111-120), one
+    // wave per (token, head), into the trait's position-major caches.
+    th::QkvPostArgs a{};
+    a.q = q->ptr;
+    a.k = k->ptr;
+    a.v = v->ptr;
+    a.q_norm = q_norm ? q_norm->ptr : nullptr;
+    a.k_norm = k_norm ? k_norm->ptr : nullptr;
+    a.rope = rope->ptr;
+    a.k_cache = k_cache->ptr;
+    a.v_cache = v_cache->ptr;
+    a.head_stride = (long long)head_dim;
+    a.pos_stride = (long long)kvd;
+    a.pos = (long long)pos;
+    a.n = (int)n;
+    a.n_heads = (int)n_heads;
+    a.n_kv_heads = (int)n_kv_heads;
+    a.head_dim = (int)head_dim;
+    a.eps = eps;
+    TH_HIP(th::launch_qk_norm_rope_append(dev->stream, a));
+    return TH_OK;
+}
+
+int th_gate_up_silu(th_device *dev, th_buffer *gate, th_buffer *up, const th_weight *w_gate, const th_weight *w_up,
+                    const th_buffer *xb) {
+    TH_REQUIRE(dev && gate && up && w_gate && w_up && xb, "th_gate_up_silu: null argument");
+    TH_REQUIRE(w_gate->ndim == 2 && w_up->ndim == 2 && w_gate->shape[0] == w_up->shape[0] &&
+                   w_gate->shape[1] == w_up->shape[1] && w_gate->shape[1] > 0,
+               "gate and up weights of one shape");
+    const size_t I = w_gate->shape[0], H = w_gate->shape[1], n = xb->len / H;
+    TH_REQUIRE(n > 0 && xb->len == n * H, "xb holds %zu activations, not whole rows of %zu", xb->len, H);
+    TH_REQUIRE(gate->len == n * I && up->len == n * I, "gate and up hold %zu tokens of %zu", n, I);
+    TH_REQUIRE(gate->ptr != xb->ptr && up->ptr != xb->ptr && gate->ptr != up->ptr, "gate, up and xb are distinct");
+    if (n == 1 && th::step_gemv_supported((int)H)) {
+        // Both projections and silu(gate) * up in one GEMV launch; up unused.
+        TH_HIP(th::launch_step_silu(dev->stream, w_gate->ptr, w_up->ptr, (int)I, (int)H, xb->ptr, gate->ptr));
+        return TH_OK;
+    }
+    if (n >= th::kGemmMinTokens && th::gemm_supported(I, H)) {
+        TH_NOT_CAPTURING(dev, "a projection of 16 or more tokens (stream-ordered scratch)");
+        const th::GemmOut o[2] = {{w_gate->ptr, I, gate->ptr}, {w_up->ptr, I, up->ptr}};
+        TH_HIP(th::launch_gemm_outs(dev->stream, xb->ptr, n, H, o, 2));
+    } else {
+        if (n >= th::kGemmMinTokens) TH_NOT_CAPTURING(dev, "a projection of 16 or more tokens (stream-ordered scratch)");
+        TH_HIP(th::launch_matmul(dev->stream, gate->ptr, w_gate->ptr, I, H, xb->ptr, n));
+        TH_HIP(th::launch_matmul(dev->stream, up->ptr, w_up->ptr, I, H, xb->ptr, n));
+    }
+    TH_HIP(th::launch_silu_mul(dev->stream, gate->ptr, up->ptr, n * I));
     return TH_OK;
 }
 

@@ -27,6 +27,10 @@ struct GemmOut {
     float *out;
 };
 
+// launch_gemm for 1-3 matrices that share x (one GEMM launch over all their
+// rows), with its scratch in stream-ordered memory for the call.
+hipError_t launch_gemm_outs(hipStream_t s, const float *x, size_t n, size_t cols, const GemmOut *outs, int n_outs);
+
 // Most ways a single-matrix GEMM splits its K range (into partial tiles that a
 // second kernel sums in a fixed order).
 constexpr int kGemmMaxSplitK = 4;

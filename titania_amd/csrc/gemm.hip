@@ -828,6 +828,23 @@ hipError_t launch_gemm_multi(hipStream_t s, const float *x, size_t n, size_t col
     return hipGetLastError();
 }
 
+hipError_t launch_gemm_outs(hipStream_t s, const float *x, size_t n, size_t cols, const GemmOut *outs, int n_outs) {
+    if (n == 0) return hipSuccess;
+    if (n_outs < 1 || n_outs > 3) return hipErrorInvalidValue;
+    size_t most = 0;
+    for (int i = 0; i < n_outs; ++i) {
+        if (!gemm_supported(outs[i].rows, cols)) return hipErrorInvalidValue;
+        most = std::max(most, outs[i].rows);
+    }
+    void *scratch = nullptr;
+    const size_t bytes = gemm_scratch_bytes(n, cols, most);
+    hipError_t e = hipMallocAsync(&scratch, bytes, s);
+    if (e != hipSuccess) return e;
+    e = launch_gemm_multi(s, x, n, cols, outs, n_outs, scratch, bytes);
+    const hipError_t f = hipFreeAsync(scratch, s);
+    return e != hipSuccess ? e : f;
+}
+
 hipError_t launch_gemm(hipStream_t s, float *out, const uint16_t *w, size_t rows, size_t cols, const float *x,
                        size_t n) {
     if (n == 0 || rows == 0) return hipSuccess;

@@ -2,10 +2,12 @@
 // State (model.rs:152-233), Model::forward (model.rs:83-149), and a greedy
 // decode loop that stays on the device (model/chat.rs:149-178 at temperature 0).
 //
-// Two paths compute the same function:
+// Three paths compute the same function:
 //  - TH_PATH_OPS calls the trait's primitives through the public C ABI in
 //    exactly the order model.rs:103-148 does, on the reference's state layout
 //    (BATCH-token chunks, position-major f32 caches);
+//  - TH_PATH_TRAIT calls the trait extension's fused methods where the
+//    patched forward_batch calls them, on the same state;
 //  - TH_PATH_FUSED runs the fused kernels on caches laid out per layer and per
 //    KV head ([layer][k|v][kv_head][max_len][head_dim], f32 or bf16), and is
 //    what a decode step captures into a HIP graph.
@@ -214,6 +216,45 @@ int forward_batch_ops(th_state *s, const uint32_t *tokens, size_t n, size_t pos)
         TRY(th_matmul(d, s->xb, L.down, s->gate));
         TRY(th_add(d, s->x, s->xb));
     }
+    TRY(th_resize(d, s->xb, H));
+    TRY(th_copy(d, s->xb, 0, s->x, (n - 1) * H, H));
+    TRY(th_rmsnorm(d, s->xb, m->norm, eps));
+    TRY(th_matmul(d, s->logits, m->out_proj(), s->xb));
+    return TH_OK;
+}
+
+// The patched forward_batch (titania_amd/rust/patches/model-model.rs.patch)
+// through the trait extension's methods, for n <= BATCH tokens, on the ops
+// path's state: copy_rmsnorm / add_rmsnorm for the residual adds and norms,
+// qkv_rope_append for model.rs:108-120, gate_up_silu for model.rs:137-139; the
+// attention, the o and down projections and the final norm as the primitives.
+int forward_batch_trait(th_state *s, const uint32_t *tokens, size_t n, size_t pos) {
+    th_model *m = s->m;
+    th_device *d = m->dev;
+    const th_config &c = m->c;
+    const float eps = c.rms_norm_eps;
+    const size_t hd = (size_t)c.head_dim, H = (size_t)c.hidden_size;
+    const size_t nh = (size_t)c.num_attention_heads, nkv = (size_t)c.num_key_value_heads;
+    size_t widths[8] = {H, H, nh * hd, nkv * hd, nkv * hd, nh * hd, (size_t)c.intermediate_size,
+                        (size_t)c.intermediate_size};
+    th_buffer *bufs[8] = {s->x, s->xb, s->q, s->k, s->v, s->att, s->gate, s->up};
+    for (int i = 0; i < 8; ++i) TRY(th_resize(d, bufs[i], n * widths[i]));  // State::batch
+
+    TRY(th_embed(d, s->x, m->embed, tokens, n));
+    for (size_t i = 0; i < m->layers.size(); ++i) {
+        const Layer &L = m->layers[i];
+        // The previous layer's down projection (in xb) added into x, then the
+        // attention norm; the first layer only normalizes.
+        TRY(th_add_rmsnorm(d, s->x, i ? s->xb : nullptr, s->xb, L.attn_norm, eps));
+        TRY(th_qkv_rope_append(d, s->q, s->k, s->v, L.q, L.k, L.v, L.q_norm, L.k_norm, s->xb, s->rope, s->k_cache[i],
+                               s->v_cache[i], pos, nh, nkv, hd, eps));
+        TRY(th_attention(d, s->att, s->q, s->k_cache[i], s->v_cache[i], pos, nh, hd, nkv));
+        TRY(th_matmul(d, s->xb, L.o, s->att));
+        TRY(th_add_rmsnorm(d, s->x, s->xb, s->xb, L.mlp_norm, eps));
+        TRY(th_gate_up_silu(d, s->gate, s->up, L.gate, L.up, s->xb));
+        TRY(th_matmul(d, s->xb, L.down, s->gate));
+    }
+    if (!m->layers.empty()) TRY(th_add(d, s->x, s->xb));
     TRY(th_resize(d, s->xb, H));
     TRY(th_copy(d, s->xb, 0, s->x, (n - 1) * H, H));
     TRY(th_rmsnorm(d, s->xb, m->norm, eps));
@@ -598,12 +639,15 @@ int stage_state_tokens(th_state *s, const uint32_t *tokens, size_t n) {
     return TH_OK;
 }
 
+// The ops and trait paths share the reference's caches; the fused path keeps
+// its own.
 int claim_path(th_state *s, int path) {
-    if (s->path != -1 && s->path != path)
+    const int layout = path == TH_PATH_TRAIT ? TH_PATH_OPS : path;
+    if (s->path != -1 && s->path != layout)
         return fail(TH_ERR_INVALID, "this state's caches were filled by the other path");
-    if (path == TH_PATH_OPS && s->kv_dtype != TH_KV_F32)
-        return fail(TH_ERR_INVALID, "the ops path keeps the reference's f32 caches");
-    s->path = path;
+    if (layout == TH_PATH_OPS && s->kv_dtype != TH_KV_F32)
+        return fail(TH_ERR_INVALID, "the ops and trait paths keep the reference's f32 caches");
+    s->path = layout;
     return TH_OK;
 }
 
@@ -806,11 +850,15 @@ int th_forward(th_model *m, th_state *s, const uint32_t *tokens, size_t n, size_
     TH_NOT_CAPTURING(m->dev, "th_forward");
     TH_REQUIRE(n > 0 && tokens, "no tokens to run");  // model.rs:84
     TH_REQUIRE(pos + n <= s->max_len, "tokens past the end of the cache");  // model.rs:85
-    TH_REQUIRE(path == TH_PATH_OPS || path == TH_PATH_FUSED, "unknown path %d", path);
+    TH_REQUIRE(path == TH_PATH_OPS || path == TH_PATH_FUSED || path == TH_PATH_TRAIT, "unknown path %d", path);
     TRY(claim_path(s, path));
     if (path == TH_PATH_OPS) {
         TRY(ensure_ops_state(s));
         for (size_t i = 0; i < n; i += kBatch) TRY(forward_batch_ops(s, tokens + i, std::min(kBatch, n - i), pos + i));
+    } else if (path == TH_PATH_TRAIT) {
+        TRY(ensure_ops_state(s));
+        for (size_t i = 0; i < n; i += kBatch)
+            TRY(forward_batch_trait(s, tokens + i, std::min(kBatch, n - i), pos + i));
     } else {
         TRY(ensure_fused_state(s));
         TRY(stage_state_tokens(s, tokens, n));

@@ -31,6 +31,18 @@ hipError_t launch_step_qkv(hipStream_t s, const StepQkvArgs &a);
 // out = W . x for W [rows, cols].
 hipError_t launch_step_gemv(hipStream_t s, const uint16_t *w, int rows, int cols, const float *x, float *out);
 
+// Whether the step GEMVs take rows of `cols` columns (whole 512-column spans:
+// 1-6, 8 or 19 of them).
+bool step_gemv_supported(int cols);
+
+// out[i] = w[i] . x for three matrices w[i] [rows[i], cols] in one launch.
+hipError_t launch_step_gemv3(hipStream_t s, const uint16_t *const w[3], const int rows[3], int cols, const float *x,
+                             float *const out[3]);
+
+// h[j] = silu(gate_j . x) * (up_j . x) for j < inter (x already normalized).
+hipError_t launch_step_silu(hipStream_t s, const uint16_t *gate, const uint16_t *up, int inter, int cols,
+                            const float *x, float *h);
+
 // x_out = x1 + o; h[j] = silu(gate_j . n) * (up_j . n) with n = rmsnorm(x_out).
 hipError_t launch_step_gate_up(hipStream_t s, const uint16_t *gate, const uint16_t *up, int inter, int hidden,
                                const float *x1, const float *o, const uint16_t *gain, float eps, float *x_out,

@@ -39,7 +39,19 @@ struct GemvArgs {
     float *x_out;          // where the summed input is kept (kNormSum), or null
     float *out;            // kStore: out[r]; kSiluPairs: out[j] for rows (j, j + n_rows/2); kLogits: logits
     uint64_t *argmax;      // kLogits: per-block (key, inverted index) maxima
+    // kStore with outs[0] set: the rows of matrix i of `rows` go to outs[i]
+    // (q, k and v in buffers of their own) instead of out.
+    float *outs[3];
 };
+
+// Where kStore writes row r.
+__device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
+    if (!a.outs[0]) return a.out + r;
+    if (r < a.rows.count[0]) return a.outs[0] + r;
+    r -= a.rows.count[0];
+    if (r < a.rows.count[1]) return a.outs[1] + r;
+    return a.outs[2] + (r - a.rows.count[1]);
+}
 
 // One block: RPW rows per wave, CPL 16-byte chunks per lane per row.
 template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
@@ -78,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         if (lane < RPW) {
 #pragma unroll
             for (int r = 0; r < RPW; ++r)
-                if (lane == r && r0 + r < a.n_rows) a.out[r0 + r] = res[r];
+                if (lane == r && r0 + r < a.n_rows) *store_at(a, r0 + r) = res[r];
         }
     } else if (EPI == kSiluPairs) {
         // Rows r0 + 2i and r0 + 2i + 1 of the wave are gate j and up j.
@@ -538,6 +550,39 @@ hipError_t launch_step_gemv(hipStream_t s, const uint16_t *w, int rows, int cols
     a.a = x;
     a.out = out;
     return gemv_dispatch<1, kPlain, kStore>(s, a);
+}
+
+bool step_gemv_supported(int cols) {
+    const int cpl = cols / 512;
+    return cols > 0 && cols % 512 == 0 && (cpl <= 6 || cpl == 8 || cpl == 19);
+}
+
+hipError_t launch_step_gemv3(hipStream_t s, const uint16_t *const w[3], const int rows[3], int cols, const float *x,
+                             float *const out[3]) {
+    GemvArgs a{};
+    for (int i = 0; i < 3; ++i) {
+        a.rows.base[i] = w[i];
+        a.rows.count[i] = rows[i];
+        a.outs[i] = out[i];
+        a.n_rows += rows[i];
+    }
+    a.cols = cols;
+    a.a = x;
+    return gemv_dispatch<2, kPlain, kStore>(s, a);
+}
+
+hipError_t launch_step_silu(hipStream_t s, const uint16_t *gate, const uint16_t *up, int inter, int cols,
+                            const float *x, float *h) {
+    GemvArgs a{};
+    a.rows.base[0] = gate;
+    a.rows.count[0] = inter;
+    a.rows.base[1] = up;
+    a.rows.count[1] = inter;
+    a.n_rows = 2 * inter;
+    a.cols = cols;
+    a.a = x;
+    a.out = h;
+    return gemv_dispatch<2, kPlain, kSiluPairs>(s, a);
 }
 
 hipError_t launch_step_gate_up(hipStream_t s, const uint16_t *gate, const uint16_t *up, int inter, int hidden,

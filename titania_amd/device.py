@@ -219,6 +219,22 @@ class Hip:
         check(lib().th_add_rmsnorm(self.handle, x.handle, y.handle if y is not None else None, xb.handle,
                                    weight.handle, float(eps)))
 
+    def qkv_rope_append(self, q: Buffer, k: Buffer, v: Buffer, wq: Weight, wk: Weight, wv: Weight,
+                        q_norm: Weight | None, k_norm: Weight | None, xb: Buffer, rope: Buffer, k_cache: Buffer,
+                        v_cache: Buffer, pos: int, n_heads: int, n_kv_heads: int, head_dim: int, eps: float) -> None:
+        """model.rs:108-120 in one call: the q/k/v projections of xb, the
+        per-head norms, the rotations and the appends to position-major
+        caches (k and v are left holding the raw projections)."""
+        check(lib().th_qkv_rope_append(self.handle, q.handle, k.handle, v.handle, wq.handle, wk.handle, wv.handle,
+                                       q_norm.handle if q_norm is not None else None,
+                                       k_norm.handle if k_norm is not None else None, xb.handle, rope.handle,
+                                       k_cache.handle, v_cache.handle, int(pos), int(n_heads), int(n_kv_heads),
+                                       int(head_dim), float(eps)))
+
+    def gate_up_silu(self, gate: Buffer, up: Buffer, w_gate: Weight, w_up: Weight, xb: Buffer) -> None:
+        """gate = silu(w_gate . xb) * (w_up . xb) (model.rs:137-139); up is scratch."""
+        check(lib().th_gate_up_silu(self.handle, gate.handle, up.handle, w_gate.handle, w_up.handle, xb.handle))
+
     def argmax(self, logits: Buffer) -> int:
         tok = C.c_uint32()
         check(lib().th_argmax(self.handle, logits.handle, C.byref(tok)))

@@ -9,7 +9,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, ThConfig, check, lib
+from ._lib import TH_KV_BF16, TH_KV_F32, TH_PATH_FUSED, TH_PATH_OPS, TH_PATH_TRAIT, ThConfig, check, lib
 from .config import Config
 from .device import Hip, Tensor, Weight
 from .synth import layer_names
@@ -139,4 +139,5 @@ def generate(model: Model, state: State, prompt, steps: int, keep_logits: bool =
     return model.decode(state, len(prompt), steps, keep_logits)
 
 
-__all__ = ["Model", "State", "generate", "BATCH", "TH_PATH_OPS", "TH_PATH_FUSED", "TH_KV_F32", "TH_KV_BF16"]
+__all__ = ["Model", "State", "generate", "BATCH", "TH_PATH_OPS", "TH_PATH_FUSED", "TH_PATH_TRAIT", "TH_KV_F32",
+           "TH_KV_BF16"]

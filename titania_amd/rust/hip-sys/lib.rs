@@ -54,6 +54,7 @@ pub const TH_KV_F32: c_int = 0;
 pub const TH_KV_BF16: c_int = 1;
 pub const TH_PATH_OPS: c_int = 0;
 pub const TH_PATH_FUSED: c_int = 1;
+pub const TH_PATH_TRAIT: c_int = 2;
 
 unsafe extern "C" {
     pub fn th_last_error() -> *const c_char;
@@ -102,6 +103,13 @@ unsafe extern "C" {
     // Fused extensions.
     pub fn th_add_rmsnorm(dev: *mut th_device, x: *mut th_buffer, y: *const th_buffer, xb: *mut th_buffer,
                           weight: *const th_weight, eps: f32) -> c_int;
+    pub fn th_qkv_rope_append(dev: *mut th_device, q: *mut th_buffer, k: *mut th_buffer, v: *mut th_buffer,
+                              wq: *const th_weight, wk: *const th_weight, wv: *const th_weight,
+                              q_norm: *const th_weight, k_norm: *const th_weight, xb: *const th_buffer,
+                              rope: *const th_buffer, k_cache: *mut th_buffer, v_cache: *mut th_buffer, pos: usize,
+                              n_heads: usize, n_kv_heads: usize, head_dim: usize, eps: f32) -> c_int;
+    pub fn th_gate_up_silu(dev: *mut th_device, gate: *mut th_buffer, up: *mut th_buffer, w_gate: *const th_weight,
+                           w_up: *const th_weight, xb: *const th_buffer) -> c_int;
     pub fn th_argmax(dev: *mut th_device, logits: *const th_buffer, token: *mut u32) -> c_int;
     pub fn th_sample(dev: *mut th_device, logits: *const th_buffer, temperature: f32, top_k: usize, top_p: f32,
                      rng: *mut u64, token: *mut u32) -> c_int;

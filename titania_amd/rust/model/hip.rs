@@ -1,16 +1,27 @@
 //! The hip device: model/device.rs's `Device` trait on an MI355X (gfx950)
 //! through the C ABI of include/titania_hip.h (the titania-hip-sys crate).
 //!
-//! Added to the reference's model crate as `mod hip; pub use hip::{Hip,
-//! HipModel};` with `titania-hip-sys` as a dependency. The trait is infallible
-//! by signature and panics on misuse (model/cpu.rs:22,40,52-53), so every
-//! non-zero status panics with the library's message; handles are freed on
-//! drop, which the trait leaves to the buffer and weight types. Not compiled
-//! in this repository's image (no Rust toolchain); tests/test_abi.py checks
-//! the crate's declarations against the header.
+//! Added to the reference's model crate by titania_amd/rust/patches/
+//! (model-lib.rs.patch: `mod hip; pub use hip::{Hip, HipModel};`,
+//! model-Cargo.toml.patch: the titania-hip-sys dependency). The trait is
+//! infallible by signature and panics on misuse (model/cpu.rs:22,40,52-53),
+//! so every non-zero status panics with the library's message. Beside the
+//! thirteen primitives, the fused methods of the trait extension
+//! (model-device.rs.patch: add_rmsnorm, qkv_rope_append, gate_up_silu,
+//! argmax) are overridden with the library's fused entry points, which the
+//! patched forward_batch calls (model-model.rs.patch).
+//!
+//! Lifetimes: every buffer, weight and model holds a reference-counted
+//! handle of its device, so the device is destroyed only after the last of
+//! them is freed, whatever order the owner drops them in (`Model<D>`
+//! declares `device` before its weights, model/model.rs:11-19, and a
+//! `State<Hip>` may outlive its model). Not compiled in this repository's
+//! image (no Rust toolchain); tests/test_abi.py checks the crate's
+//! declarations against the header and these overrides against the patch.
 
 use std::ffi::{CStr, CString};
 use std::path::Path;
+use std::rc::Rc;
 
 use titania_hip_sys as sys;
 
@@ -23,20 +34,29 @@ fn check(rc: i32) {
     }
 }
 
+/// The library's device handle, destroyed when the last owner drops it.
+struct DeviceHandle(*mut sys::th_device);
+
+impl Drop for DeviceHandle {
+    fn drop(&mut self) {
+        unsafe { sys::th_device_destroy(self.0) }
+    }
+}
+
 /// One GPU and the stream its work runs on (model/device.rs:9).
 pub struct Hip {
-    dev: *mut sys::th_device,
+    dev: Rc<DeviceHandle>,
 }
 
 /// `Device::Buffer`: f32 activations in HBM.
 pub struct HipBuffer {
-    dev: *mut sys::th_device,
+    dev: Rc<DeviceHandle>,
     ptr: *mut sys::th_buffer,
 }
 
 /// `Device::Weight`: a bf16 tensor in HBM, uploaded once.
 pub struct HipWeight {
-    dev: *mut sys::th_device,
+    dev: Rc<DeviceHandle>,
     ptr: *mut sys::th_weight,
 }
 
@@ -45,25 +65,23 @@ impl Hip {
     pub fn new(ordinal: i32) -> Hip {
         let mut dev = std::ptr::null_mut();
         check(unsafe { sys::th_device_create(ordinal, &mut dev) });
-        Hip { dev }
+        Hip { dev: Rc::new(DeviceHandle(dev)) }
     }
-}
 
-impl Drop for Hip {
-    fn drop(&mut self) {
-        unsafe { sys::th_device_destroy(self.dev) }
+    fn raw(&self) -> *mut sys::th_device {
+        self.dev.0
     }
 }
 
 impl Drop for HipBuffer {
     fn drop(&mut self) {
-        unsafe { sys::th_buffer_free(self.dev, self.ptr) }
+        unsafe { sys::th_buffer_free(self.dev.0, self.ptr) }
     }
 }
 
 impl Drop for HipWeight {
     fn drop(&mut self) {
-        unsafe { sys::th_weight_free(self.dev, self.ptr) }
+        unsafe { sys::th_weight_free(self.dev.0, self.ptr) }
     }
 }
 
@@ -74,54 +92,54 @@ impl Device for Hip {
     fn upload(&self, tensor: Tensor) -> HipWeight {
         let mut ptr = std::ptr::null_mut();
         check(unsafe {
-            sys::th_upload(self.dev, tensor.data.as_ptr(), tensor.shape.as_ptr(), tensor.shape.len(), &mut ptr)
+            sys::th_upload(self.raw(), tensor.data.as_ptr(), tensor.shape.as_ptr(), tensor.shape.len(), &mut ptr)
         });
-        HipWeight { dev: self.dev, ptr }
+        HipWeight { dev: Rc::clone(&self.dev), ptr }
     }
 
     fn alloc(&self, len: usize) -> HipBuffer {
         let mut ptr = std::ptr::null_mut();
-        check(unsafe { sys::th_alloc(self.dev, len, &mut ptr) });
-        HipBuffer { dev: self.dev, ptr }
+        check(unsafe { sys::th_alloc(self.raw(), len, &mut ptr) });
+        HipBuffer { dev: Rc::clone(&self.dev), ptr }
     }
 
     fn resize(&self, buf: &mut HipBuffer, len: usize) {
-        check(unsafe { sys::th_resize(self.dev, buf.ptr, len) })
+        check(unsafe { sys::th_resize(self.raw(), buf.ptr, len) })
     }
 
     fn read(&self, buf: &HipBuffer) -> Vec<f32> {
         let len = unsafe { sys::th_buffer_len(buf.ptr) };
         let mut out = vec![0.0f32; len];
-        check(unsafe { sys::th_read(self.dev, buf.ptr, out.as_mut_ptr(), len) });
+        check(unsafe { sys::th_read(self.raw(), buf.ptr, out.as_mut_ptr(), len) });
         out
     }
 
     fn write(&self, buf: &mut HipBuffer, data: &[f32]) {
-        check(unsafe { sys::th_write(self.dev, buf.ptr, data.as_ptr(), data.len()) })
+        check(unsafe { sys::th_write(self.raw(), buf.ptr, data.as_ptr(), data.len()) })
     }
 
     fn copy(&self, dst: &mut HipBuffer, dst_offset: usize, src: &HipBuffer, src_offset: usize, len: usize) {
-        check(unsafe { sys::th_copy(self.dev, dst.ptr, dst_offset, src.ptr, src_offset, len) })
+        check(unsafe { sys::th_copy(self.raw(), dst.ptr, dst_offset, src.ptr, src_offset, len) })
     }
 
     fn embed(&self, out: &mut HipBuffer, table: &HipWeight, tokens: &[u32]) {
-        check(unsafe { sys::th_embed(self.dev, out.ptr, table.ptr, tokens.as_ptr(), tokens.len()) })
+        check(unsafe { sys::th_embed(self.raw(), out.ptr, table.ptr, tokens.as_ptr(), tokens.len()) })
     }
 
     fn matmul(&self, out: &mut HipBuffer, w: &HipWeight, x: &HipBuffer) {
-        check(unsafe { sys::th_matmul(self.dev, out.ptr, w.ptr, x.ptr) })
+        check(unsafe { sys::th_matmul(self.raw(), out.ptr, w.ptr, x.ptr) })
     }
 
     fn add(&self, x: &mut HipBuffer, y: &HipBuffer) {
-        check(unsafe { sys::th_add(self.dev, x.ptr, y.ptr) })
+        check(unsafe { sys::th_add(self.raw(), x.ptr, y.ptr) })
     }
 
     fn rmsnorm(&self, x: &mut HipBuffer, weight: &HipWeight, eps: f32) {
-        check(unsafe { sys::th_rmsnorm(self.dev, x.ptr, weight.ptr, eps) })
+        check(unsafe { sys::th_rmsnorm(self.raw(), x.ptr, weight.ptr, eps) })
     }
 
     fn rope(&self, x: &mut HipBuffer, table: &HipBuffer, pos: usize, n_heads: usize, head_dim: usize) {
-        check(unsafe { sys::th_rope(self.dev, x.ptr, table.ptr, pos, n_heads, head_dim) })
+        check(unsafe { sys::th_rope(self.raw(), x.ptr, table.ptr, pos, n_heads, head_dim) })
     }
 
     fn attention(
@@ -136,12 +154,62 @@ impl Device for Hip {
         n_kv_heads: usize,
     ) {
         check(unsafe {
-            sys::th_attention(self.dev, out.ptr, q.ptr, k_cache.ptr, v_cache.ptr, pos, n_heads, head_dim, n_kv_heads)
+            sys::th_attention(self.raw(), out.ptr, q.ptr, k_cache.ptr, v_cache.ptr, pos, n_heads, head_dim,
+                              n_kv_heads)
         })
     }
 
     fn silu_mul(&self, gate: &mut HipBuffer, up: &HipBuffer) {
-        check(unsafe { sys::th_silu_mul(self.dev, gate.ptr, up.ptr) })
+        check(unsafe { sys::th_silu_mul(self.raw(), gate.ptr, up.ptr) })
+    }
+
+    // ---- the trait extension's fused methods ----
+
+    fn add_rmsnorm(&self, x: &mut HipBuffer, xb: &mut HipBuffer, add: bool, weight: &HipWeight, eps: f32,
+                   len: usize) {
+        assert_eq!(unsafe { sys::th_buffer_len(x.ptr) }, len, "add_rmsnorm over all of x");
+        // The residual is read from xb before xb is overwritten, row by row.
+        let y = if add { xb.ptr as *const sys::th_buffer } else { std::ptr::null() };
+        check(unsafe { sys::th_add_rmsnorm(self.raw(), x.ptr, y, xb.ptr, weight.ptr, eps) })
+    }
+
+    fn qkv_rope_append(
+        &self,
+        q: &mut HipBuffer,
+        k: &mut HipBuffer,
+        v: &mut HipBuffer,
+        w: [&HipWeight; 3],
+        q_norm: Option<&HipWeight>,
+        k_norm: Option<&HipWeight>,
+        xb: &HipBuffer,
+        rope: &HipBuffer,
+        k_cache: &mut HipBuffer,
+        v_cache: &mut HipBuffer,
+        pos: usize,
+        n: usize,
+        n_heads: usize,
+        n_kv_heads: usize,
+        head_dim: usize,
+        eps: f32,
+    ) {
+        assert_eq!(unsafe { sys::th_buffer_len(q.ptr) }, n * n_heads * head_dim, "q holds the n tokens");
+        let qn = q_norm.map_or(std::ptr::null(), |g| g.ptr as *const sys::th_weight);
+        let kn = k_norm.map_or(std::ptr::null(), |g| g.ptr as *const sys::th_weight);
+        check(unsafe {
+            sys::th_qkv_rope_append(self.raw(), q.ptr, k.ptr, v.ptr, w[0].ptr, w[1].ptr, w[2].ptr, qn, kn, xb.ptr,
+                                    rope.ptr, k_cache.ptr, v_cache.ptr, pos, n_heads, n_kv_heads, head_dim, eps)
+        })
+    }
+
+    fn gate_up_silu(&self, gate: &mut HipBuffer, up: &mut HipBuffer, w_gate: &HipWeight, w_up: &HipWeight,
+                    xb: &HipBuffer) {
+        check(unsafe { sys::th_gate_up_silu(self.raw(), gate.ptr, up.ptr, w_gate.ptr, w_up.ptr, xb.ptr) })
+    }
+
+    fn argmax(&self, logits: &HipBuffer) -> u32 {
+        let mut token = 0u32;
+        check(unsafe { sys::th_argmax(self.raw(), logits.ptr, &mut token) });
+        token
     }
 }
 
@@ -153,6 +221,8 @@ pub struct HipModel {
     model: *mut sys::th_model,
     state: *mut sys::th_state,
     vocab: usize,
+    // Dropped after Drop::drop has destroyed the state and the model.
+    _dev: Rc<DeviceHandle>,
 }
 
 impl HipModel {
@@ -161,12 +231,12 @@ impl HipModel {
     pub fn load(hip: &Hip, dir: &Path, max_len: usize) -> HipModel {
         let dir = CString::new(dir.to_string_lossy().as_bytes()).expect("path with a NUL byte");
         let mut model = std::ptr::null_mut();
-        check(unsafe { sys::th_model_load(hip.dev, dir.as_ptr(), &mut model) });
+        check(unsafe { sys::th_model_load(hip.raw(), dir.as_ptr(), &mut model) });
         let mut config = sys::th_config::default();
         check(unsafe { sys::th_model_config(model, &mut config) });
         let mut state = std::ptr::null_mut();
         check(unsafe { sys::th_state_create(model, max_len, sys::TH_KV_F32, &mut state) });
-        HipModel { model, state, vocab: config.vocab_size as usize }
+        HipModel { model, state, vocab: config.vocab_size as usize, _dev: Rc::clone(&hip.dev) }
     }
 
     /// model/model.rs:83-91 `Model::forward`: the logits after `tokens`, the
