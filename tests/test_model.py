@@ -335,6 +335,49 @@ def test_qwen4b_bf16_cache_drift(qwen4b):
     b.close()
 
 
+@pytest.mark.slow
+def test_qwen4b_8k_256_steps_against_oracle(hip):
+    """The Qwen3-4B-shaped workload at full size (36 layers, an 8192-token
+    prompt, 256 greedy steps, f32 caches) against the oracle's run of it,
+    stored by tests/golden/make_qwen4b_8k.py: the fused prefill's logits,
+    the captured decode's token stream, and its logits after the 128th and
+    the 256th fed token, all within the 2e-2 logits bar. The streams must be
+    identical, unless they part at a step whose oracle top-2 gap is below
+    twice the largest logits error measured before it (a near tie that the
+    device's rounding may break either way); the comparison stops there."""
+    import json
+
+    from titania_amd import QWEN3_4B
+    from util import GOLDEN
+
+    f = np.load(GOLDEN / "qwen4b_8k_greedy256.npz")
+    meta = json.loads(str(f["meta"]))
+    n, steps, mid = meta["n_prompt"], meta["steps"], meta["mid"]
+    cfg = QWEN3_4B
+    m = Model(hip, cfg, synth.weights(cfg, seed=meta["seed"]))
+    prompt = synth.prompt(n, cfg.vocab_size, seed=meta["prompt_seed"])
+    st = State(m, n + steps, TH_KV_F32)
+    got = m.forward(st, prompt, 0, TH_PATH_FUSED)
+    toks, logits = m.decode(st, n, steps, keep_logits=True)
+    st.close()
+    m.close()
+    errs = [float(np.max(np.abs(got - f["logits_prompt"])))]
+    want, gaps = f["tokens"], f["gaps"]
+    diverged = next((i for i in range(steps) if int(toks[i]) != int(want[i])), None)
+    # logits[i] follows the token fed at step i: the fixture's mid logits
+    # follow token mid - 1, its last logits the last token.
+    for i, key in ((mid - 1, "logits_mid"), (steps - 1, "logits_last")):
+        if diverged is None or i < diverged:
+            errs.append(float(np.max(np.abs(logits[i] - f[key]))))
+    print(f"qwen3-4b 8192+256: logits max |d| {['%.2e' % e for e in errs]}; first divergence {diverged}; "
+          f"smallest top-2 gap {float(gaps.min()):.2e}")
+    assert float(np.std(f["logits_prompt"])) > 0.3 and len(set(want.tolist())) > 100, "a run that pins little"
+    assert max(errs) <= LOGIT_TOL
+    if diverged is not None:
+        assert float(gaps[diverged]) < 2 * max(errs), (diverged, float(gaps[diverged]), errs)
+        assert diverged >= mid, "the comparison must cover at least the first half"
+
+
 # ---- sampled decode (model/chat.rs:149-178 with model/sampler.rs) ----
 
 @pytest.mark.parametrize("t,k,p,n_prompt", [(0.7, 20, 0.8, 12), (1.5, 256, 1.0, 12), (0.9, 40, 0.9, 12),

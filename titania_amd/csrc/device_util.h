@@ -144,6 +144,19 @@ __device__ __forceinline__ float rows_max(float v) {
     auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
+// rows_max for values that are never NaN: a plain v_max_f32 (fmaxf brings
+// a NaN canonicalization of each input with it).
+__device__ __forceinline__ float max_nn(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+__device__ __forceinline__ float rows_max_nn(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = max_nn(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return max_nn(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
 __device__ __forceinline__ float rows_sum(float v) {
     auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     v = __uint_as_float(p[0]) + __uint_as_float(p[1]);

@@ -287,8 +287,10 @@ int ensure_fused_state(th_state *s) {
     TH_HIP(hipMalloc(&s->kv, kv_bytes + (size_t)th::kStepKvTailRows * hd * sizeof(float)));
     // Attention partials: enough for any chunk of up to fb tokens at any context
     // up to max_len (the split count only grows with the context).
-    s->attn_part_floats = th::attention_scratch(1, (size_t)c.num_attention_heads, hd,
-                                                th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16));
+    const int step_splits = th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16,
+                                                      (int)(c.num_attention_heads / c.num_key_value_heads),
+                                                      (int)c.num_key_value_heads, m->dev->num_cus);
+    s->attn_part_floats = th::attention_scratch(1, (size_t)c.num_attention_heads, hd, step_splits);
     for (size_t n = 1; n <= s->fb; ++n) {
         int ns = th::attention_splits(n, (size_t)c.num_attention_heads, (size_t)c.num_key_value_heads, s->max_len, hd);
         s->attn_part_floats =
@@ -352,7 +354,8 @@ int enqueue_step(th_state *s) {
     const int qd = nh * hd, kvd = nkv * hd, V = (int)c.vocab_size;
     const float eps = c.rms_norm_eps;
     const int chunks = th::step_qkv_attn_chunks(s->max_len, s->kv_dtype == TH_KV_BF16, (int)nh);
-    const int nsplit = th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16);
+    const int nsplit = th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16, nh / nkv, nkv,
+                                                 m->dev->num_cus);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
     // One launch for q/k/v and attention while one split covers the context.

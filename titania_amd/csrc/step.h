@@ -71,9 +71,13 @@ struct StepAttnArgs {
 };
 
 // Splits of the context launch_step_attention wants for caches of max_len
-// positions: one up to 512, else one per register pass of rows (128 bf16 or
-// 64 f32 positions), at most 256.
-int step_attention_splits(size_t max_len, int kv_bf16);
+// positions, `group` q heads a KV head, on a GPU of num_cus compute units:
+// one up to 512 positions, else as many as fill the chip's block slots in
+// one round, in whole passes of its blocks (32 f32 / 64 bf16 positions), at
+// most 256.
+int step_attention_splits(size_t max_len, int kv_bf16, int group, int n_kv_heads, int num_cus);
+// Positions a split covers: max_len / nsplit rounded up to whole passes.
+long long step_attention_chunk(size_t max_len, int kv_bf16, int nsplit);
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a);
 
 // The q/k/v GEMV (as launch_step_qkv) and the attention in one launch: the

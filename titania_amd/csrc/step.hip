@@ -149,256 +149,6 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs &a) {
     }
 }
 
-// ---- attention for one token: q/k RMSNorm + RoPE + KV append + split attention ----
-
-constexpr int kStageRows = 64;  // cached positions staged in LDS per pass
-
-__device__ __forceinline__ void dma16(const void *src, void *wave_base) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)wave_base, 16, 0, 0);
-}
-
-__device__ __forceinline__ float lds_at(const float *row, int d) { return row[d]; }
-__device__ __forceinline__ float lds_at(const uint16_t *row, int d) { return bf16_to_f32(row[d]); }
-
-// Attention of one (KV head g, split of the positions 0..pos) by one block:
-// the group's q heads and the new k are RMSNorm'd and rotated in LDS, the split
-// holding pos appends k and v to the caches, and cached K/V rows are staged
-// into LDS 64 positions at a time (all loads of a pass in flight together) for
-// scores, online softmax and the weighted sum of values.
-//
-// The raw q/k/v come from a.qkv, or (WORDS) from (value | epoch << 32) words
-// that other blocks of the same launch are writing: then the block first
-// stages the cached rows (they do not depend on the q/k/v), then polls until
-// every word it needs carries `epoch` (bounded: about 2 s, then *err counts
-// the failure and the block goes on with what it has).
-template <int HD, int G, typename KV, bool WORDS, int ROWS>
-__device__ __forceinline__ void attend(const StepAttnArgs &a, int g, int split, const unsigned long long *words,
-                                       unsigned epoch, unsigned *err) {
-    constexpr int LPK = HD / 8, KPW = 64 / LPK, KPB = kWaves * KPW, NP = kThreads / HD;
-    static_assert(LPK == 16, "one key per 16-lane row");
-    constexpr int ROW16 = HD * (int)sizeof(KV) / 16;  // 16-byte chunks per cached row
-    __shared__ float hq[G * HD], hk[HD], hv[HD];
-    __shared__ float scores[G][ROWS];
-    __shared__ float st_m[G], st_l[G], st_a[G];
-    __shared__ float red[G][kThreads];
-    __shared__ uint4 kst[ROWS * ROW16], vst[ROWS * ROW16];
-    static_assert(HD == 128, "one rotation pair per lane");
-    constexpr int HALF = HD / 2, HPW = (G + 1 + kWaves - 1) / kWaves;  // heads (q..., k) per wave
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % LPK;
-    const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
-    const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
-    const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
-    auto stage = [&](long long c0, int rows) {
-        const int chunks = rows * ROW16;
-        const uint4 *ks = reinterpret_cast<const uint4 *>(kc + c0 * HD);
-        const uint4 *vs = reinterpret_cast<const uint4 *>(vc + c0 * HD);
-        for (int base = wave * 64; base < chunks; base += kThreads)
-            if (base + lane < chunks) {
-                dma16(ks + base + lane, kst + base);
-                dma16(vs + base + lane, vst + base);
-            }
-    };
-    // The raw q heads and k of this wave (lane holds the pair (lane, lane +
-    // HD/2)), their RMSNorm gains and this thread's element of v; from a.qkv
-    // they are requested first, with everything else that does not depend on
-    // the position.
-    float av[HPW], bv[HPW], ga[HPW], gb[HPW];
-    float vnew = 0.f;
-#pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-        const int h = wave + hh * kWaves;
-        av[hh] = bv[hh] = 0.f;
-        ga[hh] = gb[hh] = 1.f;
-        if (h <= G) {
-            const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
-            if (gain) {
-                ga[hh] = bf16_to_f32(gain[lane]);
-                gb[hh] = bf16_to_f32(gain[lane + HALF]);
-            }
-            if (!WORDS) {
-                const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
-                av[hh] = x[lane];
-                bv[hh] = x[lane + HALF];
-            }
-        }
-    }
-    if (!WORDS && tid < HD) vnew = a.qkv[qd + kvd + (size_t)g * HD + tid];
-    const long long pos = *a.pos;
-    const long long len = pos + 1;
-    const long long chunk = ((len + a.nsplit - 1) / a.nsplit + 15) / 16 * 16;
-    const long long s0 = (long long)split * chunk;
-    const long long s1 = s0 + chunk < len ? s0 + chunk : len;
-    auto cached_in = [&](long long c0, int cnt) -> int {
-        const long long nc = pos - c0;
-        return nc <= 0 ? 0 : (nc < cnt ? (int)nc : cnt);
-    };
-    // Then, once pos is known, the rotation of this position and the first
-    // pass's cached rows: one more memory round trip.
-    const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
-    {
-        const int cnt0 = (int)(s1 - s0 < ROWS ? s1 - s0 : ROWS);
-        if (s0 < s1) stage(s0, cached_in(s0, cnt0));
-    }
-    if (WORDS) {
-        for (int it = 0;; ++it) {
-            int ok = 1;
-            unsigned long long wa[HPW], wb[HPW], wv = 0;
-#pragma unroll
-            for (int hh = 0; hh < HPW; ++hh) {
-                const int h = wave + hh * kWaves;
-                if (h <= G) {
-                    const unsigned long long *x = h < G ? words + (size_t)(g * G + h) * HD : words + qd + (size_t)g * HD;
-                    wa[hh] = __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    wb[hh] = __hip_atomic_load(x + lane + HALF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            if (tid < HD)
-                wv = __hip_atomic_load(words + qd + kvd + (size_t)g * HD + tid, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-            for (int hh = 0; hh < HPW; ++hh) {
-                const int h = wave + hh * kWaves;
-                if (h <= G) {
-                    ok &= (unsigned)(wa[hh] >> 32) == epoch && (unsigned)(wb[hh] >> 32) == epoch;
-                    av[hh] = __uint_as_float((unsigned)wa[hh]);
-                    bv[hh] = __uint_as_float((unsigned)wb[hh]);
-                }
-            }
-            if (tid < HD) {
-                ok &= (unsigned)(wv >> 32) == epoch;
-                vnew = __uint_as_float((unsigned)wv);
-            }
-            if (__syncthreads_and(ok)) break;
-            if (it >= (1 << 21)) {
-                if (tid == 0) atomicAdd(err, 1u);
-                break;
-            }
-        }
-    }
-    if (tid < G) {
-        st_m[tid] = -INFINITY;
-        st_l[tid] = 0.f;
-    }
-    if (tid < HD) hv[tid] = vnew;
-    // RMSNorm (model.rs:111-116) + RoPE (model.rs:117-118) per head, in registers.
-#pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-        const int h = wave + hh * kWaves;
-        if (h > G) continue;
-        float x0 = av[hh], x1 = bv[hh];
-        if (h < G ? a.q_norm != nullptr : a.k_norm != nullptr) {
-            const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
-            const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
-            x0 = x0 * (sc * ga[hh]);
-            x1 = x1 * (sc * gb[hh]);
-        }
-        float *x = h < G ? hq + h * HD : hk;
-        x[lane] = x0 * cs.x - x1 * cs.y;
-        x[lane + HALF] = x1 * cs.x + x0 * cs.y;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    float qf[G][8];
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qf[gg][i] = hq[gg * HD + sub * 8 + i];
-    const float scale = 1.0f / sqrtf((float)HD);
-    const int d = tid % HD, pt = tid / HD;
-    const KV *ks_l = reinterpret_cast<const KV *>(kst), *vs_l = reinterpret_cast<const KV *>(vst);
-    float acc[G];
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) acc[gg] = 0.f;
-    for (long long c0 = s0; c0 < s1; c0 += ROWS) {
-        const int cnt = (int)(s1 - c0 < ROWS ? s1 - c0 : ROWS);
-        const int ncache = cached_in(c0, cnt);
-        if (c0 != s0) {
-            stage(c0, ncache);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-        }
-        for (int j0 = 0; j0 < cnt; j0 += KPB) {
-            const int j = j0 + wave * KPW + lane / LPK;
-            float kf[8];
-            if (j < ncache) {
-                lds_row8(ks_l + j * HD, sub, kf);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) kf[i] = j < cnt ? hk[sub * 8 + i] : 0.f;
-            }
-#pragma unroll
-            for (int gg = 0; gg < G; ++gg) {
-                float sc = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) sc = fmaf(qf[gg][i], kf[i], sc);
-                sc = row_sum_dpp(sc);
-                if (j < cnt && sub == 0) scores[gg][j] = scale * sc;
-            }
-        }
-        __syncthreads();
-        for (int gg = wave; gg < G; gg += kWaves) {
-            float m = -INFINITY;
-            for (int j = lane; j < cnt; j += 64) m = fmaxf(m, scores[gg][j]);
-            m = wave_max_dpp(m);
-            const float m_old = st_m[gg], m_new = fmaxf(m_old, m);
-            float l = 0.f;
-            for (int j = lane; j < cnt; j += 64) {
-                const float e = expf(scores[gg][j] - m_new);
-                scores[gg][j] = e;
-                l += e;
-            }
-            l = wave_sum_dpp(l);
-            if (lane == 0) {
-                const float al = expf(m_old - m_new);
-                st_a[gg] = al;
-                st_l[gg] = st_l[gg] * al + l;
-                st_m[gg] = m_new;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int gg = 0; gg < G; ++gg) acc[gg] *= st_a[gg];
-        for (int j = pt; j < cnt; j += NP) {
-            const float v = j < ncache ? lds_at(vs_l + j * HD, d) : hv[d];
-#pragma unroll
-            for (int gg = 0; gg < G; ++gg) acc[gg] = fmaf(scores[gg][j], v, acc[gg]);
-        }
-        __syncthreads();  // the stage and scores are rewritten by the next pass
-    }
-    // The split holding pos appends the new key and value (model.rs:119-120);
-    // no block of this launch reads that position from the caches.
-    if (pos >= s0 && pos < s1 && tid < HD) {
-        KV *kw = reinterpret_cast<KV *>(a.k_cache) + (size_t)g * a.head_stride + pos * HD;
-        KV *vw = reinterpret_cast<KV *>(a.v_cache) + (size_t)g * a.head_stride + pos * HD;
-        store_kv(kw + tid, hk[tid]);
-        store_kv(vw + tid, hv[tid]);
-    }
-#pragma unroll
-    for (int gg = 0; gg < G; ++gg) red[gg][tid] = acc[gg];
-    __syncthreads();
-    if (pt != 0) return;
-    for (int gg = 0; gg < G; ++gg) {
-        float sm = red[gg][d];
-        for (int q = 1; q < NP; ++q) sm += red[gg][q * HD + d];
-        const long long h = (long long)g * G + gg;
-        if (a.nsplit == 1) {
-            a.out[h * HD + d] = sm / st_l[gg];
-        } else {
-            const long long slot = h * a.nsplit + split;
-            a.part_acc[slot * HD + d] = sm;
-            if (d == 0) {
-                a.part_ml[slot * 2] = st_m[gg];
-                a.part_ml[slot * 2 + 1] = st_l[gg];
-            }
-        }
-    }
-}
-
-template <int HD, int G, typename KV>
-__global__ __launch_bounds__(kThreads) void step_attention_kernel(StepAttnArgs a) {
-    attend<HD, G, KV, false, kStageRows>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, nullptr, 0, nullptr);
-}
-
 // The q/k/v rows of launch_step_qkv (kQkvRowsPerWave per wave) published as
 // epoch words by the first blocks, and after them one block per q head and
 // chunk of the cache that attends from those words. Blocks start in index order and the GEMV blocks never wait, so
@@ -471,36 +221,31 @@ hipError_t qkv_attn_g(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a
     }
 }
 
-// One block per (KV head, split of `chunk` positions), cached rows in
-// registers; at most 168 VGPRs, so that three blocks fit on a CU.
+// Waves a SIMD the streaming attention is built for: the most that keeps its
+// two register sets of rows and its 16 G accumulators without spills (f32
+// rows: 115 / 124 / 162 / 251 VGPRs for groups of 1 / 2 / 4 / 8 q heads).
 template <int G, typename KV>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
-void step_attention_regs_kernel(StepAttnArgs a, long long chunk) {
-    const int g = blockIdx.x / a.nsplit;
-    attend_regs<G, KV, false>(a, g, g * G, true, blockIdx.x % a.nsplit, chunk, nullptr, 0, nullptr);
+constexpr int stream_waves_per_eu() {
+    return G <= 2 ? 4 : G == 4 ? 3 : 2;
+}
+
+// One block per (KV head, split of `chunk` positions), the rows streamed
+// through registers in double-buffered passes.
+template <int G, typename KV>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<G, KV>())))
+void step_attention_stream_kernel(StepAttnArgs a, long long chunk) {
+    attend_stream<G, KV, false>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, chunk, nullptr, 0, nullptr);
 }
 
 template <int G>
-hipError_t attn_regs_launch(hipStream_t s, const StepAttnArgs &a) {
+hipError_t attn_stream_launch(hipStream_t s, const StepAttnArgs &a) {
     const long long max_len = a.head_stride / 128;
-    const int rows = a.kv_bf16 ? KvRegs<uint16_t>::kRows : KvRegs<float>::kRows;
-    long long chunk = (max_len + a.nsplit - 1) / a.nsplit;
-    chunk = (chunk + rows - 1) / rows * rows;
+    const long long chunk = step_attention_chunk((size_t)max_len, a.kv_bf16, a.nsplit);
     dim3 grid((unsigned)(a.n_kv_heads * a.nsplit));
     if (a.kv_bf16)
-        step_attention_regs_kernel<G, uint16_t><<<grid, kThreads, 0, s>>>(a, chunk);
+        step_attention_stream_kernel<G, uint16_t><<<grid, kThreads, 0, s>>>(a, chunk);
     else
-        step_attention_regs_kernel<G, float><<<grid, kThreads, 0, s>>>(a, chunk);
-    return hipGetLastError();
-}
-
-template <int HD, int G>
-hipError_t attn_launch(hipStream_t s, const StepAttnArgs &a) {
-    dim3 grid((unsigned)(a.n_kv_heads * a.nsplit));
-    if (a.kv_bf16)
-        step_attention_kernel<HD, G, uint16_t><<<grid, kThreads, 0, s>>>(a);
-    else
-        step_attention_kernel<HD, G, float><<<grid, kThreads, 0, s>>>(a);
+        step_attention_stream_kernel<G, float><<<grid, kThreads, 0, s>>>(a, chunk);
     return hipGetLastError();
 }
 
@@ -671,18 +416,41 @@ hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
     }
 }
 
-int step_attention_splits(size_t max_len, int kv_bf16) {
-    if (max_len <= 512) return 1;
-    const size_t rows = kv_bf16 ? KvRegs<uint16_t>::kRows : KvRegs<float>::kRows;
-    return (int)std::min<size_t>((max_len + rows - 1) / rows, 256);
+// Rows of one pass of the streaming attention's block (four waves of 8 rows).
+constexpr long long kStreamPassF32 = 32, kStreamPassBf16 = 32;
+
+long long step_attention_chunk(size_t max_len, int kv_bf16, int nsplit) {
+    const long long pass = kv_bf16 ? kStreamPassBf16 : kStreamPassF32;
+    const long long c = ((long long)max_len + nsplit - 1) / nsplit;
+    return (c + pass - 1) / pass * pass;
+}
+
+int step_attention_splits(size_t max_len, int kv_bf16, int group, int n_kv_heads, int num_cus) {
+    if (max_len <= 512 || n_kv_heads < 1) return 1;
+    // As many splits as fill the chip's block slots in one round (blocks a
+    // CU = waves a SIMD the kernel is built for), in whole passes: a second,
+    // partial round of blocks would leave most of the chip idle at its end
+    // (Qwen3-4B at 8192 positions, f32: splits of 1 / 2 / 3 / 4 / 8 passes
+    // gave 2.618 / 2.532 / 2.501 / 2.616 / 2.716 ms a step; three, 704
+    // blocks for 768 slots, filled it).
+    int per_cu;
+    switch (group) {
+    case 1: per_cu = kv_bf16 ? stream_waves_per_eu<1, uint16_t>() : stream_waves_per_eu<1, float>(); break;
+    case 2: per_cu = kv_bf16 ? stream_waves_per_eu<2, uint16_t>() : stream_waves_per_eu<2, float>(); break;
+    case 4: per_cu = kv_bf16 ? stream_waves_per_eu<4, uint16_t>() : stream_waves_per_eu<4, float>(); break;
+    default: per_cu = kv_bf16 ? stream_waves_per_eu<8, uint16_t>() : stream_waves_per_eu<8, float>(); break;
+    }
+    const long long want = std::max(1LL, (long long)std::max(num_cus, 1) * per_cu / n_kv_heads);
+    long long chunk = step_attention_chunk(max_len, kv_bf16, (int)std::min(want, 256LL));
+    return (int)(((long long)max_len + chunk - 1) / chunk);
 }
 
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a) {
     switch (a.n_heads / a.n_kv_heads) {
-    case 1: return attn_launch<128, 1>(s, a);
-    case 2: return attn_regs_launch<2>(s, a);
-    case 4: return attn_regs_launch<4>(s, a);
-    case 8: return attn_launch<128, 8>(s, a);
+    case 1: return attn_stream_launch<1>(s, a);
+    case 2: return attn_stream_launch<2>(s, a);
+    case 4: return attn_stream_launch<4>(s, a);
+    case 8: return attn_stream_launch<8>(s, a);
     default: return hipErrorInvalidValue;
     }
 }

@@ -1,5 +1,6 @@
 // Device code of the decode-step kernels: the GEMV input builder, row tables,
-// and the register-resident attention of one KV head over the whole context.
+// the fused launch's attention of one q head over one chunk of the cache, and
+// the streaming split attention of one KV head's q heads for long contexts.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -122,45 +123,15 @@ __device__ __forceinline__ const uint4 *row_at(const Rows &m, int r, int cols) {
     return reinterpret_cast<const uint4 *>(p);
 }
 
-__device__ __forceinline__ void lds_row8(const float *row, int sub, float f[8]) {
-    const float4 a = reinterpret_cast<const float4 *>(row)[sub * 2], b = reinterpret_cast<const float4 *>(row)[sub * 2 + 1];
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-}
-__device__ __forceinline__ void lds_row8(const uint16_t *row, int sub, float f[8]) {
-    unpack8(reinterpret_cast<const uint4 *>(row)[sub], f);
-}
-// Cached K/V rows held in registers: in the score pass a lane holds dims
-// [8*sub, 8*sub + 8) of its keys, in the value pass dims [4*d4, 4*d4 + 4).
+// Cached positions one attention block of the fused q/k/v + attention launch
+// takes (a register pass of rows: 64 f32 or 128 bf16, 64 KB of keys and
+// values).
 template <typename KV> struct KvRegs;
 template <> struct KvRegs<float> {
-    struct K { float4 a, b; };
-    using V = float4;
-    static constexpr int kRows = 64;  // positions per pass
-    __device__ static K load_k(const float *row, int sub) {
-        const float4 *p = reinterpret_cast<const float4 *>(row) + sub * 2;
-        return K{p[0], p[1]};
-    }
-    __device__ static void unpack_k(const K &k, float f[8]) {
-        f[0] = k.a.x; f[1] = k.a.y; f[2] = k.a.z; f[3] = k.a.w;
-        f[4] = k.b.x; f[5] = k.b.y; f[6] = k.b.z; f[7] = k.b.w;
-    }
-    __device__ static V load_v(const float *row, int d4) { return reinterpret_cast<const float4 *>(row)[d4]; }
-    __device__ static void unpack_v(const V &v, float f[4]) {
-        f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
-    }
+    static constexpr int kRows = 64;
 };
 template <> struct KvRegs<uint16_t> {
-    using K = uint4;
-    using V = uint2;
     static constexpr int kRows = 128;
-    __device__ static K load_k(const uint16_t *row, int sub) { return reinterpret_cast<const uint4 *>(row)[sub]; }
-    __device__ static void unpack_k(const K &k, float f[8]) { unpack8(k, f); }
-    __device__ static V load_v(const uint16_t *row, int d4) { return reinterpret_cast<const uint2 *>(row)[d4]; }
-    __device__ static void unpack_v(const V &v, float f[4]) {
-        f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x);
-        f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-    }
 };
 
 // The end of a chunked launch for dimension d of q head h, given this chunk's
@@ -226,80 +197,123 @@ __device__ __forceinline__ void chunk_finish(const StepAttnArgs &a, long long h,
     a.out[h * HD + d] = num / den;
 }
 
-// Attention of one KV head by one block over the positions [s0, s0 + chunk)
-// of the context, s0 = split * chunk: the whole context (split 0, chunk
-// max_len) or one split of it. The raw q/k/v come from a.qkv, or (WORDS) from
-// (value | epoch << 32) words that other blocks of the same launch write,
-// polled until they all carry `epoch` (bounded: about 2 s, then *err counts
-// the failure and the block goes on). The first pass's cached rows are
-// requested before anything else, without waiting for the position: rows past
-// the context are read and then ignored (a pass starts below max_len and the
-// caches' allocation extends kStepKvTailRows rows past the last head). Later
-// passes request their rows as soon as the previous pass has used the
-// registers. Reductions are DPP. The output goes to a.out with one split,
-// else (sum, max, denominator) partials for launch_attn_combine.
+// Cached rows of the streaming attention as 16-byte chunks: 4 f32 or 8 bf16
+// values each.
+template <typename KV> struct StreamKV;
+template <> struct StreamKV<float> {
+    static constexpr int EPC = 4;  // elements per chunk
+    __device__ static void unpack(const uint4 &k, float f[EPC]) {
+        f[0] = __uint_as_float(k.x); f[1] = __uint_as_float(k.y);
+        f[2] = __uint_as_float(k.z); f[3] = __uint_as_float(k.w);
+    }
+};
+template <> struct StreamKV<uint16_t> {
+    static constexpr int EPC = 8;
+    __device__ static void unpack(const uint4 &k, float f[EPC]) { unpack8(k, f); }
+};
+
+// Sum over the 16 lanes of each DPP row, left in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_get<0xB1>(v, 0.f);   // quad_perm [1,0,3,2]
+    v += dpp_get<0x4E>(v, 0.f);   // quad_perm [2,3,0,1]
+    v += dpp_get<0x141>(v, 0.f);  // row_half_mirror: the other quad of the half-row
+    v += dpp_get<0x140>(v, 0.f);  // row_mirror: the other half of the row
+    return v;
+}
+
+// Attention of one KV head's G q heads over the positions [s0, s0 + chunk)
+// of the context (s0 = split * chunk) by one block, for contexts past the
+// fused launch's reach. The cached rows stream through registers in passes
+// of 32 positions (8 a wave), the next pass's rows requested before the
+// current pass's arithmetic, so that every wave keeps a pass of loads in
+// flight. Each wave scores and weighs only its own rows of every pass, with
+// an online softmax of its own (no block barrier between passes); the four
+// waves merge once, at the end, into the split's (sum, max, denominator)
+// partials for launch_attn_combine, or into the output with one split.
 //
-// The block's G q heads are qh0 .. qh0 + G - 1 of KV head g (qh0 = g G unless
-// a KV head's group is spread over several blocks, of which only the one with
-// `append` writes the new key and value).
-//
-// With `xw` (chunked launches, G = 1): the block covers one chunk of the
-// context; chunks past the context return at once. When several chunks hold
-// positions, each but the first publishes its (sum, max, denominator) as
-// epoch words at xw + (qh0 * n_chunks + split) * (head_dim + 2), and the
-// first polls them and merges all, in chunk order, into a.out.
+// Layout: the 16 lanes of DPP row r (r < 4) take the wave's rows r and r + 4
+// of a pass; a lane holds 8 dims of each (its 16-byte chunks sub + 16 i of
+// the row's key and value), so that each load instruction reads whole
+// 256-byte spans of four rows. A row's dot product is summed over its 16
+// lanes with DPP (every lane gets it), and a lane weighs its own value dims
+// by its own rows' weights. A lane keeps its 8 dims of q (scaled by
+// log2(e) / sqrt(head_dim): the softmax runs in base 2) and of each head's
+// weighted sums in registers; the rows' sums merge once, at the end. The raw
+// q/k/v come from a.qkv, or (WORDS) from the (value | epoch << 32) words of
+// the same launch's GEMV blocks, polled (bounded) after the first pass's
+// rows are requested.
 template <int G, typename KV, bool WORDS>
-__device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh0, bool append, int split,
-                                            long long chunk, const unsigned long long *words, unsigned epoch,
-                                            unsigned *err, unsigned long long *xw = nullptr, int n_chunks = 1) {
-    using R = KvRegs<KV>;
-    constexpr int HD = 128, HALF = HD / 2, ROWS = R::kRows;
-    constexpr int NK = ROWS / 16;  // keys per lane in the score pass
-    constexpr int NV = ROWS / 8;   // keys per lane in the value pass
-    constexpr int HPW = (G + 1 + kWaves - 1) / kWaves;
-    static_assert(G <= kWaves, "one wave per q head in the softmax");
-    static_assert(ROWS <= kStepKvTailRows, "pass longer than the caches' tail");
+__device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int split, long long chunk,
+                                              const unsigned long long *words, unsigned epoch, unsigned *err) {
+    using T = StreamKV<KV>;
+    constexpr int HD = 128, HALF = HD / 2, LPR = 16, EPC = T::EPC;
+    constexpr int RS = 2;                   // rows a lane takes each pass
+    constexpr int RW = 4 * RS;              // rows a wave takes each pass
+    constexpr int PASS = RW * kWaves;       // rows a block takes each pass
+    constexpr int NC = HD / EPC / LPR;      // 16-byte chunks of a row a lane holds (2 f32 / 1 bf16)
+    constexpr int DL = NC * EPC;            // dims a lane holds: 8
+    constexpr int HPW = (G + 1 + kWaves - 1) / kWaves;  // heads (q..., k) a wave normalizes
+    static_assert(DL == 8 && PASS <= kStepKvTailRows, "8 dims a lane; a pass within the caches' tail");
     __shared__ float hq[G * HD], hk[HD], hv[HD];
-    __shared__ float scores[G][ROWS];
-    __shared__ float st_m[G], st_l[G], st_a[G];
-    __shared__ float red[G][kWaves][HD];
+    // Each DPP row's weighted sums, per wave, head and dim.
+    __shared__ float4 red[kWaves][4][G][HD / 4];
+    __shared__ float wm[kWaves][G], wl[kWaves][G];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sub = lane & 15, kq = wave * 4 + (lane >> 4);  // score pass: dims 8*sub.., key kq of 16
-    const int d4 = tid & 31, pv = tid >> 5;                   // value pass: dims 4*d4.., key pv of 8
+    const int sub = lane % LPR, drow = lane / LPR;
     const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
-    const long long max_len = a.head_stride / HD;
-    const long long s0 = (long long)split * chunk;
     const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
     const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
-    typename R::K kr[NK];
-    typename R::V vr[NV];
-    auto load_k = [&](long long c0) {
-#pragma unroll
-        for (int i = 0; i < NK; ++i) kr[i] = R::load_k(kc + (c0 + i * 16) * HD + kq * HD, sub);
-    };
-    auto load_v = [&](long long c0) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) vr[i] = R::load_v(vc + (c0 + i * 8) * HD + pv * HD, d4);
-    };
-    // The position through the scalar cache (the kernel only reads it): a
-    // chunk past the context leaves before requesting any rows, and the small
-    // loads that depend on the position need no vector wait first.
-    const long long pos = *(const __attribute__((address_space(4))) long long *)a.pos;
-    const long long len = pos + 1;
-    if (xw && s0 >= len) return;  // a chunk past the context (uniform over the block)
-    // A range starting past max_len (it has no positions) reads the last rows
-    // again, within the caches' tail: the loads need no branch.
-    const long long k0 = s0 < max_len ? s0 : max_len - 1;
-    if (WORDS) {
-        // The q/k/v words come long after the rows: request the rows first.
-        load_k(k0);
-        load_v(k0);
+    // Positions fit 32 bits (a cache of head_dim floats a row is far smaller
+    // than 2^31 rows): 32-bit scalar arithmetic keeps the loop's bounds in
+    // scalar registers.
+    const int pos = (int)*(const __attribute__((address_space(4))) long long *)a.pos;
+    const int len = pos + 1;
+    const int s0 = split * (int)chunk;
+    const int s1 = s0 + (int)chunk < len ? s0 + (int)chunk : len;
+    if (s0 >= s1) {
+        // No positions here: empty partials (finite zeros, max -inf) for the combine.
+        for (int idx = tid; idx < G * HD; idx += kThreads) {
+            const long long slot = (long long)(g * G + idx / HD) * a.nsplit + split;
+            a.part_acc[slot * HD + idx % HD] = 0.f;
+            if (idx % HD == 0) {
+                a.part_ml[slot * 2] = -INFINITY;
+                a.part_ml[slot * 2 + 1] = 0.f;
+            }
+        }
+        return;
     }
-    const float2 cs = reinterpret_cast<const float2 *>(a.rope + pos * HD)[lane];
+    uint4 ka[RS][NC], kb[RS][NC], va[RS][NC], vb[RS][NC];
+    // Buffer loads from the head's base (scalar registers): a lane's offsets
+    // within a pass are fixed, the pass's start is a scalar offset, so the
+    // loads need no 64-bit address registers.
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(kc), 0, 0x7fffffff, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(vc), 0, 0x7fffffff, kBufferRsrcWord3);
+    constexpr int ROWB = HD * (int)sizeof(KV);  // bytes a row
+    const int ofs = (wave * RW + drow) * ROWB + sub * 16;
+    auto load = [&](uint4 (&k)[RS][NC], uint4 (&v)[RS][NC], int c0) {
+        const int base = c0 * ROWB;
+#pragma unroll
+        for (int r = 0; r < RS; ++r)
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ofs + 4 * r * ROWB + i * LPR * 16, base, 0);
+                k[r][i] = make_uint4(x.x, x.y, x.z, x.w);
+            }
+#pragma unroll
+        for (int r = 0; r < RS; ++r)
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, ofs + 4 * r * ROWB + i * LPR * 16, base, 0);
+                v[r][i] = make_uint4(x.x, x.y, x.z, x.w);
+            }
+    };
+    if (WORDS) load(ka, va, s0);  // the words come long after the rows
+    const float2 cs = reinterpret_cast<const float2 *>(a.rope + (size_t)pos * HD)[lane];
     // RMSNorm gains of this wave's heads (q heads 0..G-1, then k), and, from
-    // a.qkv, the raw rows: loaded with no branch (rows clamped to valid ones)
-    // and used only once the cached rows are requested, so that no wait for
-    // them comes before that.
+    // a.qkv, the raw rows: loaded with no branch and used only after the
+    // rows are requested, so that no wait for them comes first.
     uint32_t gra[HPW], grb[HPW];
     float ar[HPW], br[HPW], vraw = 0.f;
 #pragma unroll
@@ -311,28 +325,21 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
         grb[hh] = gp[lane + HALF];
         ar[hh] = br[hh] = 0.f;
         if (!WORDS) {
-            const float *x = h < G ? a.qkv + (size_t)(qh0 + h) * HD : a.qkv + qd + (size_t)g * HD;
+            const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
             ar[hh] = x[lane];
             br[hh] = x[lane + HALF];
         }
     }
     if (!WORDS) {
         vraw = a.qkv[qd + kvd + (size_t)g * HD + (tid & (HD - 1))];
-        // Here q/k/v are already in memory: the small loads go first, so that
-        // waiting for them (loads complete in issue order for the wait
-        // counter) does not wait for the rows, which stream in meanwhile.
         __builtin_amdgcn_sched_barrier(0);
-        load_k(k0);
-        load_v(k0);
+        load(ka, va, s0);
         __builtin_amdgcn_sched_barrier(0);
     }
-    float ga[HPW], gb[HPW], av[HPW], bv[HPW];
+    float av[HPW], bv[HPW];
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
         const int h = wave + hh * kWaves;
-        const bool gained = h <= G && (h < G ? a.q_norm : a.k_norm) != nullptr;
-        ga[hh] = gained ? bf16_to_f32((uint16_t)gra[hh]) : 1.f;
-        gb[hh] = gained ? bf16_to_f32((uint16_t)grb[hh]) : 1.f;
         av[hh] = h <= G ? ar[hh] : 0.f;
         bv[hh] = h <= G ? br[hh] : 0.f;
     }
@@ -344,22 +351,20 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
             for (int hh = 0; hh < HPW; ++hh) {
                 const int h = wave + hh * kWaves;
                 if (h <= G) {
-                    const unsigned long long *x =
-                        h < G ? words + (size_t)(qh0 + h) * HD : words + qd + (size_t)g * HD;
-                    const unsigned long long wa =
-                        __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    const unsigned long long wb =
+                    const unsigned long long *x = h < G ? words + (size_t)(g * G + h) * HD : words + qd + (size_t)g * HD;
+                    const unsigned long long w0 = __hip_atomic_load(x + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const unsigned long long w1 =
                         __hip_atomic_load(x + lane + HALF, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    ok &= (unsigned)(wa >> 32) == epoch && (unsigned)(wb >> 32) == epoch;
-                    av[hh] = __uint_as_float((unsigned)wa);
-                    bv[hh] = __uint_as_float((unsigned)wb);
+                    ok &= (unsigned)(w0 >> 32) == epoch && (unsigned)(w1 >> 32) == epoch;
+                    av[hh] = __uint_as_float((unsigned)w0);
+                    bv[hh] = __uint_as_float((unsigned)w1);
                 }
             }
             if (tid < HD) {
-                const unsigned long long wv = __hip_atomic_load(words + qd + kvd + (size_t)g * HD + tid,
+                const unsigned long long w2 = __hip_atomic_load(words + qd + kvd + (size_t)g * HD + tid,
                                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok &= (unsigned)(wv >> 32) == epoch;
-                vnew = __uint_as_float((unsigned)wv);
+                ok &= (unsigned)(w2 >> 32) == epoch;
+                vnew = __uint_as_float((unsigned)w2);
             }
             if (__syncthreads_and(ok)) break;
             if (it >= (1 << 21)) {
@@ -368,12 +373,8 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
             }
         }
     }
-    if (tid < G) {
-        st_m[tid] = -INFINITY;
-        st_l[tid] = 0.f;
-    }
     if (tid < HD) hv[tid] = vnew;
-    // RMSNorm (model.rs:111-116) + RoPE (model.rs:117-118), one head per wave.
+    // RMSNorm (model.rs:111-116) + RoPE (model.rs:117-118), one head a wave.
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
         const int h = wave + hh * kWaves;
@@ -382,137 +383,176 @@ __device__ __forceinline__ void attend_regs(const StepAttnArgs &a, int g, int qh
         if (h < G ? a.q_norm != nullptr : a.k_norm != nullptr) {
             const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
             const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
-            x0 = x0 * (sc * ga[hh]);
-            x1 = x1 * (sc * gb[hh]);
+            x0 = x0 * (sc * bf16_to_f32((uint16_t)gra[hh]));
+            x1 = x1 * (sc * bf16_to_f32((uint16_t)grb[hh]));
         }
         float *x = h < G ? hq + h * HD : hk;
         x[lane] = x0 * cs.x - x1 * cs.y;
         x[lane + HALF] = x1 * cs.x + x0 * cs.y;
     }
     __syncthreads();
-    const float scale = 1.0f / sqrtf((float)HD);
-    float acc[G][4];
+    // The lane's dims of q, scaled into the base-2 domain: scores come out as
+    // s * log2(e) / sqrt(HD), so that each weight is one v_exp_f32.
+    const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
+    float q[G][DL];
 #pragma unroll
     for (int gg = 0; gg < G; ++gg)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[gg][i] = 0.f;
-    const long long s1 = s0 + chunk < len ? s0 + chunk : len;
-    for (long long c0 = s0; c0 < s1; c0 += ROWS) {
-        const int cnt = (int)(s1 - c0 < ROWS ? s1 - c0 : ROWS);
-        const bool more = c0 + ROWS < s1;
-        // Scores: positions below pos come from the cache, pos itself is the
-        // new key. q is read from LDS once per pass, all heads together.
-        float qf[G][8];
+        for (int i = 0; i < NC; ++i)
 #pragma unroll
-        for (int gg = 0; gg < G; ++gg) lds_row8(hq + gg * HD, sub, qf[gg]);
+            for (int e = 0; e < EPC; ++e) q[gg][i * EPC + e] = scale2 * hq[gg * HD + (sub + LPR * i) * EPC + e];
+    // m: the wave's running maximum (uniform); l: the lane's running sum of
+    // its rows' weights; acc: its 8 dims' weighted sums of its rows' values.
+    float m[G], l[G], acc[G][DL];
 #pragma unroll
-        for (int i = 0; i < NK; ++i) {
-            const int j = i * 16 + kq;
-            float kf[8];
-            R::unpack_k(kr[i], kf);
-            if (c0 + j == pos) lds_row8(hk, sub, kf);
+    for (int gg = 0; gg < G; ++gg) {
+        m[gg] = -INFINITY;
+        l[gg] = 0.f;
+#pragma unroll
+        for (int e = 0; e < DL; ++e) acc[gg][e] = 0.f;
+    }
+    // One pass over rows c0.. (the new key and value at pos from LDS: the
+    // caches do not hold them yet).
+    auto pass = [&](const uint4 (&k)[RS][NC], const uint4 (&v)[RS][NC], int c0) {
+        const bool has_pos = c0 <= pos && pos < c0 + PASS;  // uniform over the block
+        const bool whole = c0 + PASS <= s1;                  // uniform: every row in the context
+        float kf[RS][DL], vf[RS][DL];
+        bool valid[RS];
+#pragma unroll
+        for (int r = 0; r < RS; ++r) {
+            const int row = c0 + wave * RW + drow + 4 * r;
+            valid[r] = row < s1;
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                T::unpack(k[r][i], kf[r] + i * EPC);
+                T::unpack(v[r][i], vf[r] + i * EPC);
+            }
+            if (has_pos && row == pos) {
+                // The new key and value (their cache row is stale).
+#pragma unroll
+                for (int i = 0; i < NC; ++i)
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) {
+                        kf[r][i * EPC + e] = hk[(sub + LPR * i) * EPC + e];
+                        vf[r][i * EPC + e] = hv[(sub + LPR * i) * EPC + e];
+                    }
+            }
+            if (!whole && !valid[r]) {
+                // Rows past the context hold stale bits (NaN among them):
+                // their weight is 0, and their value is replaced by 0 too.
+#pragma unroll
+                for (int e = 0; e < DL; ++e) vf[r][e] = 0.f;
+            }
+        }
+        // Scores of the lane's two rows for every head: independent chains.
+        float sc[RS][G];
+#pragma unroll
+        for (int r = 0; r < RS; ++r)
 #pragma unroll
             for (int gg = 0; gg < G; ++gg) {
-                float sc = 0.f;
+                float t = 0.f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) sc = fmaf(qf[gg][e], kf[e], sc);
-                sc = row_sum_dpp(sc);
-                if (sub == 0 && j < cnt) scores[gg][j] = scale * sc;
+                for (int e = 0; e < DL; ++e) t = fmaf(q[gg][e], kf[r][e], t);
+                sc[r][gg] = t;
             }
+#pragma unroll
+        for (int r = 0; r < RS; ++r)
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) sc[r][gg] = row16_sum(sc[r][gg]);
+        if (!whole) {
+            // Rows past the context: score -inf (weight 0).
+#pragma unroll
+            for (int r = 0; r < RS; ++r)
+#pragma unroll
+                for (int gg = 0; gg < G; ++gg) sc[r][gg] = valid[r] ? sc[r][gg] : -INFINITY;
         }
-        if (more) load_k(c0 + ROWS);
-        __syncthreads();
-        // Online softmax, one wave per q head.
-        if (wave < G) {
-            float m = -INFINITY;
-            for (int j = lane; j < cnt; j += 64) m = fmaxf(m, scores[wave][j]);
-            m = wave_max_dpp(m);
-            const float m_old = st_m[wave], m_new = fmaxf(m_old, m);
-            float l = 0.f;
-            for (int j = lane; j < cnt; j += 64) {
-                const float e = expf(scores[wave][j] - m_new);
-                scores[wave][j] = e;
-                l += e;
-            }
-            l = wave_sum_dpp(l);
-            if (lane == 0) {
-                const float al = expf(m_old - m_new);
-                st_a[wave] = al;
-                st_l[wave] = st_l[wave] * al + l;
-                st_m[wave] = m_new;
-            }
-        }
-        __syncthreads();
 #pragma unroll
         for (int gg = 0; gg < G; ++gg) {
-            const float al = st_a[gg];
+            // The wave's maximum over its 8 rows (scores are finite or -inf).
+            float mx = sc[0][gg];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[gg][i] *= al;
-        }
-        // Weights of this lane's keys, eight keys at a time, all of a chunk
-        // read before any is used (0 past the context, where the value
-        // registers hold rows that are not used).
-        const long long fresh = pos - c0 - pv;  // slot * 8 of the key at pos, if this lane holds it
-        constexpr int PC = NV < 8 ? NV : 8;
+            for (int r = 1; r < RS; ++r) mx = max_nn(mx, sc[r][gg]);
+            mx = rows_max_nn(mx);
+            if (mx > m[gg]) {  // uniform: rescale only when the maximum rises
+                const float alpha = m[gg] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[gg] - mx);
+                l[gg] *= alpha;
 #pragma unroll
-        for (int i0 = 0; i0 < NV; i0 += PC) {
-            float pw[PC][G];
+                for (int e = 0; e < DL; ++e) acc[gg][e] *= alpha;
+                m[gg] = mx;
+            }
+            // exp2(-inf - m) = 0 for the rows past the context (m is finite:
+            // the wave has seen a row of the context by now, or all its rows
+            // so far are past it and m, mx and every score are -inf).
+            const float mm = m[gg] == -INFINITY ? 0.f : m[gg];
 #pragma unroll
-            for (int i = 0; i < PC; ++i)
+            for (int r = 0; r < RS; ++r) {
+                const float p = __builtin_amdgcn_exp2f(sc[r][gg] - mm);
+                l[gg] += p;
 #pragma unroll
-                for (int gg = 0; gg < G; ++gg)
-                    pw[i][gg] = (i0 + i) * 8 + pv < cnt ? scores[gg][(i0 + i) * 8 + pv] : 0.f;
-#pragma unroll
-            for (int i = 0; i < PC; ++i) {
-                if ((i0 + i) * 8 + pv < cnt) {
-                    float vf[4];
-                    R::unpack_v(vr[i0 + i], vf);
-                    if (fresh == (i0 + i) * 8) {
-                        const float4 n = reinterpret_cast<const float4 *>(hv)[d4];
-                        vf[0] = n.x; vf[1] = n.y; vf[2] = n.z; vf[3] = n.w;
-                    }
-#pragma unroll
-                    for (int gg = 0; gg < G; ++gg)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) acc[gg][e] = fmaf(pw[i][gg], vf[e], acc[gg][e]);
-                }
+                for (int e = 0; e < DL; ++e) acc[gg][e] = fmaf(p, vf[r][e], acc[gg][e]);
             }
         }
-        if (more) load_v(c0 + ROWS);
-        __syncthreads();  // scores are rewritten by the next pass
+    };
+    // Passes two at a time through the two register sets: the next pass's
+    // rows are requested before this pass's arithmetic, unconditionally (with
+    // no pass left, the current rows again, which hit in the cache), so that
+    // the wait for a pass's rows never waits for the next pass's.
+    for (int c0 = s0; c0 < s1; c0 += 2 * PASS) {
+        const int c1 = c0 + PASS;
+        load(kb, vb, c1 < s1 ? c1 : c0);
+        pass(ka, va, c0);
+        if (c1 >= s1) break;
+        load(ka, va, c1 + PASS < s1 ? c1 + PASS : c1);
+        pass(kb, vb, c1);
     }
     // The split holding pos appends the new key and value (model.rs:119-120);
     // no block of this launch reads that position from the caches.
-    if (append && pos >= s0 && pos < s0 + chunk && tid < HD) {
-        store_kv(const_cast<KV *>(kc) + pos * HD + tid, hk[tid]);
-        store_kv(const_cast<KV *>(vc) + pos * HD + tid, hv[tid]);
+    if (pos >= s0 && pos < s0 + (int)chunk && tid < HD) {
+        store_kv(const_cast<KV *>(kc) + (size_t)pos * HD + tid, hk[tid]);
+        store_kv(const_cast<KV *>(vc) + (size_t)pos * HD + tid, hv[tid]);
     }
-    // Sum the 8 key groups: lanes l and l + 32 of a wave, then the 4 waves.
+    // Every lane of a DPP row holds its rows' weighted sums for its dims: the
+    // rows go to LDS; the weight sums over the wave's rows (each lane holds
+    // its two rows', the same in every lane of the DPP row). The waves and
+    // rows merge in order, the maxima back in base e.
 #pragma unroll
-    for (int gg = 0; gg < G; ++gg)
+    for (int gg = 0; gg < G; ++gg) {
+        const float ls = rows_sum(l[gg]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc[gg][i] += __shfl_xor(acc[gg][i], 32, 64);
-            if (lane < 32) red[gg][wave][d4 * 4 + i] = acc[gg][i];
+        for (int i = 0; i < NC; ++i)
+#pragma unroll
+            for (int e4 = 0; e4 < EPC / 4; ++e4)
+                red[wave][drow][gg][((sub + LPR * i) * EPC) / 4 + e4] =
+                    make_float4(acc[gg][i * EPC + 4 * e4], acc[gg][i * EPC + 4 * e4 + 1],
+                                acc[gg][i * EPC + 4 * e4 + 2], acc[gg][i * EPC + 4 * e4 + 3]);
+        if (lane == 0) {
+            wm[wave][gg] = m[gg] * 0.6931471805599453f;
+            wl[wave][gg] = ls;
         }
+    }
     __syncthreads();
-    const int n_live = (int)((len + chunk - 1) / chunk);  // chunks holding positions
     for (int idx = tid; idx < G * HD; idx += kThreads) {
         const int gg = idx / HD, d = idx % HD;
-        const float sm = ((red[gg][0][d] + red[gg][1][d]) + red[gg][2][d]) + red[gg][3][d];
-        const long long h = (long long)qh0 + gg;
-        if (xw && n_live > 1) {
-            chunk_finish(a, h, d, sm, st_m[gg], st_l[gg], xw, n_chunks, split, n_live, epoch, err);
-            continue;
+        const float mx = fmaxf(fmaxf(wm[0][gg], wm[1][gg]), fmaxf(wm[2][gg], wm[3][gg]));
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float e = wm[w][gg] == -INFINITY ? 0.f : expf(wm[w][gg] - mx);
+            const float *r = reinterpret_cast<const float *>(&red[w][0][gg][0]) + d;
+            constexpr int RSTR = G * HD;  // floats between DPP rows
+            const float sw = ((r[0] + r[RSTR]) + r[2 * RSTR]) + r[3 * RSTR];
+            num = fmaf(sw, e, num);
+            den = fmaf(wl[w][gg], e, den);
         }
+        const long long h = (long long)g * G + gg;
         if (a.nsplit == 1) {
-            a.out[h * HD + d] = sm / st_l[gg];
+            a.out[h * HD + d] = num / den;
         } else {
             const long long slot = h * a.nsplit + split;
-            a.part_acc[slot * HD + d] = sm;
+            a.part_acc[slot * HD + d] = num;
             if (d == 0) {
-                a.part_ml[slot * 2] = st_m[gg];
-                a.part_ml[slot * 2 + 1] = st_l[gg];
+                a.part_ml[slot * 2] = mx;
+                a.part_ml[slot * 2 + 1] = den;
             }
         }
     }

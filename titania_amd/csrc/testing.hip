@@ -212,7 +212,7 @@ int th_test_step_attention(th_device *dev, const th_buffer *qkv, const th_weight
     const size_t cache_floats = kv_bf16 ? (n_kv_heads * max_len * hd + 1) / 2 : n_kv_heads * max_len * hd;
     const size_t need = cache_floats + (size_t)th::kStepKvTailRows * hd;
     TH_REQUIRE(k_cache->len >= need && v_cache->len >= need, "caches need %zu floats (the tail included)", need);
-    const int nsplit = th::step_attention_splits(max_len, kv_bf16);
+    const int nsplit = th::step_attention_splits(max_len, kv_bf16, (int)group, (int)n_kv_heads, dev->num_cus);
     DevMem st, part;
     TRY(st.alloc(sizeof(th::StepState), dev->stream));
     th::StepState host{};
