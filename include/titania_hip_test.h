@@ -43,16 +43,20 @@ TH_API int th_test_step_logits(th_device *dev, const th_weight *w, const th_buff
  * x_out = x + y, q/k/v = the GEMV of rmsnorm(x_out); q and k RMSNorm'd per
  * head (q_norm / k_norm may be NULL) and rotated, k and v appended to the
  * caches at pos, att = attention over positions 0..pos (model.rs:106-124).
- * The caches extend 128 rows of 128 floats past the last head. */
+ * Past the chunked launch's reach (more than 32 chunks of 64 positions a
+ * head, or 512 attention blocks), the launch that runs the streaming split
+ * attention instead, then the combine. The caches extend 128 rows of 128
+ * floats past the last head. */
 TH_API int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_weight *wk, const th_weight *wv,
                                  const th_buffer *x, const th_buffer *y, const th_weight *gain,
                                  const th_weight *q_norm, const th_weight *k_norm, float eps, const th_buffer *rope,
                                  th_buffer *k_cache, th_buffer *v_cache, size_t max_len, size_t pos,
                                  size_t n_heads, size_t n_kv_heads, th_buffer *x_out, th_buffer *att_out);
 
-/* The decode step's split attention and its combine, the launches a step
- * takes once its context outgrows the fused q/k/v + attention launch, for
- * one token at `pos` (model.rs:111-124): qkv holds the raw q, k and v rows
+/* The decode step's split attention and its combine for one token at `pos`
+ * (model.rs:111-124), the launches a step takes at any context for groups of
+ * 1 or 8 q heads (groups of 2 and 4 run the same attention inside the q/k/v
+ * launch once the chunked launch no longer reaches): qkv holds the raw q, k and v rows
  * ([n_heads * 128][n_kv_heads * 128][n_kv_heads * 128]); q and k are
  * RMSNorm'd per head (q_norm / k_norm may be NULL) and rotated, k and v
  * appended to the caches at pos, and att = attention over positions

@@ -118,6 +118,14 @@ constexpr int kStepKvTailRows = 128;
 bool step_qkv_attn_supported(int hidden, int n_heads, int n_kv_heads);
 hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &a);
 
+// The q/k/v GEMV and the split attention of launch_step_attention in one
+// launch (the same shapes as launch_step_qkv_attn take, any context): the
+// GEMV blocks publish the rows as epoch words, then one block per (KV head,
+// split of a.at.nsplit) requests its first cached rows, polls the words and
+// attends, leaving the split partials (a.at.part_acc / part_ml) for
+// launch_attn_combine, or the output with one split. a.chunks is unused.
+hipError_t launch_step_qkv_stream(hipStream_t s, const StepQkvAttnArgs &a);
+
 __device__ __forceinline__ void kv_load8(const float *p, float f[8]) {
     const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
     f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;

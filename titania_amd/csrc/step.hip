@@ -159,20 +159,11 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs &a) {
 // 0.5673 / 0.5651 / 0.5640 / 0.5693 ms with 2 / 3 / 4 / 5).
 constexpr int kQkvRowsPerWave = 4;
 
-template <int CPL, int G, typename KV>
-__global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
+// The GEMV blocks of the q/k/v + attention launches: the q/k/v rows of
+// launch_step_qkv, published as (value | epoch << 32) words.
+template <int CPL>
+__device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, unsigned epoch) {
     constexpr int RPW = kQkvRowsPerWave, RPB = RPW * kWaves;
-    const int ngemv = (a.n_rows + RPB - 1) / RPB;
-    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
-    if ((int)blockIdx.x >= ngemv) {
-        // `chunks` blocks per q head, one per pass of cached rows: the heads
-        // of a KV group attend in parallel (each reads the group's rows), the
-        // group's first head appends; each head's first chunk merges.
-        const int b = blockIdx.x - ngemv, h = b / q.chunks, c = b % q.chunks, g = h / G;
-        unsigned long long *xw = q.words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
-        attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
-        return;
-    }
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -198,6 +189,23 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
         if (lane == r && r0 + r < a.n_rows)
             __hip_atomic_store(q.words + r0 + r, ((unsigned long long)epoch << 32) | __float_as_uint(res[r]),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int CPL, int G, typename KV>
+__global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
+    constexpr int RPB = kQkvRowsPerWave * kWaves;
+    const int ngemv = (a.n_rows + RPB - 1) / RPB;
+    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
+    if ((int)blockIdx.x >= ngemv) {
+        // `chunks` blocks per q head, one per pass of cached rows: the heads
+        // of a KV group attend in parallel (each reads the group's rows), the
+        // group's first head appends; each head's first chunk merges.
+        const int b = blockIdx.x - ngemv, h = b / q.chunks, c = b % q.chunks, g = h / G;
+        unsigned long long *xw = q.words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
+        attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
+        return;
+    }
+    qkv_publish<CPL>(q, a, epoch);
 }
 
 template <int CPL, int G>
@@ -235,6 +243,38 @@ template <int G, typename KV>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<G, KV>())))
 void step_attention_stream_kernel(StepAttnArgs a, long long chunk) {
     attend_stream<G, KV, false>(a, blockIdx.x / a.nsplit, blockIdx.x % a.nsplit, chunk, nullptr, 0, nullptr);
+}
+
+// The GEMV blocks of qkv_attn_kernel, then one streaming attention block per
+// (KV head, split), which requests its first pass's rows and then polls the
+// words: the launch for contexts past the chunked launch's reach, leaving
+// the split partials for launch_attn_combine. Blocks start in index order
+// and the GEMV blocks never wait, so the attention blocks' polls always end.
+template <int CPL, int G, typename KV>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<G, KV>())))
+void qkv_stream_kernel(StepQkvAttnArgs q, GemvArgs a, long long chunk) {
+    constexpr int RPB = kQkvRowsPerWave * kWaves;
+    const int ngemv = (a.n_rows + RPB - 1) / RPB;
+    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
+    if ((int)blockIdx.x >= ngemv) {
+        const int b = blockIdx.x - ngemv;
+        attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, q.words, epoch, q.err);
+        return;
+    }
+    qkv_publish<CPL>(q, a, epoch);
+}
+
+template <int CPL, int G>
+hipError_t qkv_stream_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a) {
+    constexpr int RPB = kQkvRowsPerWave * kWaves;
+    const long long chunk = step_attention_chunk((size_t)(q.at.head_stride / 128), q.at.kv_bf16, q.at.nsplit);
+    dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB + q.at.n_kv_heads * q.at.nsplit));
+    const size_t lds = (size_t)a.cols * sizeof(float);
+    if (q.at.kv_bf16)
+        qkv_stream_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(q, a, chunk);
+    else
+        qkv_stream_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(q, a, chunk);
+    return hipGetLastError();
 }
 
 template <int G>
@@ -388,12 +428,9 @@ size_t step_qkv_attn_words(int q_rows, int kv_rows, int n_heads, int chunks) {
     return (size_t)q_rows + 2 * (size_t)kv_rows + (size_t)n_heads * chunks * (128 + 2);
 }
 
-hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
-    const StepQkvArgs &k = q.qkv;
-    const long long max_len = q.at.head_stride / 128;
-    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit != 1 || q.chunks < 1 ||
-        q.chunks != step_qkv_attn_chunks((size_t)max_len, q.at.kv_bf16, q.at.n_heads))
-        return hipErrorInvalidValue;
+namespace {
+
+GemvArgs qkv_gemv_args(const StepQkvArgs &k) {
     GemvArgs a{};
     a.rows.base[0] = k.wq;
     a.rows.count[0] = k.q_rows;
@@ -408,6 +445,33 @@ hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
     a.gain = k.gain;
     a.eps = k.eps;
     a.x_out = k.x_out;
+    return a;
+}
+
+}  // namespace
+
+hipError_t launch_step_qkv_stream(hipStream_t s, const StepQkvAttnArgs &q) {
+    const StepQkvArgs &k = q.qkv;
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit < 1 ||
+        (q.at.nsplit > 1 && (!q.at.part_acc || !q.at.part_ml)) || (q.at.nsplit == 1 && !q.at.out))
+        return hipErrorInvalidValue;
+    const GemvArgs a = qkv_gemv_args(k);
+    const int g = q.at.n_heads / q.at.n_kv_heads;
+    switch (k.hidden / 512) {
+    case 1: return g == 2 ? qkv_stream_launch<1, 2>(s, q, a) : qkv_stream_launch<1, 4>(s, q, a);
+    case 2: return g == 2 ? qkv_stream_launch<2, 2>(s, q, a) : qkv_stream_launch<2, 4>(s, q, a);
+    case 5: return g == 2 ? qkv_stream_launch<5, 2>(s, q, a) : qkv_stream_launch<5, 4>(s, q, a);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
+    const StepQkvArgs &k = q.qkv;
+    const long long max_len = q.at.head_stride / 128;
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit != 1 || q.chunks < 1 ||
+        q.chunks != step_qkv_attn_chunks((size_t)max_len, q.at.kv_bf16, q.at.n_heads))
+        return hipErrorInvalidValue;
+    const GemvArgs a = qkv_gemv_args(k);
     switch (k.hidden / 512) {
     case 1: return qkv_attn_g<1>(s, q, a);
     case 2: return qkv_attn_g<2>(s, q, a);

@@ -5,6 +5,7 @@
 // entry points, th_forward, th_decode) never calls them. They allocate the
 // small device state a kernel needs (step state, exchange words, bf16 hi/lo
 // operands) and free it before returning.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -145,11 +146,11 @@ int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_weight *
     const size_t need = n_kv_heads * max_len * hd + (size_t)th::kStepKvTailRows * hd;
     TH_REQUIRE(k_cache->len >= need && v_cache->len >= need, "caches need %zu floats (the tail included)", need);
     const int chunks = th::step_qkv_attn_chunks(max_len, 0, (int)n_heads);
-    TH_REQUIRE(chunks > 0 && th::step_qkv_attn_supported(H, (int)n_heads, (int)n_kv_heads),
-               "the fused launch does not take this shape or context");
-    DevMem st, words, err;
+    TH_REQUIRE(th::step_qkv_attn_supported(H, (int)n_heads, (int)n_kv_heads),
+               "the fused launch does not take this shape");
+    DevMem st, words, err, part;
     TRY(st.alloc(sizeof(th::StepState), dev->stream));
-    const size_t nw = th::step_qkv_attn_words((int)qd, (int)kvd, (int)n_heads, chunks);
+    const size_t nw = th::step_qkv_attn_words((int)qd, (int)kvd, (int)n_heads, std::max(chunks, 1));
     TRY(words.alloc(nw * sizeof(unsigned long long), dev->stream));
     TRY(err.alloc(sizeof(unsigned), dev->stream));
     th::StepState host{};
@@ -185,7 +186,25 @@ int th_test_step_qkv_attn(th_device *dev, const th_weight *wq, const th_weight *
     f.st = static_cast<th::StepState *>(st.p);
     f.layer = 0;
     f.chunks = chunks;
-    TH_HIP(th::launch_step_qkv_attn(dev->stream, f));
+    if (chunks > 0) {
+        TH_HIP(th::launch_step_qkv_attn(dev->stream, f));
+    } else {
+        // Past the chunked launch's reach: the streaming split attention in
+        // the same launch, then the combine, as the decode step runs them.
+        const int nsplit = th::step_attention_splits(max_len, 0, (int)(n_heads / n_kv_heads), (int)n_kv_heads,
+                                                     dev->num_cus);
+        f.at.nsplit = nsplit;
+        const size_t pf = th::attention_scratch(1, n_heads, hd, nsplit);
+        if (pf) {
+            TRY(part.alloc(pf * sizeof(float), dev->stream));
+            f.at.part_acc = static_cast<float *>(part.p);
+            f.at.part_ml = f.at.part_acc + n_heads * (size_t)nsplit * hd;
+        }
+        TH_HIP(th::launch_step_qkv_stream(dev->stream, f));
+        if (nsplit > 1)
+            TH_HIP(th::launch_attn_combine(dev->stream, att_out->ptr, f.at.part_acc, f.at.part_ml, n_heads, nsplit,
+                                           (int)hd));
+    }
     unsigned failures = 0;
     TH_HIP(hipMemcpyAsync(&failures, err.p, sizeof failures, hipMemcpyDeviceToHost, dev->stream));
     TH_HIP(hipStreamSynchronize(dev->stream));
