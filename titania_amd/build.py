@@ -29,6 +29,10 @@ FLAGS = [
     # Packed FP32 instructions stay off: hipcc would otherwise form them from
     # ordinary float code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Kernel arguments that lead a kernel's parameter list (scalars and
+    # pointers, up to 16 dwords) arrive preloaded in SGPRs, so a kernel's first
+    # loads need not wait on a fetch of its arguments.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-result",
 ]

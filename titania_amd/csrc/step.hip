@@ -44,6 +44,17 @@ struct GemvArgs {
     float *outs[3];
 };
 
+// The fields a GEMV block needs for its first weight loads travel as leading
+// scalar kernel arguments (the matrices' bases, the first two row counts, the
+// rows and columns), which the code object asks to have preloaded into SGPRs
+// at wave launch: the weight loads then issue without waiting on a fetch of
+// the kernel arguments. The same fields stay in GemvArgs for the host side.
+#define TH_GEMV_HEAD                                                                                       \
+    const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int c0, \
+        int c1, int n_rows, int cols
+#define TH_GEMV_HEAD_OF(a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], (a).rows.count[0], (a).rows.count[1], \
+                           (a).n_rows, (a).cols
+
 // Where kStore writes row r.
 __device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
     if (!a.outs[0]) return a.out + r;
@@ -55,8 +66,9 @@ __device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
 
 // One block: RPW rows per wave, CPL 16-byte chunks per lane per row.
 template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a) {
     static_assert(EPI != kSiluPairs || RPW % 2 == 0, "a wave holds whole (gate, up) pairs");
+    const Rows rows{{w0, w1, w2}, {c0, c1, 0}};
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     __shared__ uint64_t red64[kWaves];
@@ -64,19 +76,19 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     constexpr int RPB = RPW * kWaves;
     const int r0 = blockIdx.x * RPB + wave * RPW;
     // For paired rows (gate j, up j), a wave takes j and j + half.
-    const int half = a.n_rows / 2;
+    const int half = n_rows / 2;
     uint4 w[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         int row;
         if (EPI == kSiluPairs) row = (r & 1) ? (r0 + r - 1) / 2 + half : (r0 + r) / 2;
         else row = r0 + r;
-        const bool valid = EPI == kSiluPairs ? (r0 + r - (r & 1)) / 2 < half : row < a.n_rows;
-        const uint4 *p = row_at(a.rows, valid ? row : 0, a.cols);
+        const bool valid = EPI == kSiluPairs ? (r0 + r - (r & 1)) / 2 < half : row < n_rows;
+        const uint4 *p = row_at(rows, valid ? row : 0, cols);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt_row(p, c * 64 + lane);
     }
-    build_input<PRO == kNormSum, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out,
+    build_input<PRO == kNormSum, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, cols, a.gain, a.eps, a.x_out,
                                                                         red);
     float res[RPW];
 #pragma unroll
@@ -90,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         if (lane < RPW) {
 #pragma unroll
             for (int r = 0; r < RPW; ++r)
-                if (lane == r && r0 + r < a.n_rows) *store_at(a, r0 + r) = res[r];
+                if (lane == r && r0 + r < n_rows) *store_at(a, r0 + r) = res[r];
         }
     } else if (EPI == kSiluPairs) {
         // Rows r0 + 2i and r0 + 2i + 1 of the wave are gate j and up j.
@@ -103,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         uint64_t best = 0;
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-            if (r0 + r < a.n_rows) {
+            if (r0 + r < n_rows) {
                 if (lane == 0) a.out[r0 + r] = res[r];
                 best = max_u64(best, argmax_pack(res[r], (uint32_t)(r0 + r)));
             }
@@ -122,7 +134,7 @@ template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
 hipError_t gemv_launch(hipStream_t s, const GemvArgs &a) {
     constexpr int RPB = RPW * kWaves;
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB));
-    gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, a.cols * sizeof(float), s>>>(a);
+    gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, a.cols * sizeof(float), s>>>(TH_GEMV_HEAD_OF(a), a);
     return hipGetLastError();
 }
 
@@ -162,7 +174,8 @@ constexpr int kQkvRowsPerWave = 4;
 // The GEMV blocks of the q/k/v + attention launches: the q/k/v rows of
 // launch_step_qkv, published as (value | epoch << 32) words.
 template <int CPL>
-__device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, unsigned epoch) {
+__device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, const Rows &rows, int n_rows,
+                                            int cols, unsigned epoch) {
     constexpr int RPW = kQkvRowsPerWave, RPB = RPW * kWaves;
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
@@ -171,11 +184,11 @@ __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const Gemv
     uint4 w[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-        const uint4 *p = row_at(a.rows, r0 + r < a.n_rows ? r0 + r : 0, a.cols);
+        const uint4 *p = row_at(rows, r0 + r < n_rows ? r0 + r : 0, cols);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt_row(p, c * 64 + lane);
     }
-    build_input<true, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, a.cols, a.gain, a.eps, a.x_out, red);
+    build_input<true, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, cols, a.gain, a.eps, a.x_out, red);
     float res[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -186,15 +199,15 @@ __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const Gemv
     }
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
-        if (lane == r && r0 + r < a.n_rows)
+        if (lane == r && r0 + r < n_rows)
             __hip_atomic_store(q.words + r0 + r, ((unsigned long long)epoch << 32) | __float_as_uint(res[r]),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int CPL, int G, typename KV>
-__global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, GemvArgs a) {
+__global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_GEMV_HEAD, StepQkvAttnArgs q, GemvArgs a) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
-    const int ngemv = (a.n_rows + RPB - 1) / RPB;
+    const int ngemv = (n_rows + RPB - 1) / RPB;
     const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
         // `chunks` blocks per q head, one per pass of cached rows: the heads
@@ -205,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(StepQkvAttnArgs q, G
         attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
         return;
     }
-    qkv_publish<CPL>(q, a, epoch);
+    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, epoch);
 }
 
 template <int CPL, int G>
@@ -214,9 +227,9 @@ hipError_t qkv_attn_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvAr
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB + q.at.n_heads * q.chunks));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
-        qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(q, a);
+        qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a);
     else
-        qkv_attn_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(q, a);
+        qkv_attn_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a);
     return hipGetLastError();
 }
 
@@ -252,16 +265,16 @@ void step_attention_stream_kernel(StepAttnArgs a, long long chunk) {
 // and the GEMV blocks never wait, so the attention blocks' polls always end.
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<G, KV>())))
-void qkv_stream_kernel(StepQkvAttnArgs q, GemvArgs a, long long chunk) {
+void qkv_stream_kernel(TH_GEMV_HEAD, StepQkvAttnArgs q, GemvArgs a, long long chunk) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
-    const int ngemv = (a.n_rows + RPB - 1) / RPB;
+    const int ngemv = (n_rows + RPB - 1) / RPB;
     const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
         const int b = blockIdx.x - ngemv;
         attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, q.words, epoch, q.err);
         return;
     }
-    qkv_publish<CPL>(q, a, epoch);
+    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, epoch);
 }
 
 template <int CPL, int G>
@@ -271,9 +284,9 @@ hipError_t qkv_stream_launch(hipStream_t s, const StepQkvAttnArgs &q, const Gemv
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB + q.at.n_kv_heads * q.at.nsplit));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
-        qkv_stream_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(q, a, chunk);
+        qkv_stream_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a, chunk);
     else
-        qkv_stream_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(q, a, chunk);
+        qkv_stream_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a, chunk);
     return hipGetLastError();
 }
 
