@@ -362,13 +362,19 @@ int enqueue_step(th_state *s) {
     const bool fuse_attn = chunks > 0 && th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64;
     // Past the chunked launch's reach, the q/k/v GEMV and the streaming
     // attention share a launch when the GEMV blocks are few beside the
-    // attention's, so that both find block slots at once (Qwen3-0.6B, 4096
-    // positions: 256 GEMV and 1024 attention blocks, 0.876 -> 0.852 ms a
-    // step); where the GEMV blocks alone fill the chip (Qwen3-4B at 8192
-    // positions: 768 and 704) the separate launches were 0.2% faster.
+    // attention's (Qwen3-0.6B, max_len 4096: 256 GEMV and 1024 attention
+    // blocks, 0.876 -> 0.852 ms a step) or when both fit the attention's
+    // block slots in one round (Qwen3-0.6B, 4160 positions: 256 + 520 blocks
+    // for 1024 slots, 0.829 -> 0.804 ms; a 16-token context in a state of 2200
+    // positions: 0.673 -> 0.669 ms). Where they do not (Qwen3-4B at 8192
+    // positions: 384 + 688 blocks for 768 slots) the separate launches are
+    // faster: 0.2% against the shared launch, and 3% against one whose
+    // splits were cut to fit.
     const int gemv_blocks = (qd + 2 * kvd + 15) / 16;
     const bool stream_fused = !fuse_attn && th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64 &&
-                              3 * gemv_blocks <= nkv * nsplit;
+                              (3 * gemv_blocks <= nkv * nsplit ||
+                               gemv_blocks + nkv * nsplit <= th::step_stream_slots(nh / nkv, s->kv_dtype == TH_KV_BF16,
+                                                                                   m->dev->num_cus));
     // sx_b holds the token's embedding row: the previous pick wrote it.
     const float *y_prev = nullptr;
     for (size_t l = 0; l < m->layers.size(); ++l) {

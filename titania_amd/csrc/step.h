@@ -76,6 +76,9 @@ struct StepAttnArgs {
 // one round, in whole passes of its blocks (32 f32 / 64 bf16 positions), at
 // most 256.
 int step_attention_splits(size_t max_len, int kv_bf16, int group, int n_kv_heads, int num_cus);
+// Block slots of the streaming attention's launches on a GPU of num_cus
+// compute units (blocks a CU: the waves a SIMD it is built for).
+int step_stream_slots(int group, int kv_bf16, int num_cus);
 // Positions a split covers: max_len / nsplit rounded up to whole passes.
 long long step_attention_chunk(size_t max_len, int kv_bf16, int nsplit);
 hipError_t launch_step_attention(hipStream_t s, const StepAttnArgs &a);

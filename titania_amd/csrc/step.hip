@@ -502,6 +502,17 @@ long long step_attention_chunk(size_t max_len, int kv_bf16, int nsplit) {
     return (c + pass - 1) / pass * pass;
 }
 
+int step_stream_slots(int group, int kv_bf16, int num_cus) {
+    int per_cu;
+    switch (group) {
+    case 1: per_cu = kv_bf16 ? stream_waves_per_eu<1, uint16_t>() : stream_waves_per_eu<1, float>(); break;
+    case 2: per_cu = kv_bf16 ? stream_waves_per_eu<2, uint16_t>() : stream_waves_per_eu<2, float>(); break;
+    case 4: per_cu = kv_bf16 ? stream_waves_per_eu<4, uint16_t>() : stream_waves_per_eu<4, float>(); break;
+    default: per_cu = kv_bf16 ? stream_waves_per_eu<8, uint16_t>() : stream_waves_per_eu<8, float>(); break;
+    }
+    return std::max(num_cus, 1) * per_cu;
+}
+
 int step_attention_splits(size_t max_len, int kv_bf16, int group, int n_kv_heads, int num_cus) {
     if (max_len <= 512 || n_kv_heads < 1) return 1;
     // As many splits as fill the chip's block slots in one round (blocks a
@@ -510,14 +521,7 @@ int step_attention_splits(size_t max_len, int kv_bf16, int group, int n_kv_heads
     // (Qwen3-4B at 8192 positions, f32: splits of 1 / 2 / 3 / 4 / 8 passes
     // gave 2.618 / 2.532 / 2.501 / 2.616 / 2.716 ms a step; three, 704
     // blocks for 768 slots, filled it).
-    int per_cu;
-    switch (group) {
-    case 1: per_cu = kv_bf16 ? stream_waves_per_eu<1, uint16_t>() : stream_waves_per_eu<1, float>(); break;
-    case 2: per_cu = kv_bf16 ? stream_waves_per_eu<2, uint16_t>() : stream_waves_per_eu<2, float>(); break;
-    case 4: per_cu = kv_bf16 ? stream_waves_per_eu<4, uint16_t>() : stream_waves_per_eu<4, float>(); break;
-    default: per_cu = kv_bf16 ? stream_waves_per_eu<8, uint16_t>() : stream_waves_per_eu<8, float>(); break;
-    }
-    const long long want = std::max(1LL, (long long)std::max(num_cus, 1) * per_cu / n_kv_heads);
+    const long long want = std::max(1LL, (long long)step_stream_slots(group, kv_bf16, num_cus) / n_kv_heads);
     long long chunk = step_attention_chunk(max_len, kv_bf16, (int)std::min(want, 256LL));
     return (int)(((long long)max_len + chunk - 1) / chunk);
 }

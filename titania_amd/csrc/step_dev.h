@@ -292,20 +292,29 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
         __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(vc), 0, 0x7fffffff, kBufferRsrcWord3);
     constexpr int ROWB = HD * (int)sizeof(KV);  // bytes a row
     const int ofs = (wave * RW + drow) * ROWB + sub * 16;
-    auto load = [&](uint4 (&k)[RS][NC], uint4 (&v)[RS][NC], int c0) {
+    // A request with no pass left goes through descriptors of no records:
+    // the same instructions (so that every wait counts the same requests),
+    // answered with zeros and no memory access, so the block ends without
+    // waiting for rows it would not use.
+    const __amdgpu_buffer_rsrc_t nk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(kc), 0, 0, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t nv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(vc), 0, 0, kBufferRsrcWord3);
+    auto load = [&](uint4 (&k)[RS][NC], uint4 (&v)[RS][NC], int c0, bool live = true) {
+        const __amdgpu_buffer_rsrc_t sk = live ? rk : nk, sv = live ? rv : nv;
         const int base = c0 * ROWB;
 #pragma unroll
         for (int r = 0; r < RS; ++r)
 #pragma unroll
             for (int i = 0; i < NC; ++i) {
-                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ofs + 4 * r * ROWB + i * LPR * 16, base, 0);
+                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(sk, ofs + 4 * r * ROWB + i * LPR * 16, base, 0);
                 k[r][i] = make_uint4(x.x, x.y, x.z, x.w);
             }
 #pragma unroll
         for (int r = 0; r < RS; ++r)
 #pragma unroll
             for (int i = 0; i < NC; ++i) {
-                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, ofs + 4 * r * ROWB + i * LPR * 16, base, 0);
+                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(sv, ofs + 4 * r * ROWB + i * LPR * 16, base, 0);
                 v[r][i] = make_uint4(x.x, x.y, x.z, x.w);
             }
     };
@@ -495,14 +504,14 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
     };
     // Passes two at a time through the two register sets: the next pass's
     // rows are requested before this pass's arithmetic, unconditionally (with
-    // no pass left, the current rows again, which hit in the cache), so that
-    // the wait for a pass's rows never waits for the next pass's.
+    // no pass left, through the descriptors of no records), so that the wait
+    // for a pass's rows never waits for the next pass's.
     for (int c0 = s0; c0 < s1; c0 += 2 * PASS) {
         const int c1 = c0 + PASS;
-        load(kb, vb, c1 < s1 ? c1 : c0);
+        load(kb, vb, c1 < s1 ? c1 : c0, c1 < s1);
         pass(ka, va, c0);
         if (c1 >= s1) break;
-        load(ka, va, c1 + PASS < s1 ? c1 + PASS : c1);
+        load(ka, va, c1 + PASS < s1 ? c1 + PASS : c1, c1 + PASS < s1);
         pass(kb, vb, c1);
     }
     // The split holding pos appends the new key and value (model.rs:119-120);
