@@ -234,8 +234,10 @@ def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
     """Decode with eight KV heads against the oracle: one attention chunk per
     head (9 positions), several chunks merged by each head's first (300 and
     700 positions: 5 and 12 chunks of 64 f32 or 3 of 128 bf16 positions), and
-    past the fused launch's 32 chunks a head the split attention kernel with
-    its combine (2100 f32 positions: 33 splits of 64; 4200 bf16: 33 of 128)."""
+    past the chunked launch's 32 chunks a head the streaming split attention
+    with its combine (2100 f32 and 4200 bf16 positions: 66 splits of 32 and
+    64 positions on a 256-CU chip, in the q/k/v GEMV's launch since both
+    fit its block slots)."""
     m, r = tiny8
     c = QWEN3_TINY8
     prompt = synth.prompt(prompt_len, c.vocab_size, seed=prompt_len + 1)
