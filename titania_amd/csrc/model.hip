@@ -365,8 +365,8 @@ int enqueue_step(th_state *s) {
     // attention's (Qwen3-0.6B, max_len 4096: 256 GEMV and 1024 attention
     // blocks, 0.876 -> 0.852 ms a step) or when both fit the attention's
     // block slots in one round (Qwen3-0.6B, 4160 positions: 256 + 520 blocks
-    // for 1024 slots, 0.829 -> 0.804 ms; a 16-token context in a state of 2200
-    // positions: 0.673 -> 0.669 ms). Where they do not (Qwen3-4B at 8192
+    // for 1024 slots, 0.829 -> 0.813 ms; a 16-token context in a state of 2200
+    // positions: 0.676 -> 0.672 ms). Where they do not (Qwen3-4B at 8192
     // positions: 384 + 688 blocks for 768 slots) the separate launches are
     // faster: 0.2% against the shared launch, and 3% against one whose
     // splits were cut to fit.
