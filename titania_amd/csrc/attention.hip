@@ -348,10 +348,13 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(AttnKernelArgs a) {
 // over splits, then over (dimension, group of splits)), not one after another.
 constexpr int kCombineThreads = 256, kMaxSplits = 256;
 
+// gy is gridDim.y, passed as an argument so that it arrives preloaded with
+// the others (the grid's size is otherwise one more fetch before the first
+// loads can be addressed).
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__restrict__ out,
                                                                       const float *__restrict__ part_acc,
                                                                       const float *__restrict__ part_ml, int nsplit,
-                                                                      int hd, uint16_t *__restrict__ hi,
+                                                                      int hd, int gy, uint16_t *__restrict__ hi,
                                                                       uint16_t *__restrict__ lo) {
     constexpr int kPre = 16;  // accumulator rows a thread requests up front
     __shared__ float w[kMaxSplits];
@@ -360,10 +363,10 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(float *__
     const long long th = blockIdx.x;  // token * n_heads + head
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *ml = part_ml + th * nsplit * 2;
-    // This block's dimensions [dlo, dlo + dw) (gridDim.y blocks share a
-    // head), in groups of splits: thread t takes dimension dlo + t % dw of
-    // the splits s = t / dw, + groups, ...
-    const int dw = hd / (int)gridDim.y, dlo = (int)blockIdx.y * dw;
+    // This block's dimensions [dlo, dlo + dw) (gy blocks share a head), in
+    // groups of splits: thread t takes dimension dlo + t % dw of the splits
+    // s = t / dw, + groups, ...
+    const int dw = hd / gy, dlo = (int)blockIdx.y * dw;
     const int groups = dw < kCombineThreads ? kCombineThreads / dw : 1;
     // With one pass over the dimensions and at most kPre splits a thread
     // (every launch of the decode step), the accumulator rows are requested
@@ -554,7 +557,8 @@ hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc,
     unsigned ysplit = 1;
     while (heads * ysplit < 256 && hd % (int)(ysplit * 2) == 0 && hd / (int)(ysplit * 2) >= 16) ysplit *= 2;
     attn_combine_kernel<<<dim3((unsigned)heads, ysplit), dim3(kCombineThreads), 0, s>>>(out, part_acc, part_ml,
-                                                                                         nsplit, hd, hi, lo);
+                                                                                         nsplit, hd, (int)ysplit, hi,
+                                                                                         lo);
     return hipGetLastError();
 }
 

@@ -156,9 +156,12 @@ __device__ __forceinline__ bf16x8 frag(const uint4 *tile, int row, int lc) {
 // panels of PANEL row tiles (down the panel, then across): the blocks an XCD
 // runs together cover a few weight tiles and a few token tiles, and share
 // both. The map is a bijection whatever the XCD count; only the speed assumes it.
+// gx, gy: the grid's x and y sizes, passed by the kernels as leading
+// arguments (preloaded into SGPRs with the others; the grid's size is
+// otherwise one more fetch before a block's first loads can be addressed).
 template <int PANEL>
-__device__ __forceinline__ void tile_of_block(int &tx, int &ty) {
-    const int gx = (int)gridDim.x, gy = (int)gridDim.y, nt = gx * gy;
+__device__ __forceinline__ void tile_of_block(int &tx, int &ty, int gx, int gy) {
+    const int nt = gx * gy;
     const int lin = (int)blockIdx.x + (int)blockIdx.y * gx;
     constexpr int kXcds = 8;
     const int xcd = lin % kXcds, i = lin / kXcds, q = nt / kXcds, r = nt % kXcds;
@@ -188,9 +191,9 @@ struct PairTile {
     int inter, r0;
 };
 
-__device__ __forceinline__ SegTile seg_tile(const Segs &s, int r0) {
-    const int n0 = s.rows[0], n1 = s.rows[1];
-    if (r0 < n0) return SegTile{s.w[0], s.out[0], n0, r0};
+__device__ __forceinline__ SegTile seg_tile(const uint16_t *w0, float *out0, int n0, const Segs &s, int r0) {
+    const int n1 = s.rows[1];
+    if (r0 < n0) return SegTile{w0, out0, n0, r0};
     if (r0 < n0 + n1) return SegTile{s.w[1], s.out[1], n1, r0 - n0};
     return SegTile{s.w[2], s.out[2], s.rows[2], r0 - n0 - n1};
 }
@@ -524,28 +527,31 @@ __device__ __forceinline__ void gemm_tile(int ty, SegTile sg, const uint16_t *__
             }
 }
 
-__global__ __launch_bounds__(Small::NT, 2) void gemm_kernel(Segs sg, const uint16_t *__restrict__ hi,
-                                                        const uint16_t *__restrict__ lo, int n, int cols,
-                                                        float *__restrict__ part, int ksplit) {
+__global__ __launch_bounds__(Small::NT, 2) void gemm_kernel(int gxy, int rows0, const uint16_t *__restrict__ w0,
+                                                        float *__restrict__ out0, const uint16_t *__restrict__ hi,
+                                                        const uint16_t *__restrict__ lo, int n, int cols, int ksplit,
+                                                        float *__restrict__ part, Segs sg) {
     int tx, ty;
-    tile_of_block<8>(tx, ty);
-    gemm_tile<Small>(ty, seg_tile(sg, tx * Small::BN), hi, lo, n, cols, part, ksplit);
+    tile_of_block<8>(tx, ty, gxy & 0xffff, gxy >> 16);
+    gemm_tile<Small>(ty, seg_tile(w0, out0, rows0, sg, tx * Small::BN), hi, lo, n, cols, part, ksplit);
 }
 
-__global__ __launch_bounds__(Large::NT, 1) void gemm_large_kernel(Segs sg, const uint16_t *__restrict__ hi,
-                                                              const uint16_t *__restrict__ lo, int n, int cols,
-                                                              float *__restrict__ part, int ksplit) {
+__global__ __launch_bounds__(Large::NT, 1) void gemm_large_kernel(int gxy, int rows0, const uint16_t *__restrict__ w0,
+                                                        float *__restrict__ out0, const uint16_t *__restrict__ hi,
+                                                        const uint16_t *__restrict__ lo, int n, int cols, int ksplit,
+                                                        float *__restrict__ part, Segs sg) {
     int tx, ty;
-    tile_of_block<4>(tx, ty);
-    gemm_tile<Large>(ty, seg_tile(sg, tx * Large::BN), hi, lo, n, cols, part, ksplit);
+    tile_of_block<4>(tx, ty, gxy & 0xffff, gxy >> 16);
+    gemm_tile<Large>(ty, seg_tile(w0, out0, rows0, sg, tx * Large::BN), hi, lo, n, cols, part, ksplit);
 }
 
-__global__ __launch_bounds__(Huge::NT, 1) void gemm_huge_kernel(Segs sg, const uint16_t *__restrict__ hi,
-                                                            const uint16_t *__restrict__ lo, int n, int cols,
-                                                            float *__restrict__ part, int ksplit) {
+__global__ __launch_bounds__(Huge::NT, 1) void gemm_huge_kernel(int gxy, int rows0, const uint16_t *__restrict__ w0,
+                                                        float *__restrict__ out0, const uint16_t *__restrict__ hi,
+                                                        const uint16_t *__restrict__ lo, int n, int cols, int ksplit,
+                                                        float *__restrict__ part, Segs sg) {
     int tx, ty;
-    tile_of_block<2>(tx, ty);
-    gemm_tile<Huge>(ty, seg_tile(sg, tx * Huge::BN), hi, lo, n, cols, part, ksplit);
+    tile_of_block<2>(tx, ty, gxy & 0xffff, gxy >> 16);
+    gemm_tile<Huge>(ty, seg_tile(w0, out0, rows0, sg, tx * Huge::BN), hi, lo, n, cols, part, ksplit);
 }
 
 // gate and up in one launch, block x taking rows [x BN/2, (x + 1) BN/2) of
@@ -553,10 +559,10 @@ __global__ __launch_bounds__(Huge::NT, 1) void gemm_huge_kernel(Segs sg, const u
 template <class T>
 __global__ __launch_bounds__(T::NT, T::NT == 256 ? (T::kStages == 2 ? 3 : 2) : 1) void gemm_silu_kernel(
     const uint16_t *__restrict__ gate, const uint16_t *__restrict__ up, const uint16_t *__restrict__ hi,
-    const uint16_t *__restrict__ lo, int n, int cols, int inter, uint16_t *__restrict__ h_hi,
+    const uint16_t *__restrict__ lo, int n, int cols, int inter, int gx, int gy, uint16_t *__restrict__ h_hi,
     uint16_t *__restrict__ h_lo) {
     int tx, ty;
-    tile_of_block<T::NT == 256 ? 8 : T::BM == 256 ? 2 : 4>(tx, ty);
+    tile_of_block<T::NT == 256 ? 8 : T::BM == 256 ? 2 : 4>(tx, ty, gx, gy);
     const PairTile pt{gate, up, h_hi, h_lo, inter, tx * (T::BN / 2)};
     gemm_tile<T, kSiluPairs>(ty, SegTile{}, hi, lo, n, cols, nullptr, 1, pt);
 }
@@ -570,10 +576,12 @@ __global__ __launch_bounds__(Head::NT, 2) void gemm_qkv_kernel(const uint16_t *_
                                                                const uint16_t *__restrict__ wv,
                                                                const uint16_t *__restrict__ hi,
                                                                const uint16_t *__restrict__ lo, int n, int cols,
-                                                               QkvPostArgs a) {
+                                                               int gxy, int nqkv, QkvPostArgs a) {
+    // gxy = grid x | grid y << 16, nqkv = q heads | KV heads << 16: packed so
+    // that every field the first loads need fits the 14 preloaded dwords.
+    const int nq = nqkv & 0xffff, nkv = nqkv >> 16;
     int h, ty;
-    tile_of_block<8>(h, ty);
-    const int nq = a.n_heads, nkv = a.n_kv_heads;
+    tile_of_block<8>(h, ty, gxy & 0xffff, gxy >> 16);
     const int role = h < nq ? 0 : h < nq + nkv ? 1 : 2;
     const int head = role == 0 ? h : role == 1 ? h - nq : h - nq - nkv;
     const uint16_t *w = (role == 0 ? wq : role == 1 ? wk : wv) + (size_t)head * 128 * cols;
@@ -590,10 +598,11 @@ __global__ __launch_bounds__(Huge::NT, 1) void gemm_qkv_huge_kernel(const uint16
                                                                     const uint16_t *__restrict__ wv,
                                                                     const uint16_t *__restrict__ hi,
                                                                     const uint16_t *__restrict__ lo, int n, int cols,
-                                                                    QkvPostArgs a) {
+                                                                    int gxy, int nqkv, QkvPostArgs a) {
+    // Packed as in gemm_qkv_kernel.
     int tx, ty;
-    tile_of_block<2>(tx, ty);
-    const int qd = a.n_heads * 128, kvd = a.n_kv_heads * 128, r0 = tx * Huge::BN;
+    tile_of_block<2>(tx, ty, gxy & 0xffff, gxy >> 16);
+    const int qd = (nqkv & 0xffff) * 128, kvd = (nqkv >> 16) * 128, r0 = tx * Huge::BN;
     const int role = r0 < qd ? 0 : r0 < qd + kvd ? 1 : 2;
     const int local = role == 0 ? r0 : role == 1 ? r0 - qd : r0 - qd - kvd;
     const uint16_t *w = (role == 0 ? wq : role == 1 ? wk : wv) + (size_t)local * cols;
@@ -722,15 +731,24 @@ hipError_t launch_gemm_hl(hipStream_t s, const uint16_t *hi, const uint16_t *lo,
         rows_huge = rows_huge && outs[i].rows % Huge::BN == 0;
     }
     const Plan plan = gemm_plan(n, total, cols, n_outs, rows_large, rows_huge);
+    // The grid's x and y sizes travel packed in 16 bits each (both under
+    // 65536 by the checks above).
+    auto pack = [](const dim3 &g) { return (int)(g.x | g.y << 16); };
     if (plan.huge && plan.ksplit == ksplit) {
         dim3 grid((unsigned)(total / Huge::BN), (unsigned)((n + Huge::BM - 1) / Huge::BM), (unsigned)ksplit);
-        gemm_huge_kernel<<<grid, Huge::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+        const int gxy = pack(grid);
+        gemm_huge_kernel<<<grid, Huge::NT, 0, s>>>(gxy, sg.rows[0], sg.w[0], sg.out[0], hi, lo, (int)n, (int)cols,
+                                                        ksplit, part, sg);
     } else if (plan.large && !plan.huge && plan.ksplit == ksplit) {
         dim3 grid((unsigned)(total / Large::BN), (unsigned)((n + Large::BM - 1) / Large::BM), (unsigned)ksplit);
-        gemm_large_kernel<<<grid, Large::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+        const int gxy = pack(grid);
+        gemm_large_kernel<<<grid, Large::NT, 0, s>>>(gxy, sg.rows[0], sg.w[0], sg.out[0], hi, lo, (int)n, (int)cols,
+                                                         ksplit, part, sg);
     } else {
         dim3 grid((unsigned)(total / Small::BN), (unsigned)((n + Small::BM - 1) / Small::BM), (unsigned)ksplit);
-        gemm_kernel<<<grid, Small::NT, 0, s>>>(sg, hi, lo, (int)n, (int)cols, part, ksplit);
+        const int gxy = pack(grid);
+        gemm_kernel<<<grid, Small::NT, 0, s>>>(gxy, sg.rows[0], sg.w[0], sg.out[0], hi, lo, (int)n, (int)cols,
+                                                   ksplit, part, sg);
     }
     return hipGetLastError();
 }
@@ -745,20 +763,20 @@ hipError_t launch_gemm_silu(hipStream_t s, const uint16_t *hi, const uint16_t *l
     const Plan plan = gemm_plan(n, 2 * inter, cols, 2, true, inter % (Huge::BN / 2) == 0);
     if (plan.huge) {
         dim3 grid((unsigned)(inter / (Huge::BN / 2)), (unsigned)((n + Huge::BM - 1) / Huge::BM));
-        gemm_silu_kernel<Huge><<<grid, Huge::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
-                                                          h_lo);
+        gemm_silu_kernel<Huge><<<grid, Huge::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter,
+                                                          (int)grid.x, (int)grid.y, h_hi, h_lo);
     } else if (plan.large) {
         dim3 grid((unsigned)(inter / (Large::BN / 2)), (unsigned)((n + Large::BM - 1) / Large::BM));
-        gemm_silu_kernel<Large><<<grid, Large::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter, h_hi,
-                                                           h_lo);
+        gemm_silu_kernel<Large><<<grid, Large::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter,
+                                                           (int)grid.x, (int)grid.y, h_hi, h_lo);
     } else {
         dim3 grid((unsigned)(inter / (Small::BN / 2)), (unsigned)((n + Small::BM - 1) / Small::BM));
         if ((size_t)grid.x * grid.y > kSmall2MinTiles)
             gemm_silu_kernel<Small2><<<grid, Small2::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter,
-                                                                 h_hi, h_lo);
+                                                                 (int)grid.x, (int)grid.y, h_hi, h_lo);
         else
             gemm_silu_kernel<Small><<<grid, Small::NT, 0, s>>>(gate, up, hi, lo, (int)n, (int)cols, (int)inter,
-                                                               h_hi, h_lo);
+                                                               (int)grid.x, (int)grid.y, h_hi, h_lo);
     }
     return hipGetLastError();
 }
@@ -776,10 +794,13 @@ hipError_t launch_gemm_qkv_huge(hipStream_t s, const uint16_t *hi, const uint16_
         (a.kh && (!a.kl || !a.vh || !a.vl || a.plane_len % 64 || a.pos + a.n > a.plane_len)))
         return hipErrorInvalidValue;
     dim3 grid((unsigned)((qd + 2 * kvd) / Huge::BN), (unsigned)((n + Huge::BM - 1) / Huge::BM));
+    if (grid.x > 0xffff || grid.y > 0xffff || a.n_heads > 0xffff || a.n_kv_heads > 0x7fff)
+        return hipErrorInvalidValue;  // they travel packed in 16 bits
+    const int gxy = (int)(grid.x | grid.y << 16), nqkv = a.n_heads | a.n_kv_heads << 16;
     if (a.kv_bf16)
-        gemm_qkv_huge_kernel<uint16_t><<<grid, Huge::NT, 0, s>>>(wq, wk, wv, hi, lo, (int)n, (int)cols, a);
+        gemm_qkv_huge_kernel<uint16_t><<<grid, Huge::NT, 0, s>>>(wq, wk, wv, hi, lo, (int)n, (int)cols, gxy, nqkv, a);
     else
-        gemm_qkv_huge_kernel<float><<<grid, Huge::NT, 0, s>>>(wq, wk, wv, hi, lo, (int)n, (int)cols, a);
+        gemm_qkv_huge_kernel<float><<<grid, Huge::NT, 0, s>>>(wq, wk, wv, hi, lo, (int)n, (int)cols, gxy, nqkv, a);
     return hipGetLastError();
 }
 
@@ -792,7 +813,8 @@ hipError_t launch_gemm_qkv(hipStream_t s, const uint16_t *hi, const uint16_t *lo
                            const uint16_t *wk, const uint16_t *wv, const QkvPostArgs &a) {
     if (a.n == 0) return hipSuccess;
     if (!hi || !lo || !wq || !wk || !wv || a.head_dim != 128 || cols % BK || cols >= ((size_t)1 << 20) ||
-        a.n_heads < 1 || a.n_kv_heads < 1 || (a.n + Head::BM - 1) / Head::BM > 65535)
+        a.n_heads < 1 || a.n_kv_heads < 1 || (a.n + Head::BM - 1) / Head::BM > 65535 ||
+        a.n_heads + 2 * a.n_kv_heads > 0xffff)
         return hipErrorInvalidValue;
     // The planes as launch_gemm_qkv_huge takes them (a position read on the
     // device is the caller's to keep below plane_len).
@@ -800,10 +822,11 @@ hipError_t launch_gemm_qkv(hipStream_t s, const uint16_t *hi, const uint16_t *lo
                  (!a.pos_dev && (a.pos < 0 || a.pos + a.n > a.plane_len))))
         return hipErrorInvalidValue;
     dim3 grid((unsigned)(a.n_heads + 2 * a.n_kv_heads), (unsigned)((a.n + Head::BM - 1) / Head::BM));
+    const int gxy = (int)(grid.x | grid.y << 16), nqkv = a.n_heads | a.n_kv_heads << 16;
     if (a.kv_bf16)
-        gemm_qkv_kernel<uint16_t><<<grid, Head::NT, 0, s>>>(wq, wk, wv, hi, lo, a.n, (int)cols, a);
+        gemm_qkv_kernel<uint16_t><<<grid, Head::NT, 0, s>>>(wq, wk, wv, hi, lo, a.n, (int)cols, gxy, nqkv, a);
     else
-        gemm_qkv_kernel<float><<<grid, Head::NT, 0, s>>>(wq, wk, wv, hi, lo, a.n, (int)cols, a);
+        gemm_qkv_kernel<float><<<grid, Head::NT, 0, s>>>(wq, wk, wv, hi, lo, a.n, (int)cols, gxy, nqkv, a);
     return hipGetLastError();
 }
 
