@@ -820,7 +820,7 @@ struct GqaShape<float> {
 };
 
 template <typename KV>
-__global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void attn_gqa_kernel(AttnKernelArgs a, int n) {
+__global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void attn_gqa_kernel(int gxy, int n, int gnh, const float *__restrict__ q, AttnKernelArgs a) {
     constexpr bool F32 = sizeof(KV) == 4;
     constexpr int NW = GqaShape<KV>::NW, NT = 64 * NW, SETS = kGqaRows / 16 / NW, RW = 16 * SETS;
     constexpr int HD = 128, KT = kGqaKeys;
@@ -833,10 +833,12 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
     __shared__ uint4 vth[HD * VTS / 8], vtl[F32 ? HD * VTS / 8 : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int G = a.group, QT = kGqaRows / G;
+    // Leading arguments, preloaded: the grid's x | y << 16, the query rows,
+    // the group | q heads << 16 and q (a's own fields).
+    const int G = gnh & 0xffff, QT = kGqaRows / G;
     // Blocks in order of decreasing work (the last token tiles, which see
     // the most keys, first), as in attn_planes_kernel.
-    const int gx = (int)gridDim.x, gy = (int)gridDim.y, lin = (int)blockIdx.x + (int)blockIdx.y * gx;
+    const int gx = gxy & 0xffff, gy = gxy >> 16, lin = (int)blockIdx.x + (int)blockIdx.y * gx;
     const int g = lin % gy;
     const int t0 = (gx - 1 - lin / gy) * QT;
     const int nq = n - t0 < QT ? n - t0 : QT;
@@ -850,7 +852,7 @@ __global__ __launch_bounds__(64 * GqaShape<KV>::NW, 8 / GqaShape<KV>::NW) void a
         const int r = RW * wave + 16 * s + li;
         qloc[s] = r % QT;
         head[s] = g * G + r / QT;
-        const float *qp = a.q + ((long long)(t0 + (qloc[s] < nq ? qloc[s] : 0)) * a.n_heads + head[s]) * HD + 8 * lg;
+        const float *qp = q + ((long long)(t0 + (qloc[s] < nq ? qloc[s] : 0)) * (gnh >> 16) + head[s]) * HD + 8 * lg;
 #pragma unroll
         for (int c = 0; c < HD / 32; ++c) {
             float f[8];
@@ -1218,7 +1220,8 @@ struct PlaneRefs {
 // chunk c at c ^ (r & 15), V^T row r at c ^ ((r >> 1) & 7) (two 128-byte
 // rows share a bank line).
 template <int NW, int ROWS>
-__global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs a, PlaneRefs pl, int n) {
+__global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(int gxy, int n, int gnh, const float *__restrict__ q,
+                                                                 AttnKernelArgs a, PlaneRefs pl) {
     constexpr int SETS = ROWS / 16 / NW, RW = 16 * SETS;
     constexpr int SPW = 16 / NW;  // 1 KB spans a wave fills of each 16 KB tile
     constexpr int HD = 128, KT = kGqaKeys;
@@ -1231,12 +1234,13 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs 
     __shared__ Stage ring[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
-    const int G = a.group, QT = ROWS / G;
+    // Leading arguments as attn_gqa_kernel's.
+    const int G = gnh & 0xffff, QT = ROWS / G;
     // Blocks in order of decreasing work: a token tile attends to every key
     // up to its last query, so the last tiles have the most; launching them
     // first (every KV group's last tile, then the one before, ...) keeps the
     // lightest blocks for the end of the launch instead of the heaviest.
-    const int gx = (int)gridDim.x, gy = (int)gridDim.y, lin = (int)blockIdx.x + (int)blockIdx.y * gx;
+    const int gx = gxy & 0xffff, gy = gxy >> 16, lin = (int)blockIdx.x + (int)blockIdx.y * gx;
     const int g = lin % gy;
     const int t0 = (gx - 1 - lin / gy) * QT;
     const int nq = n - t0 < QT ? n - t0 : QT;
@@ -1248,7 +1252,7 @@ __global__ __launch_bounds__(64 * NW, 1) void attn_planes_kernel(AttnKernelArgs 
         const int r = RW * wave + 16 * s + li;
         qloc[s] = r % QT;
         head[s] = g * G + r / QT;
-        const float *qp = a.q + ((long long)(t0 + (qloc[s] < nq ? qloc[s] : 0)) * a.n_heads + head[s]) * HD + 8 * lg;
+        const float *qp = q + ((long long)(t0 + (qloc[s] < nq ? qloc[s] : 0)) * (gnh >> 16) + head[s]) * HD + 8 * lg;
 #pragma unroll
         for (int c = 0; c < HD / 32; ++c) {
             float f[8];
@@ -1476,10 +1480,12 @@ hipError_t launch_attention(hipStream_t s, const AttnKernelArgs &k, size_t n, si
         if (k.group >= 1 && k.group <= 8 && 8 % k.group == 0 && k.n_kv_heads * k.group == k.n_heads) {
             const int qt = kGqaRows / k.group;
             dim3 grid((unsigned)((n + qt - 1) / qt), (unsigned)k.n_kv_heads, (unsigned)k.nsplit);
+            if (grid.x > 0xffff || grid.y > 0xffff || k.n_heads > 0x7fff) return hipErrorInvalidValue;
+            const int gxy = (int)(grid.x | grid.y << 16), gnh = k.group | k.n_heads << 16;
             if (k.kv_bf16)
-                attn_gqa_kernel<uint16_t><<<grid, 64 * GqaShape<uint16_t>::NW, 0, s>>>(k, (int)n);
+                attn_gqa_kernel<uint16_t><<<grid, 64 * GqaShape<uint16_t>::NW, 0, s>>>(gxy, (int)n, gnh, k.q, k);
             else
-                attn_gqa_kernel<float><<<grid, 64 * GqaShape<float>::NW, 0, s>>>(k, (int)n);
+                attn_gqa_kernel<float><<<grid, 64 * GqaShape<float>::NW, 0, s>>>(gxy, (int)n, gnh, k.q, k);
         } else {
             dim3 grid((unsigned)((n + kMQT - 1) / kMQT), (unsigned)k.n_heads, (unsigned)k.nsplit);
             if (k.kv_bf16)
@@ -1558,10 +1564,12 @@ hipError_t launch_attention_planes(hipStream_t s, const AttnKernelArgs &k, size_
     const bool wide = k.nsplit == 1 && plane_rows_wide(n, k.group, k.n_kv_heads);
     const int qt = (wide ? kPlaneRowsWide : kGqaRows) / k.group;
     dim3 grid((unsigned)((n + qt - 1) / qt), (unsigned)k.n_kv_heads, (unsigned)k.nsplit);
+    if (grid.x > 0xffff || grid.y > 0xffff || k.n_heads > 0x7fff) return hipErrorInvalidValue;
+    const int gxy = (int)(grid.x | grid.y << 16), gnh = k.group | k.n_heads << 16;
     if (wide)
-        attn_planes_kernel<kPlaneWaves, kPlaneRowsWide><<<grid, 64 * kPlaneWaves, 0, s>>>(k, pr, (int)n);
+        attn_planes_kernel<kPlaneWaves, kPlaneRowsWide><<<grid, 64 * kPlaneWaves, 0, s>>>(gxy, (int)n, gnh, k.q, k, pr);
     else
-        attn_planes_kernel<kPlaneWaves, kGqaRows><<<grid, 64 * kPlaneWaves, 0, s>>>(k, pr, (int)n);
+        attn_planes_kernel<kPlaneWaves, kGqaRows><<<grid, 64 * kPlaneWaves, 0, s>>>(gxy, (int)n, gnh, k.q, k, pr);
     e = hipGetLastError();
     if (e != hipSuccess || k.nsplit == 1) return e;
     return launch_attn_combine(s, k.out, k.part_acc, k.part_ml, n * (size_t)k.n_heads, k.nsplit, 128, k.out_hi,

@@ -122,13 +122,17 @@ struct NormArgs {
 };
 
 template <int NV>
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
+// The fields the first loads need lead the parameters (preloaded into
+// SGPRs); the rest of a is read as the epilogue needs it.
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float *__restrict__ ax, const float *__restrict__ ay,
+                                                          const uint16_t *__restrict__ aw, size_t arows, size_t adim,
+                                                          size_t ay_stride, int any, NormArgs a) {
     const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= a.rows) return;
-    const size_t dim = a.dim;
-    float *xr = a.x + row * dim;
-    const float *yr = a.ny ? a.y + row * dim : nullptr;
+    if (row >= arows) return;
+    const size_t dim = adim;
+    float *xr = ax + row * dim;
+    const float *yr = any ? ay + row * dim : nullptr;
     float ss = 0.f;
     if (NV > 0) {
         float4 v[NV > 0 ? NV : 1], u[NV > 0 ? NV : 1];
@@ -138,10 +142,10 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
             const int i = lane + 64 * k;
             v[k] = reinterpret_cast<const float4 *>(xr)[i];
             if (yr) u[k] = reinterpret_cast<const float4 *>(yr)[i];
-            g[k] = reinterpret_cast<const uint2 *>(a.w)[i];
+            g[k] = reinterpret_cast<const uint2 *>(aw)[i];
         }
-        for (int z = 1; z < a.ny; ++z) {
-            const float4 *yz = reinterpret_cast<const float4 *>(yr + (size_t)z * a.y_stride);
+        for (int z = 1; z < any; ++z) {
+            const float4 *yz = reinterpret_cast<const float4 *>(yr + (size_t)z * ay_stride);
             float4 t[NV > 0 ? NV : 1];
 #pragma unroll
             for (int k = 0; k < NV; ++k) t[k] = yz[lane + 64 * k];
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
         float v = xr[i];
         if (yr) {
             float u = yr[i];
-            for (int z = 1; z < a.ny; ++z) u += yr[(size_t)z * a.y_stride + i];
+            for (int z = 1; z < any; ++z) u += yr[(size_t)z * ay_stride + i];
             v = v + u;
             xr[i] = v;
         }
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(NormArgs a) {
     ss = wave_sum(ss);
     const float scale = 1.0f / sqrtf(ss / (float)dim + a.eps);
     for (size_t i = lane; i < dim; i += 64) {
-        const float o = xr[i] * (scale * bf16_to_f32(a.w[i]));
+        const float o = xr[i] * (scale * bf16_to_f32(aw[i]));
         if (a.xb) a.xb[row * dim + i] = o;
         if (a.hi) split_bf16(o, a.hi[row * dim + i], a.lo[row * dim + i]);
     }
@@ -210,13 +214,13 @@ hipError_t launch_add_rmsnorm_parts(hipStream_t s, float *x, const float *y, int
                      ((uintptr_t)x | (uintptr_t)xb | (uintptr_t)a.y | (uintptr_t)w) % 16 == 0 &&
                      ((uintptr_t)hi | (uintptr_t)lo) % 8 == 0;
     switch (vec ? dim / 256 : 0) {
-    case 1: add_rmsnorm_kernel<1><<<grid, block, 0, s>>>(a); break;
-    case 2: add_rmsnorm_kernel<2><<<grid, block, 0, s>>>(a); break;
-    case 4: add_rmsnorm_kernel<4><<<grid, block, 0, s>>>(a); break;
-    case 8: add_rmsnorm_kernel<8><<<grid, block, 0, s>>>(a); break;
-    case 10: add_rmsnorm_kernel<10><<<grid, block, 0, s>>>(a); break;
-    case 16: add_rmsnorm_kernel<16><<<grid, block, 0, s>>>(a); break;
-    default: add_rmsnorm_kernel<0><<<grid, block, 0, s>>>(a); break;
+    case 1: add_rmsnorm_kernel<1><<<grid, block, 0, s>>>(a.x, a.y, a.w, a.rows, a.dim, a.y_stride, a.ny, a); break;
+    case 2: add_rmsnorm_kernel<2><<<grid, block, 0, s>>>(a.x, a.y, a.w, a.rows, a.dim, a.y_stride, a.ny, a); break;
+    case 4: add_rmsnorm_kernel<4><<<grid, block, 0, s>>>(a.x, a.y, a.w, a.rows, a.dim, a.y_stride, a.ny, a); break;
+    case 8: add_rmsnorm_kernel<8><<<grid, block, 0, s>>>(a.x, a.y, a.w, a.rows, a.dim, a.y_stride, a.ny, a); break;
+    case 10: add_rmsnorm_kernel<10><<<grid, block, 0, s>>>(a.x, a.y, a.w, a.rows, a.dim, a.y_stride, a.ny, a); break;
+    case 16: add_rmsnorm_kernel<16><<<grid, block, 0, s>>>(a.x, a.y, a.w, a.rows, a.dim, a.y_stride, a.ny, a); break;
+    default: add_rmsnorm_kernel<0><<<grid, block, 0, s>>>(a.x, a.y, a.w, a.rows, a.dim, a.y_stride, a.ny, a); break;
     }
     return hipGetLastError();
 }
