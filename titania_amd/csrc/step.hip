@@ -175,7 +175,7 @@ constexpr int kQkvRowsPerWave = 4;
 // launch_step_qkv, published as (value | epoch << 32) words.
 template <int CPL>
 __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, const Rows &rows, int n_rows,
-                                            int cols, unsigned epoch) {
+                                            int cols) {
     constexpr int RPW = kQkvRowsPerWave, RPB = RPW * kWaves;
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
@@ -197,6 +197,10 @@ __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const Gemv
         for (int c = 0; c < CPL; ++c) acc = dot8(xs, w[r][c], c * 64 + lane, acc);
         res[r] = wave_sum_dpp(acc);
     }
+    // The epoch, read only now: the weight requests above wait on nothing
+    // (at the kernel's start its two dependent reads, the state's address
+    // and then its epoch, would hold them back).
+    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
         if (lane == r && r0 + r < n_rows)
@@ -208,8 +212,8 @@ template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_GEMV_HEAD, StepQkvAttnArgs q, GemvArgs a) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
     const int ngemv = (n_rows + RPB - 1) / RPB;
-    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
+        const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
         // `chunks` blocks per q head, one per pass of cached rows: the heads
         // of a KV group attend in parallel (each reads the group's rows), the
         // group's first head appends; each head's first chunk merges.
@@ -218,7 +222,7 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_GEMV_HEAD, StepQk
         attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
         return;
     }
-    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, epoch);
+    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols);
 }
 
 template <int CPL, int G>
@@ -268,13 +272,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream
 void qkv_stream_kernel(TH_GEMV_HEAD, StepQkvAttnArgs q, GemvArgs a, long long chunk) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
     const int ngemv = (n_rows + RPB - 1) / RPB;
-    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
     if ((int)blockIdx.x >= ngemv) {
+        const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
         const int b = blockIdx.x - ngemv;
         attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, q.words, epoch, q.err);
         return;
     }
-    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, epoch);
+    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols);
 }
 
 template <int CPL, int G>
