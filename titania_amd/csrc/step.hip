@@ -173,9 +173,19 @@ constexpr int kQkvRowsPerWave = 4;
 
 // The GEMV blocks of the q/k/v + attention launches: the q/k/v rows of
 // launch_step_qkv, published as (value | epoch << 32) words.
+// The q/k/v + attention launches lead with the GEMV head, the columns packed
+// with the layer (cols | layer << 16), then the exchange words and the step
+// state: all 14 dwords preloaded, so that the GEMV blocks fetch no kernel
+// argument before their weight requests and publish without one either.
+#define TH_QKV_HEAD                                                                                        \
+    const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int c0, \
+        int c1, int n_rows, int cols_layer, unsigned long long *words, const StepState *st
+#define TH_QKV_HEAD_OF(q, a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], (a).rows.count[0], \
+                             (a).rows.count[1], (a).n_rows, (a).cols | (q).layer << 16, (q).words, (q).st
+
 template <int CPL>
-__device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, const Rows &rows, int n_rows,
-                                            int cols) {
+__device__ __forceinline__ void qkv_publish(const GemvArgs &a, const Rows &rows, int n_rows, int cols,
+                                            unsigned long long *words, const StepState *st, int layer) {
     constexpr int RPW = kQkvRowsPerWave, RPB = RPW * kWaves;
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
@@ -197,32 +207,30 @@ __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const Gemv
         for (int c = 0; c < CPL; ++c) acc = dot8(xs, w[r][c], c * 64 + lane, acc);
         res[r] = wave_sum_dpp(acc);
     }
-    // The epoch, read only now: the weight requests above wait on nothing
-    // (at the kernel's start its two dependent reads, the state's address
-    // and then its epoch, would hold them back).
-    const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
+    // The epoch, read only now: the weight requests above wait on nothing.
+    const unsigned epoch = st->epoch * 64u + (unsigned)layer + 1u;
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
         if (lane == r && r0 + r < n_rows)
-            __hip_atomic_store(q.words + r0 + r, ((unsigned long long)epoch << 32) | __float_as_uint(res[r]),
+            __hip_atomic_store(words + r0 + r, ((unsigned long long)epoch << 32) | __float_as_uint(res[r]),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int CPL, int G, typename KV>
-__global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_GEMV_HEAD, StepQkvAttnArgs q, GemvArgs a) {
+__global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_QKV_HEAD, StepQkvAttnArgs q, GemvArgs a) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
-    const int ngemv = (n_rows + RPB - 1) / RPB;
+    const int ngemv = (n_rows + RPB - 1) / RPB, cols = cols_layer & 0xffff, layer = cols_layer >> 16;
     if ((int)blockIdx.x >= ngemv) {
-        const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
+        const unsigned epoch = st->epoch * 64u + (unsigned)layer + 1u;
         // `chunks` blocks per q head, one per pass of cached rows: the heads
         // of a KV group attend in parallel (each reads the group's rows), the
         // group's first head appends; each head's first chunk merges.
         const int b = blockIdx.x - ngemv, h = b / q.chunks, c = b % q.chunks, g = h / G;
-        unsigned long long *xw = q.words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
-        attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
+        unsigned long long *xw = words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
+        attend_wave4<KV>(q.at, g, h, h % G == 0, c, words, epoch, q.err, xw, q.chunks);
         return;
     }
-    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols);
+    qkv_publish<CPL>(a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, words, st, layer);
 }
 
 template <int CPL, int G>
@@ -231,9 +239,9 @@ hipError_t qkv_attn_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvAr
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB + q.at.n_heads * q.chunks));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
-        qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a);
+        qkv_attn_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(TH_QKV_HEAD_OF(q, a), q, a);
     else
-        qkv_attn_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a);
+        qkv_attn_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(TH_QKV_HEAD_OF(q, a), q, a);
     return hipGetLastError();
 }
 
@@ -269,16 +277,16 @@ void step_attention_stream_kernel(StepAttnArgs a, long long chunk) {
 // and the GEMV blocks never wait, so the attention blocks' polls always end.
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<G, KV>())))
-void qkv_stream_kernel(TH_GEMV_HEAD, StepQkvAttnArgs q, GemvArgs a, long long chunk) {
+void qkv_stream_kernel(TH_QKV_HEAD, StepQkvAttnArgs q, GemvArgs a, long long chunk) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
-    const int ngemv = (n_rows + RPB - 1) / RPB;
+    const int ngemv = (n_rows + RPB - 1) / RPB, cols = cols_layer & 0xffff, layer = cols_layer >> 16;
     if ((int)blockIdx.x >= ngemv) {
-        const unsigned epoch = q.st->epoch * 64u + (unsigned)q.layer + 1u;
+        const unsigned epoch = st->epoch * 64u + (unsigned)layer + 1u;
         const int b = blockIdx.x - ngemv;
-        attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, q.words, epoch, q.err);
+        attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, words, epoch, q.err);
         return;
     }
-    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols);
+    qkv_publish<CPL>(a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, words, st, layer);
 }
 
 template <int CPL, int G>
@@ -288,9 +296,9 @@ hipError_t qkv_stream_launch(hipStream_t s, const StepQkvAttnArgs &q, const Gemv
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB + q.at.n_kv_heads * q.at.nsplit));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
-        qkv_stream_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a, chunk);
+        qkv_stream_kernel<CPL, G, uint16_t><<<grid, kThreads, lds, s>>>(TH_QKV_HEAD_OF(q, a), q, a, chunk);
     else
-        qkv_stream_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(TH_GEMV_HEAD_OF(a), q, a, chunk);
+        qkv_stream_kernel<CPL, G, float><<<grid, kThreads, lds, s>>>(TH_QKV_HEAD_OF(q, a), q, a, chunk);
     return hipGetLastError();
 }
 
@@ -475,8 +483,10 @@ GemvArgs qkv_gemv_args(const StepQkvArgs &k) {
 
 hipError_t launch_step_qkv_stream(hipStream_t s, const StepQkvAttnArgs &q) {
     const StepQkvArgs &k = q.qkv;
-    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit < 1 ||
-        (q.at.nsplit > 1 && (!q.at.part_acc || !q.at.part_ml)) || (q.at.nsplit == 1 && !q.at.out))
+    // layer + 1 < 64 keeps the epoch words of successive steps apart (and
+    // packs with the columns).
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.layer < 0 || q.layer >= 63 ||
+        q.at.nsplit < 1 || (q.at.nsplit > 1 && (!q.at.part_acc || !q.at.part_ml)) || (q.at.nsplit == 1 && !q.at.out))
         return hipErrorInvalidValue;
     const GemvArgs a = qkv_gemv_args(k);
     const int g = q.at.n_heads / q.at.n_kv_heads;
@@ -491,7 +501,8 @@ hipError_t launch_step_qkv_stream(hipStream_t s, const StepQkvAttnArgs &q) {
 hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
     const StepQkvArgs &k = q.qkv;
     const long long max_len = q.at.head_stride / 128;
-    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.at.nsplit != 1 || q.chunks < 1 ||
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.layer < 0 || q.layer >= 63 ||
+        q.at.nsplit != 1 || q.chunks < 1 ||
         q.chunks != step_qkv_attn_chunks((size_t)max_len, q.at.kv_bf16, q.at.n_heads))
         return hipErrorInvalidValue;
     const GemvArgs a = qkv_gemv_args(k);
