@@ -49,11 +49,16 @@ struct GemvArgs {
 // rows and columns), which the code object asks to have preloaded into SGPRs
 // at wave launch: the weight loads then issue without waiting on a fetch of
 // the kernel arguments. The same fields stay in GemvArgs for the host side.
-#define TH_GEMV_HEAD                                                                                       \
+#define TH_ROWS_HEAD                                                                                       \
     const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int c0, \
-        int c1, int n_rows, int cols
-#define TH_GEMV_HEAD_OF(a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], (a).rows.count[0], (a).rows.count[1], \
-                           (a).n_rows, (a).cols
+        int c1, int n_rows
+#define TH_ROWS_HEAD_OF(a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], (a).rows.count[0], (a).rows.count[1], \
+                           (a).n_rows
+// The plain GEMVs also take the input vectors' addresses there, so that the
+// input requests follow the weight requests at once (14 dwords: what gfx950
+// preloads).
+#define TH_GEMV_HEAD TH_ROWS_HEAD, int cols, const float *__restrict__ in_a, const float *__restrict__ in_b
+#define TH_GEMV_HEAD_OF(a) TH_ROWS_HEAD_OF(a), (a).cols, (a).a, (a).b
 
 // Where kStore writes row r.
 __device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
@@ -77,6 +82,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a
     const int r0 = blockIdx.x * RPB + wave * RPW;
     // For paired rows (gate j, up j), a wave takes j and j + half.
     const int half = n_rows / 2;
+    // The input's requests go first (their addresses are preloaded): its
+    // sum, and the RMSNorm's reduction, then wait only for them, while the
+    // weight rows stream in behind.
+    constexpr int NV = (CPL * 128 + kThreads - 1) / kThreads;
+    InputRegs<NV> in;
+    load_input(in, in_a, in_b, cols);
     uint4 w[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -88,8 +99,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a
 #pragma unroll
         for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt_row(p, c * 64 + lane);
     }
-    build_input<PRO == kNormSum, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, cols, a.gain, a.eps, a.x_out,
-                                                                        red);
+    finish_input<PRO == kNormSum>(in, xs, in_b != nullptr, cols, a.gain, a.eps, a.x_out, red);
     float res[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -177,11 +187,8 @@ constexpr int kQkvRowsPerWave = 4;
 // with the layer (cols | layer << 16), then the exchange words and the step
 // state: all 14 dwords preloaded, so that the GEMV blocks fetch no kernel
 // argument before their weight requests and publish without one either.
-#define TH_QKV_HEAD                                                                                        \
-    const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int c0, \
-        int c1, int n_rows, int cols_layer, unsigned long long *words, const StepState *st
-#define TH_QKV_HEAD_OF(q, a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], (a).rows.count[0], \
-                             (a).rows.count[1], (a).n_rows, (a).cols | (q).layer << 16, (q).words, (q).st
+#define TH_QKV_HEAD TH_ROWS_HEAD, int cols_layer, unsigned long long *words, const StepState *st
+#define TH_QKV_HEAD_OF(q, a) TH_ROWS_HEAD_OF(a), (a).cols | (q).layer << 16, (q).words, (q).st
 
 template <int CPL>
 __device__ __forceinline__ void qkv_publish(const GemvArgs &a, const Rows &rows, int n_rows, int cols,

@@ -19,29 +19,44 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
-// Builds the block's f32 input in LDS: x = a (+ b), optionally RMSNorm'd with
-// gain g (model/cpu.rs:85-94); block 0 keeps the un-normalized sum in x_out.
-// Every thread issues all its loads (NV float4 of a, of b
-// and 4-element groups of g) before using any, so the input costs one memory
-// round trip rather than one per loop iteration.
-template <bool NORM, int NV>
-__device__ __forceinline__ void build_input(float *xs, const float *a, const float *b, int n, const uint16_t *g,
-                                            float eps, float *x_out, float *red) {
-    const int tid = threadIdx.x;
-    const int n4 = n >> 2;
-    const float4 *a4 = reinterpret_cast<const float4 *>(a);
-    const float4 *b4 = reinterpret_cast<const float4 *>(b);
-    const uint2 *g4 = reinterpret_cast<const uint2 *>(g);
+// The block's input x = a (+ b) in registers: NV float4 of each a thread.
+template <int NV>
+struct InputRegs {
     float4 va[NV], vb[NV];
-    uint2 vg[NV];
+};
+
+// Issues the loads of the block's input vectors a (and b, if not null).
+template <int NV>
+__device__ __forceinline__ void load_input(InputRegs<NV> &in, const float *a, const float *b, int n) {
+    const int tid = threadIdx.x, n4 = n >> 2;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int i = tid + k * kThreads;
         if (i < n4) {
-            va[k] = a4[i];
-            if (b) vb[k] = b4[i];
-            if (NORM) vg[k] = g4[i];
+            in.va[k] = reinterpret_cast<const float4 *>(a)[i];
+            if (b) in.vb[k] = reinterpret_cast<const float4 *>(b)[i];
         }
+    }
+}
+
+// Builds the block's f32 input in LDS from the loaded vectors: x = a (+ b
+// when has_b), optionally RMSNorm'd with gain g (model/cpu.rs:85-94); block 0
+// keeps the un-normalized sum in x_out. Every thread issues all its gain loads
+// before using any input, so the input costs one memory round trip rather
+// than one per loop iteration.
+template <bool NORM, int NV>
+__device__ __forceinline__ void finish_input(InputRegs<NV> &in, float *xs, bool has_b, int n, const uint16_t *g,
+                                             float eps, float *x_out, float *red) {
+    const int tid = threadIdx.x;
+    const int n4 = n >> 2;
+    const uint2 *g4 = reinterpret_cast<const uint2 *>(g);
+    float4 *va = in.va;
+    const float4 *vb = in.vb;
+    uint2 vg[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int i = tid + k * kThreads;
+        if (NORM && i < n4) vg[k] = g4[i];
     }
     float ss = 0.f;
 #pragma unroll
@@ -49,7 +64,7 @@ __device__ __forceinline__ void build_input(float *xs, const float *a, const flo
         const int i = tid + k * kThreads;
         if (i < n4) {
             float4 v = va[k];
-            if (b) {
+            if (has_b) {
                 v.x = v.x + vb[k].x;
                 v.y = v.y + vb[k].y;
                 v.z = v.z + vb[k].z;
@@ -90,6 +105,15 @@ __device__ __forceinline__ void build_input(float *xs, const float *a, const flo
         }
     }
     __syncthreads();
+}
+
+// load_input and finish_input in one: the input's loads, then its use.
+template <bool NORM, int NV>
+__device__ __forceinline__ void build_input(float *xs, const float *a, const float *b, int n, const uint16_t *g,
+                                            float eps, float *x_out, float *red) {
+    InputRegs<NV> in;
+    load_input(in, a, b, n);
+    finish_input<NORM>(in, xs, b != nullptr, n, g, eps, x_out, red);
 }
 
 __device__ __forceinline__ float dot8(const float *xs, const uint4 &w, int col, float acc) {
