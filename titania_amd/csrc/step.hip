@@ -44,21 +44,15 @@ struct GemvArgs {
     float *outs[3];
 };
 
-// The fields a GEMV block needs for its first weight loads travel as leading
-// scalar kernel arguments (the matrices' bases, the first two row counts, the
-// rows and columns), which the code object asks to have preloaded into SGPRs
-// at wave launch: the weight loads then issue without waiting on a fetch of
+// The fields a GEMV block needs for its first loads travel as leading scalar
+// kernel arguments (the matrices' bases, the first two row counts, the rows
+// and columns, the input vectors' addresses: 14 dwords, what gfx950
+// preloads), which the code object asks to have preloaded into SGPRs at wave
+// launch: the input and weight loads then issue without waiting on a fetch of
 // the kernel arguments. The same fields stay in GemvArgs for the host side.
-#define TH_ROWS_HEAD                                                                                       \
+#define TH_GEMV_HEAD                                                                                       \
     const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int c0, \
-        int c1, int n_rows
-#define TH_ROWS_HEAD_OF(a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], (a).rows.count[0], (a).rows.count[1], \
-                           (a).n_rows
-// The plain GEMVs also take the input vectors' addresses there, so that the
-// input requests follow the weight requests at once (14 dwords: what gfx950
-// preloads).
-#define TH_GEMV_HEAD TH_ROWS_HEAD, int cols, const float *__restrict__ in_a, const float *__restrict__ in_b
-#define TH_GEMV_HEAD_OF(a) TH_ROWS_HEAD_OF(a), (a).cols, (a).a, (a).b
+        int c1, int n_rows, int cols, const float *__restrict__ in_a, const float *__restrict__ in_b
 
 // Where kStore writes row r.
 __device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
@@ -69,11 +63,17 @@ __device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
     return a.outs[2] + (r - a.rows.count[1]);
 }
 
+constexpr bool gemv_early_gain(Prologue pro, Epilogue epi) { return pro == kNormSum && epi != kStore; }
+
 // One block: RPW rows per wave, CPL 16-byte chunks per lane per row.
 template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a) {
     static_assert(EPI != kSiluPairs || RPW % 2 == 0, "a wave holds whole (gate, up) pairs");
-    const Rows rows{{w0, w1, w2}, {c0, c1, 0}};
+    // The RMSNorm launches of one or two matrices (gate/up, the output
+    // projection) take the gains' address in the third matrix's slot and
+    // request them with the input, ahead of the weight rows.
+    constexpr bool kEarlyGain = gemv_early_gain(PRO, EPI);
+    const Rows rows{{w0, w1, kEarlyGain ? nullptr : w2}, {c0, c1, 0}};
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     __shared__ uint64_t red64[kWaves];
@@ -88,6 +88,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a
     constexpr int NV = (CPL * 128 + kThreads - 1) / kThreads;
     InputRegs<NV> in;
     load_input(in, in_a, in_b, cols);
+    if constexpr (kEarlyGain) load_gain(in, w2, cols);
     uint4 w[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -99,7 +100,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a
 #pragma unroll
         for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt_row(p, c * 64 + lane);
     }
-    finish_input<PRO == kNormSum>(in, xs, in_b != nullptr, cols, a.gain, a.eps, a.x_out, red);
+    if constexpr (PRO == kNormSum && !kEarlyGain) load_gain(in, a.gain, cols);
+    finish_input<PRO == kNormSum>(in, xs, in_b != nullptr, cols, a.eps, a.x_out, red);
     float res[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -144,7 +146,10 @@ template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
 hipError_t gemv_launch(hipStream_t s, const GemvArgs &a) {
     constexpr int RPB = RPW * kWaves;
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB));
-    gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, a.cols * sizeof(float), s>>>(TH_GEMV_HEAD_OF(a), a);
+    if (gemv_early_gain(PRO, EPI) && a.rows.count[0] + a.rows.count[1] != a.n_rows) return hipErrorInvalidValue;
+    gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, a.cols * sizeof(float), s>>>(
+        a.rows.base[0], a.rows.base[1], gemv_early_gain(PRO, EPI) ? a.gain : a.rows.base[2], a.rows.count[0],
+        a.rows.count[1], a.n_rows, a.cols, a.a, a.b, a);
     return hipGetLastError();
 }
 
@@ -183,21 +188,37 @@ constexpr int kQkvRowsPerWave = 4;
 
 // The GEMV blocks of the q/k/v + attention launches: the q/k/v rows of
 // launch_step_qkv, published as (value | epoch << 32) words.
-// The q/k/v + attention launches lead with the GEMV head, the columns packed
-// with the layer (cols | layer << 16), then the exchange words and the step
-// state: all 14 dwords preloaded, so that the GEMV blocks fetch no kernel
-// argument before their weight requests and publish without one either.
-#define TH_QKV_HEAD TH_ROWS_HEAD, int cols_layer, unsigned long long *words, const StepState *st
-#define TH_QKV_HEAD_OF(q, a) TH_ROWS_HEAD_OF(a), (a).cols | (q).layer << 16, (q).words, (q).st
+// The q/k/v + attention launches lead with the three matrices' bases, the q
+// and k row counts packed (q | k << 16; v has k's), the columns packed with
+// the layer (cols | layer << 16), the input vectors' and the RMSNorm gains'
+// addresses: 14 dwords, all preloaded, so that the GEMV blocks request their
+// input, gains and weight rows without fetching a kernel argument.
+#define TH_QKV_HEAD                                                                                        \
+    const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int rows01, \
+        int cols_layer, const float *__restrict__ in_a, const float *__restrict__ in_b,                         \
+        const uint16_t *__restrict__ gain
+#define TH_QKV_HEAD_OF(q, a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], \
+                             (a).rows.count[0] | (a).rows.count[1] << 16, (a).cols | (q).layer << 16, (a).a, (a).b, \
+                             (a).gain
+// Unpacks TH_QKV_HEAD's counts.
+#define TH_QKV_HEAD_UNPACK                                                                          \
+    const int c0 = rows01 & 0xffff, c1 = rows01 >> 16, n_rows = c0 + 2 * c1, cols = cols_layer & 0xffff, \
+              layer = cols_layer >> 16
 
 template <int CPL>
-__device__ __forceinline__ void qkv_publish(const GemvArgs &a, const Rows &rows, int n_rows, int cols,
-                                            unsigned long long *words, const StepState *st, int layer) {
+__device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, const Rows &rows, int n_rows,
+                                            int cols, const float *in_a, const float *in_b, const uint16_t *gain,
+                                            int layer) {
     constexpr int RPW = kQkvRowsPerWave, RPB = RPW * kWaves;
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r0 = blockIdx.x * RPB + wave * RPW;
+    // The input and its gains first, then the weight rows (as gemv_kernel).
+    constexpr int NV = (CPL * 128 + kThreads - 1) / kThreads;
+    InputRegs<NV> in;
+    load_input(in, in_a, in_b, cols);
+    load_gain(in, gain, cols);
     uint4 w[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -205,7 +226,7 @@ __device__ __forceinline__ void qkv_publish(const GemvArgs &a, const Rows &rows,
 #pragma unroll
         for (int c = 0; c < CPL; ++c) w[r][c] = ld_nt_row(p, c * 64 + lane);
     }
-    build_input<true, (CPL * 128 + kThreads - 1) / kThreads>(xs, a.a, a.b, cols, a.gain, a.eps, a.x_out, red);
+    finish_input<true>(in, xs, in_b != nullptr, cols, a.eps, a.x_out, red);
     float res[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -215,29 +236,30 @@ __device__ __forceinline__ void qkv_publish(const GemvArgs &a, const Rows &rows,
         res[r] = wave_sum_dpp(acc);
     }
     // The epoch, read only now: the weight requests above wait on nothing.
-    const unsigned epoch = st->epoch * 64u + (unsigned)layer + 1u;
+    const unsigned epoch = q.st->epoch * 64u + (unsigned)layer + 1u;
 #pragma unroll
     for (int r = 0; r < RPW; ++r)
         if (lane == r && r0 + r < n_rows)
-            __hip_atomic_store(words + r0 + r, ((unsigned long long)epoch << 32) | __float_as_uint(res[r]),
+            __hip_atomic_store(q.words + r0 + r, ((unsigned long long)epoch << 32) | __float_as_uint(res[r]),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_QKV_HEAD, StepQkvAttnArgs q, GemvArgs a) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
-    const int ngemv = (n_rows + RPB - 1) / RPB, cols = cols_layer & 0xffff, layer = cols_layer >> 16;
+    TH_QKV_HEAD_UNPACK;
+    const int ngemv = (n_rows + RPB - 1) / RPB;
     if ((int)blockIdx.x >= ngemv) {
-        const unsigned epoch = st->epoch * 64u + (unsigned)layer + 1u;
+        const unsigned epoch = q.st->epoch * 64u + (unsigned)layer + 1u;
         // `chunks` blocks per q head, one per pass of cached rows: the heads
         // of a KV group attend in parallel (each reads the group's rows), the
         // group's first head appends; each head's first chunk merges.
         const int b = blockIdx.x - ngemv, h = b / q.chunks, c = b % q.chunks, g = h / G;
-        unsigned long long *xw = words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
-        attend_wave4<KV>(q.at, g, h, h % G == 0, c, words, epoch, q.err, xw, q.chunks);
+        unsigned long long *xw = q.words + q.qkv.q_rows + 2 * q.qkv.kv_rows;
+        attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
         return;
     }
-    qkv_publish<CPL>(a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, words, st, layer);
+    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, in_a, in_b, gain, layer);
 }
 
 template <int CPL, int G>
@@ -286,14 +308,15 @@ template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(stream_waves_per_eu<G, KV>())))
 void qkv_stream_kernel(TH_QKV_HEAD, StepQkvAttnArgs q, GemvArgs a, long long chunk) {
     constexpr int RPB = kQkvRowsPerWave * kWaves;
-    const int ngemv = (n_rows + RPB - 1) / RPB, cols = cols_layer & 0xffff, layer = cols_layer >> 16;
+    TH_QKV_HEAD_UNPACK;
+    const int ngemv = (n_rows + RPB - 1) / RPB;
     if ((int)blockIdx.x >= ngemv) {
-        const unsigned epoch = st->epoch * 64u + (unsigned)layer + 1u;
+        const unsigned epoch = q.st->epoch * 64u + (unsigned)layer + 1u;
         const int b = blockIdx.x - ngemv;
-        attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, words, epoch, q.err);
+        attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, q.words, epoch, q.err);
         return;
     }
-    qkv_publish<CPL>(a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, words, st, layer);
+    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, in_a, in_b, gain, layer);
 }
 
 template <int CPL, int G>
@@ -486,13 +509,19 @@ GemvArgs qkv_gemv_args(const StepQkvArgs &k) {
     return a;
 }
 
+// Whether TH_QKV_HEAD's packed fields hold the launch's counts: rows and
+// columns below 2^16; layer + 1 < 64, which also keeps the epoch words of
+// successive steps apart.
+bool qkv_head_packs(const StepQkvAttnArgs &q) {
+    return q.qkv.q_rows > 0 && q.qkv.q_rows < 65536 && q.qkv.kv_rows > 0 && q.qkv.kv_rows < 32768 &&
+           q.qkv.hidden < 65536 && q.layer >= 0 && q.layer < 63;
+}
+
 }  // namespace
 
 hipError_t launch_step_qkv_stream(hipStream_t s, const StepQkvAttnArgs &q) {
     const StepQkvArgs &k = q.qkv;
-    // layer + 1 < 64 keeps the epoch words of successive steps apart (and
-    // packs with the columns).
-    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.layer < 0 || q.layer >= 63 ||
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || !qkv_head_packs(q) ||
         q.at.nsplit < 1 || (q.at.nsplit > 1 && (!q.at.part_acc || !q.at.part_ml)) || (q.at.nsplit == 1 && !q.at.out))
         return hipErrorInvalidValue;
     const GemvArgs a = qkv_gemv_args(k);
@@ -508,7 +537,7 @@ hipError_t launch_step_qkv_stream(hipStream_t s, const StepQkvAttnArgs &q) {
 hipError_t launch_step_qkv_attn(hipStream_t s, const StepQkvAttnArgs &q) {
     const StepQkvArgs &k = q.qkv;
     const long long max_len = q.at.head_stride / 128;
-    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || q.layer < 0 || q.layer >= 63 ||
+    if (!step_qkv_attn_supported(k.hidden, q.at.n_heads, q.at.n_kv_heads) || !qkv_head_packs(q) ||
         q.at.nsplit != 1 || q.chunks < 1 ||
         q.chunks != step_qkv_attn_chunks((size_t)max_len, q.at.kv_bf16, q.at.n_heads))
         return hipErrorInvalidValue;

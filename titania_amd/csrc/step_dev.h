@@ -19,10 +19,12 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
-// The block's input x = a (+ b) in registers: NV float4 of each a thread.
+// The block's input x = a (+ b) in registers, NV float4 of each a thread,
+// and the RMSNorm gains of those elements.
 template <int NV>
 struct InputRegs {
     float4 va[NV], vb[NV];
+    uint2 vg[NV];
 };
 
 // Issues the loads of the block's input vectors a (and b, if not null).
@@ -39,25 +41,30 @@ __device__ __forceinline__ void load_input(InputRegs<NV> &in, const float *a, co
     }
 }
 
-// Builds the block's f32 input in LDS from the loaded vectors: x = a (+ b
-// when has_b), optionally RMSNorm'd with gain g (model/cpu.rs:85-94); block 0
-// keeps the un-normalized sum in x_out. Every thread issues all its gain loads
-// before using any input, so the input costs one memory round trip rather
-// than one per loop iteration.
-template <bool NORM, int NV>
-__device__ __forceinline__ void finish_input(InputRegs<NV> &in, float *xs, bool has_b, int n, const uint16_t *g,
-                                             float eps, float *x_out, float *red) {
-    const int tid = threadIdx.x;
-    const int n4 = n >> 2;
-    const uint2 *g4 = reinterpret_cast<const uint2 *>(g);
-    float4 *va = in.va;
-    const float4 *vb = in.vb;
-    uint2 vg[NV];
+// Issues the loads of the bf16 RMSNorm gains g of the block's input.
+template <int NV>
+__device__ __forceinline__ void load_gain(InputRegs<NV> &in, const uint16_t *g, int n) {
+    const int tid = threadIdx.x, n4 = n >> 2;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int i = tid + k * kThreads;
-        if (NORM && i < n4) vg[k] = g4[i];
+        if (i < n4) in.vg[k] = reinterpret_cast<const uint2 *>(g)[i];
     }
+}
+
+// Builds the block's f32 input in LDS from the loaded vectors: x = a (+ b
+// when has_b), optionally RMSNorm'd with the loaded gains (model/cpu.rs:85-94);
+// block 0 keeps the un-normalized sum in x_out. All loads are issued before
+// any is used, so the input costs one memory round trip rather than one per
+// loop iteration.
+template <bool NORM, int NV>
+__device__ __forceinline__ void finish_input(InputRegs<NV> &in, float *xs, bool has_b, int n, float eps,
+                                             float *x_out, float *red) {
+    const int tid = threadIdx.x;
+    const int n4 = n >> 2;
+    float4 *va = in.va;
+    const float4 *vb = in.vb;
+    const uint2 *vg = in.vg;
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -113,7 +120,8 @@ __device__ __forceinline__ void build_input(float *xs, const float *a, const flo
                                             float eps, float *x_out, float *red) {
     InputRegs<NV> in;
     load_input(in, a, b, n);
-    finish_input<NORM>(in, xs, b != nullptr, n, g, eps, x_out, red);
+    if (NORM) load_gain(in, g, n);
+    finish_input<NORM>(in, xs, b != nullptr, n, eps, x_out, red);
 }
 
 __device__ __forceinline__ float dot8(const float *xs, const uint4 &w, int col, float acc) {
