@@ -176,15 +176,23 @@ hipError_t gemv_dispatch(hipStream_t s, const GemvArgs &a) {
     }
 }
 
-// The q/k/v rows of launch_step_qkv (kQkvRowsPerWave per wave) published as
-// epoch words by the first blocks, and after them one block per q head and
-// chunk of the cache that attends from those words. Blocks start in index order and the GEMV blocks never wait, so
-// the attention blocks' polls always end.
-// Rows a wave of the q/k/v GEMV blocks in qkv_attn_kernel (Qwen3-0.6B step:
-// 0.6114 ms with 2, 0.6094 with 4, 0.645 with 1; with the branch-free P.V
-// loop, 0.5990 with 4 and 0.5975 with 5; with non-temporal weight loads,
-// 0.5673 / 0.5651 / 0.5640 / 0.5693 ms with 2 / 3 / 4 / 5).
+// The q/k/v rows of launch_step_qkv published as epoch words by the first
+// blocks, and after them one block per q head and chunk of the cache that
+// attends from those words. Blocks start in index order and the GEMV blocks
+// never wait, so the attention blocks' polls always end.
+// Rows a wave of the q/k/v GEMV blocks (Qwen3-0.6B step: 0.6114 ms with 2,
+// 0.6094 with 4, 0.645 with 1; with the branch-free P.V loop, 0.5990 with 4
+// and 0.5975 with 5; with non-temporal weight loads, 0.5673 / 0.5651 /
+// 0.5640 / 0.5693 ms with 2 / 3 / 4 / 5; with the input requested ahead of
+// the weights, 0.5145 / 0.5178 / 0.5113 ms with 3 / 4 / 5, while five slowed
+// the streaming launch at 4K positions, 0.761 -> 0.804 ms, and the Qwen3-4B
+// shape, 1.674 -> 1.717 ms).
 constexpr int kQkvRowsPerWave = 4;
+// Those of qkv_attn_kernel for rows of CPL 512-column spans.
+template <int CPL>
+constexpr int qkv_attn_rows_per_wave() {
+    return CPL <= 2 ? 5 : kQkvRowsPerWave;
+}
 
 // The GEMV blocks of the q/k/v + attention launches: the q/k/v rows of
 // launch_step_qkv, published as (value | epoch << 32) words.
@@ -205,11 +213,11 @@ constexpr int kQkvRowsPerWave = 4;
     const int c0 = rows01 & 0xffff, c1 = rows01 >> 16, n_rows = c0 + 2 * c1, cols = cols_layer & 0xffff, \
               layer = cols_layer >> 16
 
-template <int CPL>
+template <int CPL, int RPW>
 __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, const Rows &rows, int n_rows,
                                             int cols, const float *in_a, const float *in_b, const uint16_t *gain,
                                             int layer) {
-    constexpr int RPW = kQkvRowsPerWave, RPB = RPW * kWaves;
+    constexpr int RPB = RPW * kWaves;
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -246,7 +254,7 @@ __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const Gemv
 
 template <int CPL, int G, typename KV>
 __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_QKV_HEAD, StepQkvAttnArgs q, GemvArgs a) {
-    constexpr int RPB = kQkvRowsPerWave * kWaves;
+    constexpr int RPW = qkv_attn_rows_per_wave<CPL>(), RPB = RPW * kWaves;
     TH_QKV_HEAD_UNPACK;
     const int ngemv = (n_rows + RPB - 1) / RPB;
     if ((int)blockIdx.x >= ngemv) {
@@ -259,12 +267,12 @@ __global__ __launch_bounds__(kThreads) void qkv_attn_kernel(TH_QKV_HEAD, StepQkv
         attend_wave4<KV>(q.at, g, h, h % G == 0, c, q.words, epoch, q.err, xw, q.chunks);
         return;
     }
-    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, in_a, in_b, gain, layer);
+    qkv_publish<CPL, RPW>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, in_a, in_b, gain, layer);
 }
 
 template <int CPL, int G>
 hipError_t qkv_attn_launch(hipStream_t s, const StepQkvAttnArgs &q, const GemvArgs &a) {
-    constexpr int RPB = kQkvRowsPerWave * kWaves;
+    constexpr int RPB = qkv_attn_rows_per_wave<CPL>() * kWaves;
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB + q.at.n_heads * q.chunks));
     const size_t lds = (size_t)a.cols * sizeof(float);
     if (q.at.kv_bf16)
@@ -316,7 +324,7 @@ void qkv_stream_kernel(TH_QKV_HEAD, StepQkvAttnArgs q, GemvArgs a, long long chu
         attend_stream<G, KV, true>(q.at, b / q.at.nsplit, b % q.at.nsplit, chunk, q.words, epoch, q.err);
         return;
     }
-    qkv_publish<CPL>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, in_a, in_b, gain, layer);
+    qkv_publish<CPL, kQkvRowsPerWave>(q, a, Rows{{w0, w1, w2}, {c0, c1, 0}}, n_rows, cols, in_a, in_b, gain, layer);
 }
 
 template <int CPL, int G>
