@@ -191,13 +191,14 @@ def _head_norm_rope(x, gain, table, pos, n_heads):
 
 
 @pytest.mark.parametrize("shape,pos", [("0.6b", 0), ("0.6b", 47), ("0.6b", 300), ("4b", 5), ("4b", 600),
-                                       ("0.6b", 2100), ("0.6b", 5000), ("4b", 1100), ("4b", 8300)])
+                                       ("0.6b", 1900), ("0.6b", 2100), ("0.6b", 5000), ("4b", 1100), ("4b", 8300)])
 def test_step_qkv_attn(hip, tlib, shape, pos):
     """The fused launch against q/k/v GEMV, per-head norms, RoPE, the cache
     append and the attention over positions 0..pos; 300 and 600 positions
-    span several 64-position chunks, merged by each head's first chunk; past
-    32 chunks a head (0.6B) or 512 attention blocks (4B), the launch holds
-    the streaming split attention instead, merged by the combine."""
+    span several 64-position chunks, merged by each head's first chunk, 1900
+    the chunked launch's reach (31 chunks, 496 attention blocks); past 32
+    chunks a head (0.6B) or 512 attention blocks (4B), the launch holds the
+    streaming split attention instead, merged by the combine."""
     H, nh, nkv, _ = SHAPES[shape]
     hd, qd, kvd = 128, nh * 128, nkv * 128
     max_len = pos + 24

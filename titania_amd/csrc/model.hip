@@ -358,8 +358,16 @@ int enqueue_step(th_state *s) {
                                                  m->dev->num_cus);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
-    // One launch for q/k/v and attention while one split covers the context.
-    const bool fuse_attn = chunks > 0 && th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64;
+    // One launch for q/k/v and the chunked attention while its blocks stay
+    // few: at most 16 chunks a head and fewer than 512 attention blocks.
+    // Past that the streaming launch below is faster (paired runs, ms a step,
+    // chunked -> streaming; Qwen3-0.6B, f32 caches of 1024 positions, 16
+    // chunks: 0.629 -> 0.659; 1280: 0.712 -> 0.665; 1536: 0.717 -> 0.683;
+    // 2048: 0.784 -> 0.708; bf16 caches of 2560: 0.760 -> 0.706; Qwen3-4B,
+    // f32 caches of 768 positions, 384 blocks: 1.904 -> 1.915; 1024, 512
+    // blocks: 1.965 -> 1.939; bf16 caches of 2048: 1.967 -> 1.938).
+    const bool fuse_attn = chunks > 0 && chunks <= 16 && chunks * nh < th::kStepQkvAttnMaxBlocks &&
+                           th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64;
     // Past the chunked launch's reach, the q/k/v GEMV and the streaming
     // attention share a launch when the GEMV blocks are few beside the
     // attention's (Qwen3-0.6B, max_len 4096: 256 GEMV and 1024 attention
