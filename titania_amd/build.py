@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import subprocess
 import sys
 from pathlib import Path
@@ -35,6 +36,10 @@ FLAGS = [
     "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-result",
+    # Per-kernel resource remarks, read by _compile: no kernel here may use
+    # scratch memory (a spill, or a local table the compiler failed to keep in
+    # registers, turns a kernel's loads into slow, serialized ones).
+    "-Rpass-analysis=kernel-resource-usage",
 ]
 
 
@@ -48,7 +53,22 @@ def _compile(src: Path) -> tuple[Path, str]:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stdout}\n{r.stderr}")
-    return obj, r.stderr
+    scratch, kernel, notes, remark = [], None, [], False
+    for line in r.stderr.splitlines():
+        if "[-Rpass-analysis=kernel-resource-usage]" not in line:
+            # A remark's source excerpt and caret follow it.
+            if not (remark and re.match(r"\s*\d*\s*\|", line)):
+                notes.append(line)
+                remark = False
+            continue
+        remark = True
+        if (m := re.search(r"Function Name: (\S+)", line)):
+            kernel = m.group(1)
+        elif (m := re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)) and int(m.group(1)):
+            scratch.append(f"{kernel}: {m.group(1)} bytes a lane")
+    if scratch:
+        raise RuntimeError(f"kernels of {src.name} use scratch memory:\n" + "\n".join(scratch))
+    return obj, "\n".join(notes)
 
 
 SYNTH_SRC = PKG / "synth.c"

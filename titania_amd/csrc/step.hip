@@ -54,6 +54,24 @@ struct GemvArgs {
     const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int c0, \
         int c1, int n_rows, int cols, const float *__restrict__ in_a, const float *__restrict__ in_b
 
+// The q/k/v GEMV and the q/k/v + attention launches lead with the three
+// matrices' bases, the q and k row counts packed (q | k << 16; v has k's),
+// the columns packed with the layer (cols | layer << 16), the input vectors'
+// and the RMSNorm gains' addresses: 14 dwords, all preloaded, so that the
+// GEMV blocks request their input, gains and weight rows without fetching a
+// kernel argument.
+#define TH_QKV_HEAD                                                                                        \
+    const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int rows01, \
+        int cols_layer, const float *__restrict__ in_a, const float *__restrict__ in_b,                         \
+        const uint16_t *__restrict__ gain
+#define TH_QKV_HEAD_OF(q, a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], \
+                             (a).rows.count[0] | (a).rows.count[1] << 16, (a).cols | (q).layer << 16, (a).a, (a).b, \
+                             (a).gain
+// Unpacks TH_QKV_HEAD's counts.
+#define TH_QKV_HEAD_UNPACK                                                                          \
+    const int c0 = rows01 & 0xffff, c1 = rows01 >> 16, n_rows = c0 + 2 * c1, cols = cols_layer & 0xffff, \
+              layer = cols_layer >> 16
+
 // Where kStore writes row r.
 __device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
     if (!a.outs[0]) return a.out + r;
@@ -65,15 +83,19 @@ __device__ __forceinline__ float *store_at(const GemvArgs &a, int r) {
 
 constexpr bool gemv_early_gain(Prologue pro, Epilogue epi) { return pro == kNormSum && epi != kStore; }
 
-// One block: RPW rows per wave, CPL 16-byte chunks per lane per row.
-template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a) {
+// One block: RPW rows per wave, CPL 16-byte chunks per lane per row. With
+// EARLY, the RMSNorm gains (at `gain`) are requested with the input, ahead of
+// the weight rows; otherwise after them, from a.gain.
+// The matrices' table is built here from scalars: a table passed in by
+// reference went to scratch memory, its row selection into a
+// dynamically-indexed load.
+template <int RPW, int CPL, Prologue PRO, Epilogue EPI, bool EARLY>
+__device__ __forceinline__ void gemv_body(const uint16_t *w0, const uint16_t *w1, const uint16_t *w2, int c0, int c1,
+                                          int n_rows, int cols, const float *in_a, const float *in_b,
+                                          const uint16_t *gain, const GemvArgs &a) {
     static_assert(EPI != kSiluPairs || RPW % 2 == 0, "a wave holds whole (gate, up) pairs");
-    // The RMSNorm launches of one or two matrices (gate/up, the output
-    // projection) take the gains' address in the third matrix's slot and
-    // request them with the input, ahead of the weight rows.
-    constexpr bool kEarlyGain = gemv_early_gain(PRO, EPI);
-    const Rows rows{{w0, w1, kEarlyGain ? nullptr : w2}, {c0, c1, 0}};
+    constexpr bool kEarlyGain = EARLY;
+    const Rows rows{{w0, w1, w2}, {c0, c1, 0}};
     extern __shared__ float xs[];
     __shared__ float red[kWaves];
     __shared__ uint64_t red64[kWaves];
@@ -88,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a
     constexpr int NV = (CPL * 128 + kThreads - 1) / kThreads;
     InputRegs<NV> in;
     load_input(in, in_a, in_b, cols);
-    if constexpr (kEarlyGain) load_gain(in, w2, cols);
+    if constexpr (kEarlyGain) load_gain(in, gain, cols);
     uint4 w[RPW][CPL];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
@@ -142,14 +164,49 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a
     }
 }
 
+// The RMSNorm launches of one or two matrices (gate/up, the output
+// projection) take the gains' address in the third matrix's slot and request
+// them early.
+template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a) {
+    constexpr bool kEarlyGain = gemv_early_gain(PRO, EPI);
+    gemv_body<RPW, CPL, PRO, EPI, kEarlyGain>(w0, w1, kEarlyGain ? nullptr : w2, c0, c1, n_rows, cols, in_a, in_b, w2,
+                                              a);
+}
+
+// The q/k/v GEMV (RMSNorm, three matrices) with the head of the q/k/v +
+// attention launches, whose gains' address it requests early.
+template <int RPW, int CPL>
+__global__ __launch_bounds__(kThreads) void gemv_qkv_kernel(TH_QKV_HEAD, GemvArgs a) {
+    TH_QKV_HEAD_UNPACK;
+    (void)layer;
+    gemv_body<RPW, CPL, kNormSum, kStore, true>(w0, w1, w2, c0, c1, n_rows, cols, in_a, in_b, gain, a);
+}
+
+// Whether TH_QKV_HEAD's packed fields hold a q/k/v GEMV's counts (k and v
+// rows equal; rows and columns below 2^16).
+bool qkv_rows_pack(const GemvArgs &a) {
+    return a.rows.count[0] > 0 && a.rows.count[0] < 65536 && a.rows.count[1] > 0 && a.rows.count[1] < 32768 &&
+           a.rows.count[2] == a.rows.count[1] && a.n_rows == a.rows.count[0] + 2 * a.rows.count[1] &&
+           a.cols < 65536;
+}
+
 template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
 hipError_t gemv_launch(hipStream_t s, const GemvArgs &a) {
     constexpr int RPB = RPW * kWaves;
     dim3 grid((unsigned)((a.n_rows + RPB - 1) / RPB));
-    if (gemv_early_gain(PRO, EPI) && a.rows.count[0] + a.rows.count[1] != a.n_rows) return hipErrorInvalidValue;
-    gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, a.cols * sizeof(float), s>>>(
-        a.rows.base[0], a.rows.base[1], gemv_early_gain(PRO, EPI) ? a.gain : a.rows.base[2], a.rows.count[0],
-        a.rows.count[1], a.n_rows, a.cols, a.a, a.b, a);
+    const size_t lds = a.cols * sizeof(float);
+    if constexpr (PRO == kNormSum && EPI == kStore) {
+        if (!qkv_rows_pack(a)) return hipErrorInvalidValue;
+        gemv_qkv_kernel<RPW, CPL><<<grid, kThreads, lds, s>>>(
+            a.rows.base[0], a.rows.base[1], a.rows.base[2], a.rows.count[0] | a.rows.count[1] << 16, a.cols, a.a, a.b,
+            a.gain, a);
+    } else {
+        if (gemv_early_gain(PRO, EPI) && a.rows.count[0] + a.rows.count[1] != a.n_rows) return hipErrorInvalidValue;
+        gemv_kernel<RPW, CPL, PRO, EPI><<<grid, kThreads, lds, s>>>(
+            a.rows.base[0], a.rows.base[1], gemv_early_gain(PRO, EPI) ? a.gain : a.rows.base[2], a.rows.count[0],
+            a.rows.count[1], a.n_rows, a.cols, a.a, a.b, a);
+    }
     return hipGetLastError();
 }
 
@@ -196,23 +253,6 @@ constexpr int qkv_attn_rows_per_wave() {
 
 // The GEMV blocks of the q/k/v + attention launches: the q/k/v rows of
 // launch_step_qkv, published as (value | epoch << 32) words.
-// The q/k/v + attention launches lead with the three matrices' bases, the q
-// and k row counts packed (q | k << 16; v has k's), the columns packed with
-// the layer (cols | layer << 16), the input vectors' and the RMSNorm gains'
-// addresses: 14 dwords, all preloaded, so that the GEMV blocks request their
-// input, gains and weight rows without fetching a kernel argument.
-#define TH_QKV_HEAD                                                                                        \
-    const uint16_t *__restrict__ w0, const uint16_t *__restrict__ w1, const uint16_t *__restrict__ w2, int rows01, \
-        int cols_layer, const float *__restrict__ in_a, const float *__restrict__ in_b,                         \
-        const uint16_t *__restrict__ gain
-#define TH_QKV_HEAD_OF(q, a) (a).rows.base[0], (a).rows.base[1], (a).rows.base[2], \
-                             (a).rows.count[0] | (a).rows.count[1] << 16, (a).cols | (q).layer << 16, (a).a, (a).b, \
-                             (a).gain
-// Unpacks TH_QKV_HEAD's counts.
-#define TH_QKV_HEAD_UNPACK                                                                          \
-    const int c0 = rows01 & 0xffff, c1 = rows01 >> 16, n_rows = c0 + 2 * c1, cols = cols_layer & 0xffff, \
-              layer = cols_layer >> 16
-
 template <int CPL, int RPW>
 __device__ __forceinline__ void qkv_publish(const StepQkvAttnArgs &q, const GemvArgs &a, const Rows &rows, int n_rows,
                                             int cols, const float *in_a, const float *in_b, const uint16_t *gain,
