@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "device_util.h"
 #include "fused.h"
@@ -253,6 +254,17 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+// The fields the streaming attention reads before the position is known,
+// without WORDS: the caches' bases and head stride (max_len * head_dim), the
+// raw q/k/v rows, the q/k RMSNorm gains (or null) and the head counts.
+struct StreamHead {
+    const void *k_cache, *v_cache;
+    const float *qkv;
+    const uint16_t *q_norm, *k_norm;
+    int head_stride;
+    int n_heads, n_kv_heads;
+};
+
 // Attention of one KV head's G q heads over the positions [s0, s0 + chunk)
 // of the context (s0 = split * chunk) by one block, for contexts past the
 // fused launch's reach. The cached rows stream through registers in passes
@@ -273,10 +285,16 @@ __device__ __forceinline__ float row16_sum(float v) {
 // weighted sums in registers; the rows' sums merge once, at the end. The raw
 // q/k/v come from a.qkv, or (WORDS) from the (value | epoch << 32) words of
 // the same launch's GEMV blocks, polled (bounded) after the first pass's
-// rows are requested.
+// rows are requested. Without WORDS, for f32 caches, `e` (preloaded) gives
+// what the first requests need: the raw q/k/v rows, the gains and the first
+// pass's rows go out before the position is read, a device value behind the kernel
+// arguments whose round trip then overlaps their flight. With WORDS the rows
+// wait for the position: requested any earlier they compete with the same
+// launch's GEMV blocks, whose words the attention waits for.
 template <int G, typename KV, bool WORDS>
 __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int split, long long chunk,
-                                              const unsigned long long *words, unsigned epoch, unsigned *err) {
+                                              const unsigned long long *words, unsigned epoch, unsigned *err,
+                                              const StreamHead *e = nullptr) {
     using T = StreamKV<KV>;
     constexpr int HD = 128, HALF = HD / 2, LPR = 16, EPC = T::EPC;
     constexpr int RS = 2;                   // rows a lane takes each pass
@@ -286,15 +304,68 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
     constexpr int DL = NC * EPC;            // dims a lane holds: 8
     constexpr int HPW = (G + 1 + kWaves - 1) / kWaves;  // heads (q..., k) a wave normalizes
     static_assert(DL == 8 && PASS <= kStepKvTailRows, "8 dims a lane; a pass within the caches' tail");
+    // The early requests (below) for f32 caches only: with bf16 caches they
+    // measured slower (Qwen3-4B at 8192 positions 2.084 -> 2.098 ms a step).
+    constexpr bool EARLY = !WORDS && std::is_same<KV, float>::value;
     __shared__ float hq[G * HD], hk[HD], hv[HD];
     // Each DPP row's weighted sums, per wave, head and dim.
     __shared__ float4 red[kWaves][4][G][HD / 4];
     __shared__ float wm[kWaves][G], wl[kWaves][G];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane % LPR, drow = lane / LPR;
-    const int qd = a.n_heads * HD, kvd = a.n_kv_heads * HD;
-    const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
-    const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
+    const int qd = (EARLY ? e->n_heads : a.n_heads) * HD, kvd = (EARLY ? e->n_kv_heads : a.n_kv_heads) * HD;
+    const KV *kc = EARLY ? reinterpret_cast<const KV *>(e->k_cache) + (size_t)g * e->head_stride
+                         : reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
+    const KV *vc = EARLY ? reinterpret_cast<const KV *>(e->v_cache) + (size_t)g * e->head_stride
+                         : reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
+    constexpr int ROWB = HD * (int)sizeof(KV);  // bytes a row
+    uint4 ka[RS][NC], kb[RS][NC], va[RS][NC], vb[RS][NC];
+    // RMSNorm gains of this wave's heads (q heads 0..G-1, then k), and the
+    // raw q/k rows (without WORDS).
+    uint32_t gra[HPW], grb[HPW];
+    float ar[HPW], br[HPW], vraw = 0.f;
+    uint16_t g16a[HPW], g16b[HPW];  // EARLY: the gains as loaded
+    if constexpr (EARLY) {
+        // The gains, the raw rows (from e->qkv), then the first pass's rows,
+        // whatever the position: a split's start lies inside the caches (rows
+        // past them would come from the allocation's tail of kStepKvTailRows
+        // rows, and rows past the context are ignored below).
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh) {
+            const int h = min(wave + hh * kWaves, G);
+            const uint16_t *gain = h < G ? e->q_norm : e->k_norm;
+            const uint16_t *gp = gain ? gain : reinterpret_cast<const uint16_t *>(e->qkv);
+            g16a[hh] = gp[lane];
+            g16b[hh] = gp[lane + HALF];
+            const float *x = h < G ? e->qkv + (size_t)(g * G + h) * HD : e->qkv + qd + (size_t)g * HD;
+            ar[hh] = x[lane];
+            br[hh] = x[lane + HALF];
+        }
+        vraw = e->qkv[qd + kvd + (size_t)g * HD + (tid & (HD - 1))];
+        const int c0 = split * (int)chunk;
+        const bool live = c0 < e->head_stride / HD;
+        const __amdgpu_buffer_rsrc_t sk =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(kc), 0, live ? 0x7fffffff : 0, kBufferRsrcWord3);
+        const __amdgpu_buffer_rsrc_t sv =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(vc), 0, live ? 0x7fffffff : 0, kBufferRsrcWord3);
+        const int o = (wave * RW + drow) * ROWB + sub * 16, base = c0 * ROWB;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < RS; ++r)
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(sk, o + 4 * r * ROWB + i * LPR * 16, base, 0);
+                ka[r][i] = make_uint4(x.x, x.y, x.z, x.w);
+            }
+#pragma unroll
+        for (int r = 0; r < RS; ++r)
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                const th_u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(sv, o + 4 * r * ROWB + i * LPR * 16, base, 0);
+                va[r][i] = make_uint4(x.x, x.y, x.z, x.w);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // Positions fit 32 bits (a cache of head_dim floats a row is far smaller
     // than 2^31 rows): 32-bit scalar arithmetic keeps the loop's bounds in
     // scalar registers.
@@ -303,6 +374,22 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
     const int s0 = split * (int)chunk;
     const int s1 = s0 + (int)chunk < len ? s0 + (int)chunk : len;
     if (s0 >= s1) {
+        if constexpr (EARLY) {
+            // The raw rows and the first pass's rows count as used here too,
+            // as loaded (no arithmetic on them, which the compiler would
+            // hoist above the branch with a wait): otherwise it sinks their
+            // loads into the other path, behind the position's read. The
+            // 16-bit gains are left out: their widening would be hoisted.
+#pragma unroll
+            for (int hh = 0; hh < HPW; ++hh) asm volatile("" ::"v"(ar[hh]), "v"(br[hh]));
+            asm volatile("" ::"v"(vraw));
+#pragma unroll
+            for (int r = 0; r < RS; ++r)
+#pragma unroll
+                for (int i = 0; i < NC; ++i)
+                    asm volatile("" ::"v"(ka[r][i].x), "v"(ka[r][i].y), "v"(ka[r][i].z), "v"(ka[r][i].w),
+                                 "v"(va[r][i].x), "v"(va[r][i].y), "v"(va[r][i].z), "v"(va[r][i].w));
+        }
         // No positions here: empty partials (finite zeros, max -inf) for the combine.
         for (int idx = tid; idx < G * HD; idx += kThreads) {
             const long long slot = (long long)(g * G + idx / HD) * a.nsplit + split;
@@ -314,7 +401,6 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
         }
         return;
     }
-    uint4 ka[RS][NC], kb[RS][NC], va[RS][NC], vb[RS][NC];
     // Buffer loads from the head's base (scalar registers): a lane's offsets
     // within a pass are fixed, the pass's start is a scalar offset, so the
     // loads need no 64-bit address registers.
@@ -322,7 +408,6 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
         __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(kc), 0, 0x7fffffff, kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t rv =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<KV *>(vc), 0, 0x7fffffff, kBufferRsrcWord3);
-    constexpr int ROWB = HD * (int)sizeof(KV);  // bytes a row
     const int ofs = (wave * RW + drow) * ROWB + sub * 16;
     // A request with no pass left goes through descriptors of no records:
     // the same instructions (so that every wait counts the same requests),
@@ -352,30 +437,30 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
     };
     if (WORDS) load(ka, va, s0);  // the words come long after the rows
     const float2 cs = reinterpret_cast<const float2 *>(a.rope + (size_t)pos * HD)[lane];
-    // RMSNorm gains of this wave's heads (q heads 0..G-1, then k), and, from
-    // a.qkv, the raw rows: loaded with no branch and used only after the
-    // rows are requested, so that no wait for them comes first.
-    uint32_t gra[HPW], grb[HPW];
-    float ar[HPW], br[HPW], vraw = 0.f;
+    // Unless EARLY, the gains and, from a.qkv, the raw rows: loaded with no
+    // branch and used only after the rows are requested, so that no wait for
+    // them comes first.
+    if constexpr (!EARLY) {
 #pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-        const int h = min(wave + hh * kWaves, G);
-        const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
-        const uint16_t *gp = gain ? gain : reinterpret_cast<const uint16_t *>(a.rope);
-        gra[hh] = gp[lane];
-        grb[hh] = gp[lane + HALF];
-        ar[hh] = br[hh] = 0.f;
-        if (!WORDS) {
-            const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
-            ar[hh] = x[lane];
-            br[hh] = x[lane + HALF];
+        for (int hh = 0; hh < HPW; ++hh) {
+            const int h = min(wave + hh * kWaves, G);
+            const uint16_t *gain = h < G ? a.q_norm : a.k_norm;
+            const uint16_t *gp = gain ? gain : reinterpret_cast<const uint16_t *>(a.rope);
+            gra[hh] = gp[lane];
+            grb[hh] = gp[lane + HALF];
+            ar[hh] = br[hh] = 0.f;
+            if (!WORDS) {
+                const float *x = h < G ? a.qkv + (size_t)(g * G + h) * HD : a.qkv + qd + (size_t)g * HD;
+                ar[hh] = x[lane];
+                br[hh] = x[lane + HALF];
+            }
         }
-    }
-    if (!WORDS) {
-        vraw = a.qkv[qd + kvd + (size_t)g * HD + (tid & (HD - 1))];
-        __builtin_amdgcn_sched_barrier(0);
-        load(ka, va, s0);
-        __builtin_amdgcn_sched_barrier(0);
+        if (!WORDS) {
+            vraw = a.qkv[qd + kvd + (size_t)g * HD + (tid & (HD - 1))];
+            __builtin_amdgcn_sched_barrier(0);
+            load(ka, va, s0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     float av[HPW], bv[HPW];
 #pragma unroll
@@ -424,8 +509,8 @@ __device__ __forceinline__ void attend_stream(const StepAttnArgs &a, int g, int 
         if (h < G ? a.q_norm != nullptr : a.k_norm != nullptr) {
             const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
             const float sc = 1.0f / sqrtf(ss / (float)HD + a.eps);
-            x0 = x0 * (sc * bf16_to_f32((uint16_t)gra[hh]));
-            x1 = x1 * (sc * bf16_to_f32((uint16_t)grb[hh]));
+            x0 = x0 * (sc * bf16_to_f32(EARLY ? g16a[hh] : (uint16_t)gra[hh]));
+            x1 = x1 * (sc * bf16_to_f32(EARLY ? g16b[hh] : (uint16_t)grb[hh]));
         }
         float *x = h < G ? hq + h * HD : hk;
         x[lane] = x0 * cs.x - x1 * cs.y;
