@@ -88,8 +88,8 @@ def test_qwen06_two_chunk_prefill(hip):
     """Two layers of the Qwen3-0.6B shape, a 2600-token prompt fed in two
     forward calls, the second at positions 2048.. (its attention reads the
     first call's keys and values through the planes), then 8 greedy steps on
-    the split attention path (2608 positions: more than the fused launch's
-    32 chunks a head)."""
+    the split attention path (2608 positions: more than the 16 chunks a head
+    a step gives the fused launch)."""
     check_workload(hip, QWEN3_0_6B.with_layers(2), seed=12, n_prompt=2600, steps=8, what="qwen3-0.6b x2 2600+8",
                    split=2048)
 
