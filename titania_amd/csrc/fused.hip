@@ -83,13 +83,15 @@ __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__
     __shared__ uint64_t red[16];
     __shared__ uint32_t picked;
     uint64_t best = 0;
-    // Eight loads in flight per thread per round.
-    for (size_t i0 = threadIdx.x; i0 < m; i0 += 8 * 1024) {
-        uint64_t v[8];
+    // Sixteen loads in flight per thread per round: the 9496 partials of a
+    // 151936-entry vocabulary in one round trip (with eight a round, two
+    // dependent ones).
+    for (size_t i0 = threadIdx.x; i0 < m; i0 += 16 * 1024) {
+        uint64_t v[16];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = i0 + k * 1024 < m ? partials[i0 + k * 1024] : 0;
+        for (int k = 0; k < 16; ++k) v[k] = i0 + k * 1024 < m ? partials[i0 + k * 1024] : 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) best = max_u64(best, v[k]);
+        for (int k = 0; k < 16; ++k) best = max_u64(best, v[k]);
     }
     best = wave_max_u64(best);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
