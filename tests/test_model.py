@@ -235,10 +235,9 @@ def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
     head (9 positions), several chunks merged by each head's first (300 and
     700 positions: 5 and 12 chunks of 64 f32 or 3 of 128 bf16 positions), and
     past the 16 chunks a head that a step gives the chunked launch, the
-    streaming split attention
-    with its combine (2100 f32 and 4200 bf16 positions: 66 splits of 32 and
-    64 positions on a 256-CU chip, in the q/k/v GEMV's launch since both
-    fit its block slots)."""
+    streaming split attention with its combine (2100 f32 and 4200 bf16
+    positions: 66 splits of 32 and 64 positions on a 256-CU chip, in the
+    q/k/v GEMV's launch since both fit its block slots)."""
     m, r = tiny8
     c = QWEN3_TINY8
     prompt = synth.prompt(prompt_len, c.vocab_size, seed=prompt_len + 1)
@@ -255,6 +254,32 @@ def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
     st.close()
 
 
+
+
+@pytest.mark.parametrize("decode_mode", ["graph", "eager"], indirect=True)
+def test_tiny8_decode_crossing(tiny8, decode_mode):
+    """A state of 1037 positions takes the chunked q/k/v + attention launch
+    while the context is at most 16 chunks of 64 positions and the streaming
+    split attention past that: 24 steps from position 1010 cross over inside
+    one call (graph replays of both sets, or the eager steps one by one),
+    against the oracle, logits at every step."""
+    m, r = tiny8
+    c = QWEN3_TINY8
+    n, steps = 1010, 24
+    prompt = synth.prompt(n, c.vocab_size, seed=n + 1)
+    st = State(m, n + steps + 3, TH_KV_F32)
+    m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
+    toks, logits = m.decode(st, n, steps, keep_logits=True)
+    rtoks, gaps, _ = r.generate(r.state(n + steps + 3), prompt, steps)
+    assert list(toks) == list(rtoks) or np.min(gaps) < 1e-4
+    # The logits after each fed token, against the oracle fed the same tokens.
+    rs = r.state(n + steps + 3)
+    r.forward(rs, prompt, 0)
+    for i in range(steps):
+        exp = r.forward(rs, [int(toks[i])], n + i)
+        assert float(np.std(exp)) > 0.05
+        assert float(np.max(np.abs(logits[i] - exp))) <= 1e-4, f"step {i} (position {n + i})"
+    st.close()
 
 
 def _long_context_check(model, cfg, n_prompt, steps, kv, tol, seed):

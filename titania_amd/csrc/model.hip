@@ -93,6 +93,12 @@ struct th_state {
     hipGraphExec_t graph_exec = nullptr;
     hipGraph_t graph_n = nullptr;  // kGraphSteps decode steps
     hipGraphExec_t graph_n_exec = nullptr;
+    // The same with the streaming attention, for states whose step takes the
+    // chunked launch only while the context is short (step_dual).
+    hipGraph_t graph_l = nullptr;
+    hipGraphExec_t graph_l_exec = nullptr;
+    hipGraph_t graph_ln = nullptr;
+    hipGraphExec_t graph_ln_exec = nullptr;
 
     // The captured decode step's buffers (fixed addresses for the graph).
     bool step_fused = false;
@@ -343,9 +349,43 @@ th::PickEmbed step_embed(th_state *s) {
     return e;
 }
 
+// Whether the chunked q/k/v + attention launch takes a step of this state's
+// fused decode with `ctx` positions in the context (ctx <= max_len). That
+// launch covers the state when its chunks reach max_len (at most 32 a head
+// and 512 attention blocks); it is preferred while the context's chunks stay
+// at most 16 a head and fewer than 512 blocks. Past that the streaming launch
+// is faster (paired runs, ms a step, chunked -> streaming, the context filling
+// the state: Qwen3-0.6B, f32 caches of 1024 positions, 16 chunks: 0.629 ->
+// 0.659; 1280: 0.712 -> 0.665; 1536: 0.717 -> 0.683; 2048: 0.784 -> 0.708;
+// bf16 caches of 2560: 0.760 -> 0.706; Qwen3-4B, f32 caches of 768
+// positions, 384 blocks: 1.904 -> 1.915; 1024, 512 blocks: 1.965 -> 1.939;
+// bf16 caches of 2048: 1.967 -> 1.938), while at a short context in a large
+// state the chunked launch's blocks past the context leave at once
+// (Qwen3-0.6B, 2048 positions, a 16-token context: 0.563 against 0.616 ms).
+// So a state the launch covers takes it up to the preferred reach and the
+// streaming launch past it, in graphs of their own (step_dual).
+bool step_chunked(const th_state *s, long long ctx) {
+    const th_config &c = s->m->c;
+    const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads;
+    const int bf16 = s->kv_dtype == TH_KV_BF16;
+    if (th::step_qkv_attn_chunks(s->max_len, bf16, nh) <= 0 ||
+        !th::step_qkv_attn_supported((int)c.hidden_size, nh, nkv) || s->m->layers.size() >= 64)
+        return false;
+    const int k = th::step_qkv_attn_chunks((size_t)std::max(ctx, 1LL), bf16, nh);
+    return k > 0 && k <= 16 && k * nh < th::kStepQkvAttnMaxBlocks;
+}
+
+// Whether the state keeps two sets of step graphs: the chunked launch's for
+// short contexts and the streaming launch's for long ones.
+bool step_dual(const th_state *s) {
+    return step_chunked(s, 1) && !step_chunked(s, (long long)s->max_len);
+}
+
 // Queues one decode step with the fused step kernels: the token and position
-// come from s->step, the picked token goes back there.
-int enqueue_step(th_state *s) {
+// come from s->step, the picked token goes back there. `chunked`: the q/k/v +
+// attention take the chunked launch, where the state allows it (step_chunked
+// for a short context), or else the streaming one.
+int enqueue_step(th_state *s, bool chunked) {
     th_model *m = s->m;
     hipStream_t st = m->dev->stream;
     const th_config &c = m->c;
@@ -358,16 +398,8 @@ int enqueue_step(th_state *s) {
                                                  m->dev->num_cus);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
         return fail(TH_ERR_INVALID, "attention partials exceed the state's scratch");
-    // One launch for q/k/v and the chunked attention while its blocks stay
-    // few: at most 16 chunks a head and fewer than 512 attention blocks.
-    // Past that the streaming launch below is faster (paired runs, ms a step,
-    // chunked -> streaming; Qwen3-0.6B, f32 caches of 1024 positions, 16
-    // chunks: 0.629 -> 0.659; 1280: 0.712 -> 0.665; 1536: 0.717 -> 0.683;
-    // 2048: 0.784 -> 0.708; bf16 caches of 2560: 0.760 -> 0.706; Qwen3-4B,
-    // f32 caches of 768 positions, 384 blocks: 1.904 -> 1.915; 1024, 512
-    // blocks: 1.965 -> 1.939; bf16 caches of 2048: 1.967 -> 1.938).
-    const bool fuse_attn = chunks > 0 && chunks <= 16 && chunks * nh < th::kStepQkvAttnMaxBlocks &&
-                           th::step_qkv_attn_supported(H, nh, nkv) && m->layers.size() < 64;
+    // One launch for q/k/v and the chunked attention (step_chunked).
+    const bool fuse_attn = chunked && step_chunked(s, 1);
     // Past the chunked launch's reach, the q/k/v GEMV and the streaming
     // attention share a launch when the GEMV blocks are few beside the
     // attention's (Qwen3-0.6B, max_len 4096: 256 GEMV and 1024 attention
@@ -697,8 +729,8 @@ int claim_path(th_state *s, int path) {
 constexpr size_t kGraphSteps = 8;
 
 // Captures `n_steps` decode steps (n = 1 each, position and token from
-// s->step) as one graph.
-int capture_steps(th_state *s, size_t n_steps, hipGraph_t *graph, hipGraphExec_t *exec) {
+// s->step) as one graph; `chunked` as enqueue_step takes it.
+int capture_steps(th_state *s, size_t n_steps, bool chunked, hipGraph_t *graph, hipGraphExec_t *exec) {
     if (*exec) return TH_OK;
     th_model *m = s->m;
     hipStream_t st = m->dev->stream;
@@ -707,7 +739,7 @@ int capture_steps(th_state *s, size_t n_steps, hipGraph_t *graph, hipGraphExec_t
     int rc = TH_OK;
     for (size_t k = 0; k < n_steps && rc == TH_OK; ++k) {
         if (s->step_fused) {
-            rc = enqueue_step(s);
+            rc = enqueue_step(s, chunked);
         } else {
             const long long *pos_dev = &s->step->pos;
             const uint32_t *tok_dev = &s->step->token;
@@ -733,13 +765,23 @@ int capture_steps(th_state *s, size_t n_steps, hipGraph_t *graph, hipGraphExec_t
     return TH_OK;
 }
 
-// Queues `n` decode steps (the graphs captured by capture_or_keep): replays
-// of the multi-step graph, then of the one-step graph for the rest.
-int launch_steps(th_state *s, size_t n) {
+// Whether the decode steps fed at positions [pos, pos + n) take the chunked
+// launch's graphs of a state that keeps both (the context at the last of them
+// is at most pos + n: a step advances the position by one at most).
+bool steps_chunked(const th_state *s, size_t pos, size_t n) { return step_chunked(s, (long long)(pos + n)); }
+
+// Queues `n` decode steps fed from position `pos` on (the graphs captured by
+// capture_or_keep): replays of the multi-step graph, then of the one-step
+// graph for the rest, each from the chunked or the streaming set by the
+// context it can reach.
+int launch_steps(th_state *s, size_t pos, size_t n) {
     hipStream_t st = s->m->dev->stream;
     TH_REQUIRE(s->graph_exec && s->graph_n_exec, "decode steps launched before their capture");
-    for (; n >= kGraphSteps; n -= kGraphSteps) TH_HIP(hipGraphLaunch(s->graph_n_exec, st));
-    for (; n; --n) TH_HIP(hipGraphLaunch(s->graph_exec, st));
+    const bool dual = s->graph_l_exec != nullptr;
+    for (; n >= kGraphSteps; n -= kGraphSteps, pos += kGraphSteps)
+        TH_HIP(hipGraphLaunch(dual && !steps_chunked(s, pos, kGraphSteps) ? s->graph_ln_exec : s->graph_n_exec, st));
+    for (; n; --n, ++pos)
+        TH_HIP(hipGraphLaunch(dual && !steps_chunked(s, pos, 1) ? s->graph_l_exec : s->graph_exec, st));
     return TH_OK;
 }
 
@@ -752,15 +794,29 @@ int capture_or_keep(th_state *s, bool keep, bool sampling) {
         if (s->graph) TH_HIP(hipGraphDestroy(s->graph));
         if (s->graph_n_exec) TH_HIP(hipGraphExecDestroy(s->graph_n_exec));
         if (s->graph_n) TH_HIP(hipGraphDestroy(s->graph_n));
+        if (s->graph_l_exec) TH_HIP(hipGraphExecDestroy(s->graph_l_exec));
+        if (s->graph_l) TH_HIP(hipGraphDestroy(s->graph_l));
+        if (s->graph_ln_exec) TH_HIP(hipGraphExecDestroy(s->graph_ln_exec));
+        if (s->graph_ln) TH_HIP(hipGraphDestroy(s->graph_ln));
         s->graph_exec = nullptr;
         s->graph = nullptr;
         s->graph_n_exec = nullptr;
         s->graph_n = nullptr;
+        s->graph_l_exec = nullptr;
+        s->graph_l = nullptr;
+        s->graph_ln_exec = nullptr;
+        s->graph_ln = nullptr;
     }
     s->graph_keep = keep;
     s->sampling = sampling;
-    TRY(capture_steps(s, 1, &s->graph, &s->graph_exec));
-    return capture_steps(s, kGraphSteps, &s->graph_n, &s->graph_n_exec);
+    // The default set: the chunked launch where the state allows it for a
+    // short context; a state that keeps both also gets the streaming set.
+    const bool chunked = step_chunked(s, 1);
+    TRY(capture_steps(s, 1, chunked, &s->graph, &s->graph_exec));
+    TRY(capture_steps(s, kGraphSteps, chunked, &s->graph_n, &s->graph_n_exec));
+    if (!s->step_fused || !step_dual(s)) return TH_OK;
+    TRY(capture_steps(s, 1, false, &s->graph_l, &s->graph_l_exec));
+    return capture_steps(s, kGraphSteps, false, &s->graph_ln, &s->graph_ln_exec);
 }
 
 }  // namespace
@@ -871,6 +927,10 @@ void th_state_destroy(th_state *s) {
     if (s->graph) (void)hipGraphDestroy(s->graph);
     if (s->graph_n_exec) (void)hipGraphExecDestroy(s->graph_n_exec);
     if (s->graph_n) (void)hipGraphDestroy(s->graph_n);
+    if (s->graph_l_exec) (void)hipGraphExecDestroy(s->graph_l_exec);
+    if (s->graph_l) (void)hipGraphDestroy(s->graph_l);
+    if (s->graph_ln_exec) (void)hipGraphExecDestroy(s->graph_ln_exec);
+    if (s->graph_ln) (void)hipGraphDestroy(s->graph_ln);
     th_buffer *bufs[] = {s->rope, s->logits, s->x, s->xb, s->q, s->k, s->v, s->att, s->gate, s->up};
     for (th_buffer *b : bufs) th_buffer_free(d, b);
     for (th_buffer *b : s->k_cache) th_buffer_free(d, b);
@@ -993,7 +1053,7 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
         TRY(look());
         while (!stopped && launched < steps) {
             const size_t n = std::min(kStopCheckSteps, steps - launched);
-            TRY(launch_steps(s, n));
+            TRY(launch_steps(s, pos + launched, n));
             launched += n;
             TRY(look());
         }
@@ -1003,12 +1063,12 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
         s->graph_keep = out_logits != nullptr;
         s->sampling = sampling;
         TH_HIP(first_pick());
-        for (size_t i = 0; i < steps; ++i) TRY(enqueue_step(s));
+        for (size_t i = 0; i < steps; ++i) TRY(enqueue_step(s, step_chunked(s, (long long)(pos + i + 1))));
         launched = steps;
     } else {
         TRY(capture_or_keep(s, out_logits != nullptr, sampling));
         TH_HIP(first_pick());
-        TRY(launch_steps(s, steps));
+        TRY(launch_steps(s, pos, steps));
         launched = steps;
     }
     s->step_epoch += (uint32_t)launched;
