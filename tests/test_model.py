@@ -257,23 +257,25 @@ def test_tiny8_decode_modes(tiny8, decode_mode, prompt_len, steps, kv):
 
 
 @pytest.mark.parametrize("decode_mode", ["graph", "eager"], indirect=True)
-def test_tiny8_decode_crossing(tiny8, decode_mode):
-    """A state of 1037 positions takes the chunked q/k/v + attention launch
-    while the context is at most 16 chunks of 64 positions and the streaming
-    split attention past that: 24 steps from position 1010 cross over inside
-    one call (graph replays of both sets, or the eager steps one by one),
-    against the oracle, logits at every step."""
+@pytest.mark.parametrize("n,steps,max_len", [(1010, 24, 1037), (200, 16, 5000)])
+def test_tiny8_decode_crossing(tiny8, decode_mode, n, steps, max_len):
+    """A decode step takes the chunked q/k/v + attention launch, of at most 16
+    chunks of 64 positions a head, while they cover the context, and the
+    streaming split attention past that. In a state of 1037 positions, 24
+    steps from position 1010 cross over inside one call (graph replays of both
+    sets, or the eager steps one by one); in a state of 5000 positions (79
+    chunks), a 200-token context takes the chunked launch of 16. Against the
+    oracle, logits at every step."""
     m, r = tiny8
     c = QWEN3_TINY8
-    n, steps = 1010, 24
     prompt = synth.prompt(n, c.vocab_size, seed=n + 1)
-    st = State(m, n + steps + 3, TH_KV_F32)
+    st = State(m, max_len, TH_KV_F32)
     m.forward(st, prompt, 0, TH_PATH_FUSED, want_logits=False)
     toks, logits = m.decode(st, n, steps, keep_logits=True)
-    rtoks, gaps, _ = r.generate(r.state(n + steps + 3), prompt, steps)
+    rtoks, gaps, _ = r.generate(r.state(max_len), prompt, steps)
     assert list(toks) == list(rtoks) or np.min(gaps) < 1e-4
     # The logits after each fed token, against the oracle fed the same tokens.
-    rs = r.state(n + steps + 3)
+    rs = r.state(max_len)
     r.forward(rs, prompt, 0)
     for i in range(steps):
         exp = r.forward(rs, [int(toks[i])], n + i)

@@ -268,6 +268,20 @@ int forward_batch_trait(th_state *s, const uint32_t *tokens, size_t n, size_t po
     return TH_OK;
 }
 
+// Attention blocks per q head of this state's chunked q/k/v + attention
+// launch: the chunks max_len needs, at most 16 and fewer than 512 blocks in
+// all (the reach in which that launch beats the streaming one, below); 0
+// where the launch does not serve the model.
+int step_reach_chunks(const th_state *s) {
+    const th_config &c = s->m->c;
+    const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads;
+    if (!th::step_qkv_attn_supported((int)c.hidden_size, nh, nkv) || s->m->layers.size() >= 64) return 0;
+    const long long rows = th::step_qkv_attn_rows(s->kv_dtype == TH_KV_BF16);
+    int k = (int)std::min<long long>(((long long)s->max_len + rows - 1) / rows, 16);
+    while (k > 0 && k * nh >= th::kStepQkvAttnMaxBlocks) --k;
+    return k;
+}
+
 int ensure_fused_state(th_state *s) {
     if (s->fx) return TH_OK;
     th_model *m = s->m;
@@ -326,8 +340,7 @@ int ensure_fused_state(th_state *s) {
         // Zeroed: epoch 0 precedes every epoch a step uses. Cleared on the
         // device's stream, which is non-blocking: a null-stream hipMemset
         // would not be ordered before the step kernels.
-        const int chunks = std::max(
-            th::step_qkv_attn_chunks(s->max_len, s->kv_dtype == TH_KV_BF16, (int)c.num_attention_heads), 1);
+        const int chunks = std::max(step_reach_chunks(s), 1);
         const size_t words = th::step_qkv_attn_words((int)qd, (int)kvd, (int)c.num_attention_heads, chunks);
         TH_HIP(hipMalloc(&s->s_words, words * sizeof(unsigned long long)));
         TH_HIP(hipMemsetAsync(s->s_words, 0, words * sizeof(unsigned long long), m->dev->stream));
@@ -350,10 +363,10 @@ th::PickEmbed step_embed(th_state *s) {
 }
 
 // Whether the chunked q/k/v + attention launch takes a step of this state's
-// fused decode with `ctx` positions in the context (ctx <= max_len). That
-// launch covers the state when its chunks reach max_len (at most 32 a head
-// and 512 attention blocks); it is preferred while the context's chunks stay
-// at most 16 a head and fewer than 512 blocks. Past that the streaming launch
+// fused decode with `ctx` positions in the context (ctx <= max_len): while
+// its chunks (step_reach_chunks) cover the context. That launch is preferred
+// while the context's chunks stay at most 16 a head and fewer than 512
+// blocks (its blocks past the context leave at once). Past that the streaming launch
 // is faster (paired runs, ms a step, chunked -> streaming, the context filling
 // the state: Qwen3-0.6B, f32 caches of 1024 positions, 16 chunks: 0.629 ->
 // 0.659; 1280: 0.712 -> 0.665; 1536: 0.717 -> 0.683; 2048: 0.784 -> 0.708;
@@ -362,17 +375,11 @@ th::PickEmbed step_embed(th_state *s) {
 // bf16 caches of 2048: 1.967 -> 1.938), while at a short context in a large
 // state the chunked launch's blocks past the context leave at once
 // (Qwen3-0.6B, 2048 positions, a 16-token context: 0.563 against 0.616 ms).
-// So a state the launch covers takes it up to the preferred reach and the
-// streaming launch past it, in graphs of their own (step_dual).
+// So a step takes the chunked launch while its chunks cover the context and
+// the streaming launch past that, each in graphs of their own (step_dual).
 bool step_chunked(const th_state *s, long long ctx) {
-    const th_config &c = s->m->c;
-    const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads;
-    const int bf16 = s->kv_dtype == TH_KV_BF16;
-    if (th::step_qkv_attn_chunks(s->max_len, bf16, nh) <= 0 ||
-        !th::step_qkv_attn_supported((int)c.hidden_size, nh, nkv) || s->m->layers.size() >= 64)
-        return false;
-    const int k = th::step_qkv_attn_chunks((size_t)std::max(ctx, 1LL), bf16, nh);
-    return k > 0 && k <= 16 && k * nh < th::kStepQkvAttnMaxBlocks;
+    const long long rows = th::step_qkv_attn_rows(s->kv_dtype == TH_KV_BF16);
+    return (std::max(ctx, 1LL) + rows - 1) / rows <= step_reach_chunks(s);
 }
 
 // Whether the state keeps two sets of step graphs: the chunked launch's for
@@ -393,7 +400,7 @@ int enqueue_step(th_state *s, bool chunked) {
     const int nh = (int)c.num_attention_heads, nkv = (int)c.num_key_value_heads;
     const int qd = nh * hd, kvd = nkv * hd, V = (int)c.vocab_size;
     const float eps = c.rms_norm_eps;
-    const int chunks = th::step_qkv_attn_chunks(s->max_len, s->kv_dtype == TH_KV_BF16, (int)nh);
+    const int chunks = step_reach_chunks(s);
     const int nsplit = th::step_attention_splits(s->max_len, s->kv_dtype == TH_KV_BF16, nh / nkv, nkv,
                                                  m->dev->num_cus);
     if (th::attention_scratch(1, (size_t)nh, (size_t)hd, nsplit) > s->attn_part_floats)
@@ -1088,6 +1095,8 @@ int decode(th_model *m, th_state *s, size_t pos, size_t steps, uint32_t *out_tok
     if (s->s_err) TH_HIP(hipMemcpyAsync(&poll_failures, s->s_err, sizeof poll_failures, hipMemcpyDeviceToHost, st));
     if (sampling) TH_HIP(hipMemcpyAsync(sp, s->s_sample, sizeof *sp, hipMemcpyDeviceToHost, st));
     TH_HIP(hipStreamSynchronize(st));
+    if (poll_failures >= th::kStepReachError)
+        return fail(TH_ERR_HIP, "decode: a step's context passed its chunked attention launch's chunks");
     if (poll_failures)
         return fail(TH_ERR_HIP, "decode: %u attention blocks gave up waiting for their q/k/v", poll_failures);
     return TH_OK;

@@ -97,18 +97,30 @@ struct StepQkvAttnArgs {
     unsigned *err;                 // counts attention blocks whose poll gave up
     const StepState *st;
     int layer;
-    int chunks;                    // attention blocks per q head (step_qkv_attn_chunks)
+    // attention blocks per q head: at most step_qkv_attn_chunks(max_len) (0
+    // there: at most kStepQkvAttnMaxChunks and kStepQkvAttnMaxBlocks in all),
+    // and they must cover the step's context (chunks x 64 f32 / 128 bf16
+    // positions); a launch of fewer than max_len needs serves short contexts
+    // of a large state
+    int chunks;
 };
 
 // Most attention blocks per q head, and per launch, in launch_step_qkv_attn.
 constexpr int kStepQkvAttnMaxChunks = 32;
 constexpr int kStepQkvAttnMaxBlocks = 512;
+// Added to the error counter (StepQkvAttnArgs::err) by a chunked launch
+// whose chunks do not cover the step's context, beside the count of
+// attention blocks whose poll gave up.
+constexpr unsigned kStepReachError = 1u << 20;
 
 // Attention blocks per q head that launch_step_qkv_attn uses for caches of
 // max_len positions (one per register pass of rows: 64 f32 or 128 bf16
 // positions), or 0 when that is more than kStepQkvAttnMaxChunks or the
 // launch's attention blocks more than kStepQkvAttnMaxBlocks.
 int step_qkv_attn_chunks(size_t max_len, int kv_bf16, int n_heads);
+// Cached positions one attention block of launch_step_qkv_attn takes (64 f32
+// or 128 bf16).
+int step_qkv_attn_rows(int kv_bf16);
 
 // Exchange words launch_step_qkv_attn needs.
 size_t step_qkv_attn_words(int q_rows, int kv_rows, int n_heads, int chunks);

@@ -731,6 +731,10 @@ __device__ __forceinline__ void attend_wave4(const StepAttnArgs &a, int g, int h
     const long long s0 = (long long)split * ROWS;
     const long long pos = *(const __attribute__((address_space(4))) long long *)a.pos;
     const long long len = pos + 1;
+    // The launch's chunks must cover the context (the host picks a launch of
+    // fewer chunks than the caches hold only while they do): past them rows
+    // would go unread, so the head's first chunk flags it.
+    if (split == 0 && threadIdx.x == 0 && len > (long long)n_chunks * ROWS) atomicAdd(err, kStepReachError);
     if (s0 >= len) return;  // a chunk past the context (uniform over the block)
     const KV *kc = reinterpret_cast<const KV *>(a.k_cache) + (size_t)g * a.head_stride;
     const KV *vc = reinterpret_cast<const KV *>(a.v_cache) + (size_t)g * a.head_stride;
