@@ -502,6 +502,64 @@ __global__ __launch_bounds__(256) void attn_combine_wave_kernel(float *__restric
     }
 }
 
+// The same merge for few (token, head) pairs of at most kCombineLaneSplits
+// splits (decode): one wave per (pair, 16 dimensions), with no block barrier
+// among the waves. Lane s holds the statistics of splits s and s + 64; lane
+// 16 q + d accumulates dimension d over the splits q, q + 4, q + 8, ...,
+// whose accumulator rows it requests together with the statistics, so that
+// the merge waits for one memory round trip. The weights pass through LDS in
+// that order (the wave's own writes, then its reads); the four lane rows'
+// sums combine with permlane swaps.
+constexpr int kCombineLaneSplits = 128;
+
+__global__ __launch_bounds__(64) void attn_combine_lanes_kernel(float *__restrict__ out,
+                                                                const float *__restrict__ part_acc,
+                                                                const float *__restrict__ part_ml, int nsplit, int hd,
+                                                                uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
+    constexpr int NG = 4, K = kCombineLaneSplits / NG;  // groups of splits; splits a lane
+    __shared__ float4 wsh[NG][K / 4];
+    const int slices = hd / 16;
+    const long long th = blockIdx.x / slices;
+    const int lane = threadIdx.x, grp = lane >> 4;
+    const int d = (int)(blockIdx.x % slices) * 16 + (lane & 15);
+    const float2 *ml = reinterpret_cast<const float2 *>(part_ml + th * nsplit * 2);
+    const float *pa = part_acc + th * nsplit * hd + d;
+    const float2 st0 = lane < nsplit ? ml[lane] : make_float2(-INFINITY, 0.f);
+    const float2 st1 = lane + 64 < nsplit ? ml[lane + 64] : make_float2(-INFINITY, 0.f);
+    float pacc[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int s = grp + NG * k;
+        pacc[k] = s < nsplit ? pa[(size_t)s * hd] : 0.f;
+    }
+    const float m = wave_max_dpp(fmaxf(st0.x, st1.x));
+    // Splits past nsplit and empty splits (max -inf) weigh 0; their
+    // accumulators are zeros.
+    const float w0 = st0.x != -INFINITY ? expf(st0.x - m) : 0.f;
+    const float w1 = st1.x != -INFINITY ? expf(st1.x - m) : 0.f;
+    const float l = wave_sum_dpp(st0.y * w0 + st1.y * w1);
+    float *wf = reinterpret_cast<float *>(&wsh[0][0]);
+    wf[(lane % NG) * K + lane / NG] = w0;
+    wf[((lane + 64) % NG) * K + (lane + 64) / NG] = w1;
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int k4 = 0; k4 < K / 4; ++k4) {
+        const float4 w = wsh[grp][k4];
+        acc = fmaf(pacc[4 * k4], w.x, acc);
+        acc = fmaf(pacc[4 * k4 + 1], w.y, acc);
+        acc = fmaf(pacc[4 * k4 + 2], w.z, acc);
+        acc = fmaf(pacc[4 * k4 + 3], w.w, acc);
+    }
+    acc = rows_sum(acc);
+    if (grp == 0) {
+        if (hi)
+            split_bf16(acc / l, hi[th * hd + d], lo[th * hd + d]);
+        else
+            out[th * hd + d] = acc / l;
+    }
+}
+
 int attention_splits(size_t n, size_t n_heads, size_t n_kv_heads, size_t max_len, size_t head_dim) {
     // Several tokens on the matrix cores: split the keys until the launch has
     // about 512 blocks (two a CU), keeping at least two 64-key tiles a split,
@@ -550,6 +608,11 @@ hipError_t launch_attn_combine(hipStream_t s, float *out, const float *part_acc,
         case 128: attn_combine_wave_kernel<128><<<grid, 256, 0, s>>>(out, part_acc, part_ml, nsplit, heads, hi, lo); break;
         default: attn_combine_wave_kernel<256><<<grid, 256, 0, s>>>(out, part_acc, part_ml, nsplit, heads, hi, lo); break;
         }
+        return hipGetLastError();
+    }
+    if (nsplit <= kCombineLaneSplits && hd % 16 == 0) {
+        attn_combine_lanes_kernel<<<(unsigned)(heads * (size_t)(hd / 16)), 64, 0, s>>>(out, part_acc, part_ml, nsplit,
+                                                                                        hd, hi, lo);
         return hipGetLastError();
     }
     // Few (token, head) pairs (decode): their dimensions spread over several
