@@ -93,6 +93,31 @@ __device__ __forceinline__ uint32_t step_record(StepState *st, int advance, uint
     return tok;
 }
 
+// step_record from a copy of the state read ahead (`loc`, loaded before the
+// caller's own loads, so that its round trip overlaps theirs instead of
+// following its pick), writing back only the fields that change; the same
+// updates as step_record when nothing else writes the state meanwhile.
+__device__ __forceinline__ uint32_t step_record_from(StepState *st, const StepState &loc, int advance, uint32_t tok) {
+    if (advance) st->epoch = loc.epoch + 1;
+    if (loc.stopped) return loc.token;
+    bool stop = false;
+#pragma unroll
+    for (int i = 0; i < kStepMaxStops; ++i) stop = stop || (i < loc.n_stop && tok == loc.stop[i]);
+    const long long step = loc.step + (advance ? 1 : 0);
+    if (stop) {
+        if (loc.tokens_out) loc.tokens_out[step] = tok;
+        st->stopped = (int)step + 1;
+        return loc.token;
+    }
+    if (advance) {
+        st->pos = loc.pos + 1;
+        st->step = step;
+    }
+    st->token = tok;
+    if (loc.tokens_out) loc.tokens_out[step] = tok;
+    return tok;
+}
+
 // emb.out = the embedding row of `tok` (model/cpu.rs:38-47), by the block.
 __device__ __forceinline__ void write_embedding(const PickEmbed &emb, uint32_t tok) {
     const uint4 *row = reinterpret_cast<const uint4 *>(emb.table + (size_t)tok * emb.dim);

@@ -82,6 +82,9 @@ __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__
                                                    int advance, PickEmbed emb) {
     __shared__ uint64_t red[16];
     __shared__ uint32_t picked;
+    // The state, read before the partials (its wait then ends with theirs).
+    StepState loc{};
+    if (threadIdx.x == 0) loc = *st;
     uint64_t best = 0;
     // Sixteen loads in flight per thread per round: the 9496 partials of a
     // 151936-entry vocabulary in one round trip (with eight a round, two
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(1024) void pick_kernel(const uint64_t *__restrict__
     if (threadIdx.x == 0) {
         uint64_t b = 0;
         for (int w = 0; w < 16; ++w) b = max_u64(b, red[w]);
-        picked = step_record(st, advance, argmax_index(b));
+        picked = step_record_from(st, loc, advance, argmax_index(b));
     }
     if (!emb.table) return;
     __syncthreads();
