@@ -358,6 +358,17 @@ void step_attention_stream_kernel(const void *__restrict__ k_cache, const void *
                                   const float *__restrict__ qkv, const uint16_t *__restrict__ q_norm,
                                   const uint16_t *__restrict__ k_norm, int head_stride, int split_chunk, int heads,
                                   StepAttnArgs a) {
+    // Waves of different blocks at different issue priorities (blocks in
+    // turn), so that the waves a SIMD holds do not all reach their arithmetic
+    // together: the favoured one computes while the others wait for rows.
+    // Qwen3-4B at 8192 positions 2.1900 -> 2.1835 ms a step over six paired
+    // runs (all six faster).
+    switch (blockIdx.x & 3) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+    }
     const StreamHead e{k_cache, v_cache, qkv, q_norm, k_norm, head_stride, heads & 0xffff, heads >> 16};
     const int nsplit = split_chunk & 0x1ff;
     attend_stream<G, KV, false>(a, blockIdx.x / nsplit, blockIdx.x % nsplit, split_chunk >> 9, nullptr, 0, nullptr,
