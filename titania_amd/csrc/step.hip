@@ -358,12 +358,15 @@ void step_attention_stream_kernel(const void *__restrict__ k_cache, const void *
                                   const float *__restrict__ qkv, const uint16_t *__restrict__ q_norm,
                                   const uint16_t *__restrict__ k_norm, int head_stride, int split_chunk, int heads,
                                   StepAttnArgs a) {
-    // Waves of different blocks at different issue priorities (blocks in
-    // turn), so that the waves a SIMD holds do not all reach their arithmetic
-    // together: the favoured one computes while the others wait for rows.
-    // Qwen3-4B at 8192 positions 2.1900 -> 2.1835 ms a step over six paired
-    // runs (all six faster).
-    switch (blockIdx.x & 3) {
+    // The blocks a CU holds at once at different issue priorities, so that
+    // the waves a SIMD holds do not all reach their arithmetic together: the
+    // favoured one computes while the others wait for rows. Blocks go to the
+    // 8 XCDs in turn and to an XCD's 32 CUs in turn, so a CU's blocks are
+    // 256 apart and the priority follows blockIdx.x / 256. Qwen3-4B at 8192
+    // positions, six paired runs each: 2.1900 -> 2.1835 ms a step with the
+    // priority following blockIdx.x % 4 (a CU's blocks then share one), and
+    // 2.1817 -> 2.1787 ms from that to blockIdx.x / 256.
+    switch ((blockIdx.x >> 8) & 3) {
     case 0: __builtin_amdgcn_s_setprio(0); break;
     case 1: __builtin_amdgcn_s_setprio(1); break;
     case 2: __builtin_amdgcn_s_setprio(2); break;
