@@ -170,6 +170,20 @@ __device__ __forceinline__ void gemv_body(const uint16_t *w0, const uint16_t *w1
 template <int RPW, int CPL, Prologue PRO, Epilogue EPI>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(TH_GEMV_HEAD, GemvArgs a) {
     constexpr bool kEarlyGain = gemv_early_gain(PRO, EPI);
+    // The gate/up launch of rows of at most two 512-column spans (one round
+    // of blocks at the Qwen3-0.6B shape) with a CU's blocks at different
+    // issue priorities, as the attention launches: Qwen3-0.6B step 0.5117 ->
+    // 0.5094 ms over four paired runs (all faster). At five spans (Qwen3-4B,
+    // two rounds of blocks) it was slower (2.1844 -> 2.2008 ms at 8192
+    // positions), and so were the other GEMVs.
+    if constexpr (EPI == kSiluPairs && CPL <= 2) {
+        switch ((blockIdx.x >> 8) & 3) {
+        case 0: __builtin_amdgcn_s_setprio(0); break;
+        case 1: __builtin_amdgcn_s_setprio(1); break;
+        case 2: __builtin_amdgcn_s_setprio(2); break;
+        default: __builtin_amdgcn_s_setprio(3); break;
+        }
+    }
     gemv_body<RPW, CPL, PRO, EPI, kEarlyGain>(w0, w1, kEarlyGain ? nullptr : w2, c0, c1, n_rows, cols, in_a, in_b, w2,
                                               a);
 }
